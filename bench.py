@@ -1,0 +1,250 @@
+"""Paged-decode benchmark on one MI355X (gfx950).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+
+A step is one layer's paged-attention decode over the whole batch (split-K
+partials kernel + merge kernel), replayed from a captured hipGraph with the
+block tables, context lengths, workspace and output in static device buffers.
+The default workload is BASELINE.json's headline config C3 (Llama-3-8B
+attention geometry, bf16, batch 64, context log-uniform in [1024, 8192]); C2
+captures all 24 layers in one graph and reports per-layer figures.
+
+Printed: one JSON line with the throughput (algorithmic KV-read GB/s), the
+per-layer latency, the roofline of the dominant kernel (HIP events around the
+partials kernel on the stream it runs on) and the reference's CPU path timed
+on this host's cores (the oracle's restatement of attention.py, bounded
+sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = ("paged-decode µs/layer; KV-read HBM GB/s as % of peak (bs64, ctx<=8k, 1 GPU)")
+HBM_PEAK_GBS = 8000.0
+PROFILES = ROOT / "profiles"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="target CPU time of the cpu_baseline sample")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build is a one-GPU kernel library: bench.py runs on "
+                                   "exactly one GPU (--gpus 1); multi-GPU figures are not "
+                                   "produced", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+
+    from miniserve_amd import _native as nat
+    from miniserve_amd.attention import paged_attention
+    from miniserve_amd.workloads import make_workload
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a ROCm GPU")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = nat.lib()
+
+    t0 = time.time()
+    w = make_workload(args.config, device=dev, values_device=dev, part="decode")
+    print(f"[bench] built {w.name}: B={w.batch} H={w.num_heads} KVH={w.num_kv_heads} "
+          f"D={w.head_dim} layers={w.layers} pool={w.num_blocks} pages, "
+          f"ctx {min(w.lens)}..{max(w.lens)} (sum {sum(w.lens)}) in {time.time() - t0:.1f}s",
+          file=sys.stderr, flush=True)
+
+    B, H, KVH, D, bs = w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    table = w.table.to(device=dev, dtype=torch.int32).contiguous()
+    lens = torch.tensor(w.lens, dtype=torch.int32, device=dev)
+    W = table.shape[1]
+    max_ctx = W * bs  # capture-safe bound: the table capacity
+    q = w.query.to(dev).contiguous()
+    ws_bytes = lib.msattn_workspace_bytes(B, 1, H, KVH, D, max_ctx)
+    part_tokens = lib.msattn_partition_tokens(B, 1, H, KVH, D, max_ctx)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    outs = [torch.empty_like(q) for _ in range(w.layers)]
+    qcode, kvcode = nat.dtype_code(w.dtype), nat.dtype_code(w.dtype)
+
+    def step():
+        for layer in range(w.layers):
+            paged_attention(q, w.k_caches[layer], w.v_caches[layer], table, lens,
+                            max_context=max_ctx, workspace=ws, out=outs[layer])
+
+    # eager warm-up on a side stream, then capture the step into a hipGraph
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    print(f"[bench] graph replay: {ms_per_step * 1e3:.2f} us/step over {args.steps} steps",
+          file=sys.stderr, flush=True)
+
+    # Dominant kernel: the partials kernel, bracketed by HIP events on the stream it
+    # is launched on (torch's current stream), over its own timed loop.
+    stream = nat.stream_handle(dev)
+    kc, vc = w.k_caches[0], w.v_caches[0]
+    n_k = max(10, min(args.steps, 200))
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+            torch.cuda.Event(enable_timing=True)) for _ in range(n_k)]
+    for i in range(n_k + 5):
+        e = evs[i - 5] if i >= 5 else None
+        if e:
+            e[0].record()
+        st = lib.msattn_paged_attention_partials(
+            q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
+            table.data_ptr(), lens.data_ptr(), ws.data_ptr(), ws_bytes, B, 1, H, KVH, D, bs,
+            w.num_blocks, W, max_ctx, 1, 0, w.scale, qcode, kvcode, stream)
+        nat.check("partials", st)
+        if e:
+            e[1].record()
+        st = lib.msattn_merge_partials(ws.data_ptr(), ws_bytes, lens.data_ptr(),
+                                       outs[0].data_ptr(), B, 1, H, KVH, D, max_ctx, qcode, stream)
+        nat.check("merge", st)
+        if e:
+            e[2].record()
+    torch.cuda.synchronize()
+    split_ms = sorted(a.elapsed_time(b) for a, b, _ in evs)
+    merge_ms = sorted(b.elapsed_time(c) for _, b, c in evs)
+    split_avg = sum(split_ms) / len(split_ms)
+    merge_avg = sum(merge_ms) / len(merge_ms)
+
+    per_layer_bytes = w.algorithmic_bytes(unique=True)
+    layer_us = ms_per_step * 1e3 / w.layers
+    value_gbs = per_layer_bytes * w.layers / (ms_per_step * 1e-3) / 1e9
+    achieved = per_layer_bytes / (split_avg * 1e-3) / 1e9
+
+    traffic = None
+    tfile = PROFILES / f"traffic_{w.name}.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+
+    result = {
+        "metric": METRIC,
+        "value": round(value_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_layer": round(layer_us, 2),
+        "frac_of_hbm_peak": round(value_gbs / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float32: "f32"}[w.dtype],
+        "data": "synthetic: seeded N(0,1) q/K/V, seeded scattered block tables (16-token pages)",
+        "config": {
+            "workload": f"{w.name}: paged decode, H{H}/KVH{KVH}/D{D}, batch {B}, "
+                        f"ctx {min(w.lens)}..{max(w.lens)}, {w.layers} layer(s), hipGraph replay",
+            "batch": B, "q_len": 1, "num_heads": H, "num_kv_heads": KVH, "head_dim": D,
+            "block_size": bs, "layers": w.layers, "context_tokens": sum(w.lens),
+            "pool_pages": w.num_blocks, "partition_tokens": part_tokens,
+            "algorithmic_bytes_per_layer": per_layer_bytes,
+        },
+        "roofline": {
+            "kernel": "msattn::split_kernel (partials)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel_avg_us": round(split_avg * 1e3, 2),
+            "kernel_median_us": round(split_ms[len(split_ms) // 2] * 1e3, 2),
+            "merge_avg_us": round(merge_avg * 1e3, 2),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(w, target_s: float):
+    """The reference's CPU path (oracle restatement of attention.py:205-250, torch SDPA)
+    on a bounded sample of the same batch: the first rows whose contexts sum to a share
+    that runs about `target_s` seconds in total. Reported as KV-read GB/s."""
+    import torch
+
+    from oracle import paged_sdpa
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    kc = w.k_caches[0].cpu()
+    vc = w.v_caches[0].cpu()
+    q = w.query.cpu()
+    n_rows = 1
+    probe = None
+    while True:
+        rows = list(range(n_rows))
+        args = (q[rows], kc, vc, w.table[rows], [w.lens[i] for i in rows])
+        t = time.perf_counter()
+        paged_sdpa.paged_attention_sdpa(*args)
+        probe = time.perf_counter() - t
+        if probe * 5 >= target_s or n_rows >= w.batch:
+            break
+        n_rows = min(w.batch, max(n_rows * 2, int(n_rows * target_s / max(5 * probe, 1e-3))))
+    times = []
+    for _ in range(5):
+        t = time.perf_counter()
+        paged_sdpa.paged_attention_sdpa(*args)
+        times.append(time.perf_counter() - t)
+    med = sorted(times)[len(times) // 2]
+    tokens = sum(w.lens[i] for i in rows)
+    kv_bytes = tokens * w.kv_bytes_per_token()
+    full_tokens = sum(w.lens)
+    gbs = kv_bytes / med / 1e9
+    return {
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"rows 0..{n_rows - 1} of {w.name} ({tokens} of {full_tokens} context tokens), "
+                  f"median of 5 runs of the oracle's SDPA restatement in {str(w.dtype)[6:]}",
+        "us_per_layer_extrapolated": round(med * 1e6 * full_tokens / tokens, 1),
+        "torch": torch.__version__,
+    }
+
+
+if __name__ == "__main__":
+    main()

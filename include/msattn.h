@@ -1,0 +1,158 @@
+/*
+ * msattn.h -- C ABI of libmsattn.so, the MI355X (gfx950) paged-attention library.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, a
+ * dtype code and a HIP stream (passed as void*, a hipStream_t). No entry point
+ * allocates device memory except where stated, none throws, and all of them
+ * return an msattn_status code. Work is enqueued on the given stream, so a
+ * caller that is capturing that stream into a hipGraph records it.
+ *
+ * Layouts (all "contiguous" means row-major, innermost dimension last):
+ *   query / out     [batch, q_len, num_heads, head_dim]                 contiguous
+ *   k_cache/v_cache [num_blocks, block_size, num_kv_heads, head_dim]    strided, last dim contiguous
+ *   block_table     int32 [batch, table_width]                          contiguous
+ *   context_lens    int32 [batch]
+ *   kv (write_kv)   [batch, tokens, num_kv_heads, head_dim]             contiguous
+ *
+ * Query heads h = kvh * group + g (group = num_heads / num_kv_heads) all read KV
+ * head kvh. Query token i of row b sits at absolute position
+ * q_pos = context_lens[b] - q_len + i; it attends to key positions k with
+ * k < context_lens[b], k <= q_pos when causal, and k > q_pos - window when
+ * window > 0. A row whose key set is empty produces zeros. Block-table entries
+ * outside [0, num_blocks) are treated as holes: their tokens are neither read
+ * nor written.
+ */
+#ifndef MSATTN_H
+#define MSATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSATTN_ABI_VERSION 1
+
+typedef enum msattn_dtype {
+  MSATTN_F32 = 0,
+  MSATTN_F16 = 1,
+  MSATTN_BF16 = 2,
+  MSATTN_FP8_E4M3 = 3, /* OCP float8 e4m3fn (torch.float8_e4m3fn) */
+} msattn_dtype;
+
+typedef enum msattn_status {
+  MSATTN_OK = 0,
+  MSATTN_ERR_INVALID_ARG = 1,  /* null pointer, bad size, misaligned pointer or stride */
+  MSATTN_ERR_UNSUPPORTED = 2,  /* valid request outside the compiled kernel set */
+  MSATTN_ERR_WORKSPACE = 3,    /* workspace smaller than msattn_workspace_bytes() */
+  MSATTN_ERR_HIP = 4,          /* a HIP launch reported an error */
+} msattn_status;
+
+/* ABI version (MSATTN_ABI_VERSION). No reference counterpart. */
+int msattn_abi_version(void);
+
+/* Static, human-readable text for a status code. No reference counterpart. */
+const char* msattn_status_string(int status);
+
+/*
+ * Context partition (tokens) the library uses for this geometry. The split-K
+ * decomposition cuts every row's context into ceil(context_len / partition)
+ * slices; max_context bounds every context_lens entry.
+ * Replaces the host-side split policy of kernels/paged_attn_triton.py:80-84
+ * (num_splits_for) and :313-314 (splits from lens.max()/lens.min()), which need
+ * a device->host read; this one depends on sizes only, so it is capture-safe.
+ */
+int msattn_partition_tokens(int batch, int q_len, int num_heads, int num_kv_heads,
+                            int head_dim, int max_context);
+
+/*
+ * Bytes of caller-owned device workspace msattn_paged_attention needs.
+ * Replaces the per-call torch.empty partial buffers of
+ * kernels/paged_attn_triton.py:320-323.
+ */
+size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_heads,
+                              int head_dim, int max_context);
+
+/*
+ * Paged attention forward: out = softmax(scale * q k^T + mask) v over the paged
+ * cache, for any q_len (decode q_len == 1, chunked prefill q_len > 1).
+ * Replaces PagedAttention.forward (miniserve/attention.py:205-250: gather
+ * :155-171, mask :135-153, GQA expansion :245-247, SDPA :249) and the split-K
+ * launcher flash_decode (kernels/paged_attn_triton.py:286-344).
+ * cache_*_stride are in elements and shared by k_cache and v_cache.
+ * max_context bounds context_lens (entries above it are clamped to it) and
+ * sizes the launch grid; pass table_width * block_size for a capture-safe call.
+ * window <= 0 means no sliding window. Runs msattn_paged_attention_partials
+ * followed by msattn_merge_partials.
+ */
+int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
+                           int64_t cache_block_stride, int64_t cache_slot_stride,
+                           int64_t cache_head_stride, const int32_t* block_table,
+                           const int32_t* context_lens, void* out, void* workspace,
+                           size_t workspace_bytes, int batch, int q_len, int num_heads,
+                           int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                           int table_width, int max_context, int causal, int window,
+                           float scale, int q_dtype, int kv_dtype, void* stream);
+
+/*
+ * First half of msattn_paged_attention: writes the split-K partials (running
+ * max m, sum l and unnormalised accumulator per context partition) into the
+ * workspace. The workspace layout is: float ml[rows][max_parts][2] followed by
+ * float acc[rows][max_parts][head_dim], rows = batch * q_len * num_heads
+ * ordered like `out`, max_parts = ceil(max_context / partition), m in base-2
+ * units (m = max of scale * log2(e) * q.k). Replaces _split_kernel
+ * (kernels/paged_attn_triton.py:176-248).
+ */
+int msattn_paged_attention_partials(const void* query, const void* k_cache, const void* v_cache,
+                                    int64_t cache_block_stride, int64_t cache_slot_stride,
+                                    int64_t cache_head_stride, const int32_t* block_table,
+                                    const int32_t* context_lens, void* workspace,
+                                    size_t workspace_bytes, int batch, int q_len, int num_heads,
+                                    int num_kv_heads, int head_dim, int block_size,
+                                    int num_blocks, int table_width, int max_context, int causal,
+                                    int window, float scale, int q_dtype, int kv_dtype,
+                                    void* stream);
+
+/*
+ * Second half of msattn_paged_attention: log-sum-exp merge of the partials in
+ * `workspace` into `out` (q_dtype). Replaces _merge_kernel
+ * (kernels/paged_attn_triton.py:250-284).
+ */
+int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
+                          const int32_t* context_lens, void* out, int batch, int q_len,
+                          int num_heads, int num_kv_heads, int head_dim, int max_context,
+                          int q_dtype, void* stream);
+
+/*
+ * Scatter new keys/values into the paged cache: for row b, token t,
+ * pos = starts[b] + t, cache[table[b, pos / block_size], pos % block_size] = kv[b, t]
+ * converted to kv_dtype (round to nearest even). Replaces PagedAttention.write_kv
+ * (miniserve/attention.py:111-133). Tokens whose page is a hole are skipped.
+ */
+int msattn_write_kv(void* k_cache, void* v_cache, int64_t cache_block_stride,
+                    int64_t cache_slot_stride, int64_t cache_head_stride, const void* k,
+                    const void* v, const int32_t* block_table, const int32_t* starts,
+                    int batch, int tokens, int num_kv_heads, int head_dim, int block_size,
+                    int num_blocks, int table_width, int src_dtype, int kv_dtype,
+                    void* stream);
+
+/*
+ * Block-table gather: out[b, p] = cache[table[b, p / block_size], p % block_size]
+ * for p < context_lens[b]; positions p >= context_lens[b] read page 0 (as the
+ * reference does), holes give zero rows. out is [batch, max_context,
+ * num_kv_heads, head_dim] in the cache dtype, bytes copied unchanged.
+ * Replaces PagedAttention._gather (miniserve/attention.py:155-171); used to
+ * prove the kernels' page addressing bit-exact.
+ */
+int msattn_gather_kv(const void* cache, int64_t cache_block_stride, int64_t cache_slot_stride,
+                     int64_t cache_head_stride, const int32_t* block_table,
+                     const int32_t* context_lens, void* out, int batch, int max_context,
+                     int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                     int table_width, int kv_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSATTN_H */

@@ -1,0 +1,355 @@
+"""miniserve_amd.attention -- PagedAttention over hand-written HIP kernels.
+
+Drop-in for ``miniserve.attention`` (miniserve/attention.py:65-250): the same
+constructor, ``allocate_kv_cache``, ``write_kv``, ``build_mask`` and
+``forward`` signature, the same cache layout ``[num_blocks, block_size,
+num_kv_heads, head_dim]``, the same GQA head map (query head h reads KV head
+h // group) and the same mask rules. ``forward`` and ``write_kv`` run on the
+GPU through libmsattn.so (include/msattn.h); there is no CPU or PyTorch
+fallback -- CPU tensors raise.
+
+Differences from the reference, all deliberate:
+  * ``forward`` takes an optional keyword ``scale`` (default 1/sqrt(head_dim),
+    the value the reference's SDPA call uses, attention.py:249).
+  * Rows with no visible key (context length 0) return zeros instead of the
+    NaN an all-False SDPA mask row produces.
+  * Block-table entries outside [0, num_blocks) are holes: never read or
+    written (the reference wraps -1 to the last page, attention.py:131, 171).
+  * The result is a contiguous [batch, q_len, heads, head_dim] tensor (the
+    reference returns a transposed view; its caller reshapes it either way).
+"""
+from __future__ import annotations
+
+import math
+from typing import Sequence
+
+import torch
+
+from . import _native as nat
+
+_BACKENDS = ("sdpa", "triton_flash")
+
+
+def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def apply_rope(q: torch.Tensor, k: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
+               position_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Rotate-half RoPE, signature of miniserve/attention.py:41-62.
+
+    ``q`` [batch, heads, seq, dim], ``k`` [batch, kv_heads, seq, dim] or None,
+    ``cos``/``sin`` [max_pos, dim], ``position_ids`` [seq] or [batch, seq].
+    """
+    cos = cos[position_ids].to(q.dtype)
+    sin = sin[position_ids].to(q.dtype)
+    if cos.ndim == 2:
+        cos, sin = cos.unsqueeze(0), sin.unsqueeze(0)
+    cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+    q_rot = q * cos + _rotate_half(q) * sin
+    k_rot = None if k is None else k * cos + _rotate_half(k) * sin
+    return q_rot, k_rot
+
+
+def _require_gpu(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"msattn needs ROCm GPU tensors: {what} is on {t.device} (there is no CPU path)")
+
+
+def block_table_i32(block_table, device: torch.device) -> torch.Tensor:
+    """Block table as a contiguous int32 [batch, width] tensor on `device`."""
+    table = torch.as_tensor(block_table, device=device)
+    if table.ndim == 1:
+        table = table[None, :]
+    if table.ndim != 2:
+        raise ValueError("block_table must be 1-D or 2-D")
+    if table.dtype != torch.int32:
+        table = table.to(torch.int32)
+    return table.contiguous()
+
+
+def context_lens_i32(context_lens, device: torch.device, batch: int) -> tuple[torch.Tensor, int | None]:
+    """(int32 [batch] device tensor, host-known max or None) for context_lens."""
+    if isinstance(context_lens, torch.Tensor):
+        lens = context_lens.reshape(-1)
+        host_max = int(lens.max()) if (lens.device.type == "cpu" and lens.numel()) else None
+        lens = lens.to(device=device, dtype=torch.int32).contiguous()
+    else:
+        values = [int(x) for x in context_lens]
+        host_max = max(values) if values else 0
+        lens = torch.tensor(values, dtype=torch.int32, device=device)
+    if lens.numel() != batch:
+        raise ValueError(f"context_lens has {lens.numel()} entries for a batch of {batch}")
+    return lens, host_max
+
+
+class PagedAttention:
+    """Paged attention over a block-table-mapped KV cache (HIP kernels)."""
+
+    def __init__(
+        self,
+        num_heads: int,
+        num_kv_heads: int | None = None,
+        head_dim: int | None = None,
+        *,
+        num_blocks: int,
+        block_size: int,
+        dtype: torch.dtype = torch.float16,
+        device: torch.device | str = "cpu",
+        window: int | None = None,
+        kv_dtype: torch.dtype = torch.float16,
+    ) -> None:
+        # Argument contract of miniserve/attention.py:81-92.
+        if num_heads <= 0:
+            raise ValueError("num_heads must be positive")
+        if num_kv_heads is None:
+            num_kv_heads = num_heads
+        if num_kv_heads <= 0 or num_heads % num_kv_heads:
+            raise ValueError("num_heads must be a multiple of num_kv_heads")
+        if head_dim is None or head_dim <= 0 or head_dim % 2:
+            raise ValueError("head_dim must be a positive even integer")
+        if num_blocks <= 0 or block_size <= 0:
+            raise ValueError("num_blocks and block_size must be positive")
+        if window is not None and window <= 0:
+            raise ValueError("window must be positive")
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.window = window
+        self.kv_dtype = kv_dtype
+        self.group = num_heads // num_kv_heads
+
+    def allocate_kv_cache(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """(k_cache, v_cache), each zeros [num_blocks, block_size, kv_heads, head_dim]."""
+        shape = (self.num_blocks, self.block_size, self.num_kv_heads, self.head_dim)
+        k = torch.zeros(shape, dtype=self.kv_dtype, device=self.device)
+        v = torch.zeros(shape, dtype=self.kv_dtype, device=self.device)
+        return k, v
+
+    def write_kv(
+        self,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        block_table: torch.Tensor,
+        start: int | Sequence[int] | torch.Tensor = 0,
+    ) -> None:
+        """Scatter k/v [batch, tokens, kv_heads, head_dim] into the cache.
+
+        Row b's token t lands at position start[b] + t (``start`` is an int,
+        one entry per row, or an int tensor already on the device).
+        """
+        for t, name in ((k_cache, "k_cache"), (v_cache, "v_cache"), (k, "k"), (v, "v")):
+            _require_gpu(t, name)
+        if k.shape != v.shape or k.ndim != 4:
+            raise ValueError("k and v must both be [batch, tokens, kv_heads, head_dim]")
+        if k.dtype != v.dtype:
+            raise ValueError("k and v must share a dtype")
+        if k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype or \
+                k_cache.stride() != v_cache.stride():
+            raise ValueError("k_cache and v_cache must share shape, dtype and strides")
+        B, T, KVH, D = k.shape
+        if k_cache.shape[2] != KVH or k_cache.shape[3] != D:
+            raise ValueError("k/v heads or head_dim do not match the cache")
+        if k_cache.stride(3) != 1:
+            raise ValueError("cache head_dim must be contiguous")
+        dev = k_cache.device
+        table = block_table_i32(block_table, dev)
+        if table.shape[0] < B:
+            raise ValueError("block_table has fewer rows than k")
+        if isinstance(start, torch.Tensor):
+            starts = start.reshape(-1).to(device=dev, dtype=torch.int32)
+        elif isinstance(start, Sequence):
+            starts = torch.tensor([int(s) for s in start], dtype=torch.int32, device=dev)
+        else:
+            starts = torch.full((B,), int(start), dtype=torch.int32, device=dev)
+        if starts.numel() < B:
+            raise ValueError("start needs one entry per batch row")
+        starts = starts.contiguous()
+        kc = k.contiguous()
+        vc = v.contiguous()
+        status = nat.lib().msattn_write_kv(
+            k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+            k_cache.stride(2), kc.data_ptr(), vc.data_ptr(), table.data_ptr(), starts.data_ptr(),
+            B, T, KVH, D, k_cache.shape[1], k_cache.shape[0], table.shape[1],
+            nat.dtype_code(k.dtype), nat.dtype_code(k_cache.dtype), nat.stream_handle(dev))
+        nat.check("msattn_write_kv", status)
+
+    def build_mask(
+        self,
+        context_lens: torch.Tensor | Sequence[int],
+        q_len: int,
+        window: int | None = None,
+        causal: bool = True,
+    ) -> torch.Tensor:
+        """Boolean keep-mask [batch, q_len, max_ctx] (True = attend).
+
+        The rules of miniserve/attention.py:135-153, which the kernels apply as
+        per-key predicates: q_pos = len - q_len + i; keep key if key < len,
+        key <= q_pos when causal, key > q_pos - window when windowed.
+        """
+        lens = torch.as_tensor(context_lens, device=self.device).reshape(-1)
+        max_ctx = int(lens.max()) if lens.numel() else 0
+        key = torch.arange(max_ctx, device=self.device).view(1, 1, -1)
+        q_pos = (lens.view(-1, 1) - q_len + torch.arange(q_len, device=self.device).view(1, -1))
+        keep = key < lens.view(-1, 1, 1)
+        if causal:
+            keep = keep & (key <= q_pos.unsqueeze(-1))
+        if window is not None:
+            keep = keep & (key > (q_pos - window).unsqueeze(-1))
+        return keep.expand(lens.numel(), q_len, max_ctx).contiguous()
+
+    def forward(
+        self,
+        query: torch.Tensor,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor,
+        block_table: torch.Tensor,
+        context_lens: torch.Tensor | Sequence[int],
+        causal: bool = True,
+        window: int | None = None,
+        *,
+        backend: str = "sdpa",
+        cos: torch.Tensor | None = None,
+        sin: torch.Tensor | None = None,
+        position: torch.Tensor | None = None,
+        scale: float | None = None,
+    ) -> torch.Tensor:
+        """Paged attention; ``window`` overrides the constructor value.
+
+        ``backend`` is kept for signature compatibility. Both accepted names run
+        the same HIP kernels; "triton_flash" keeps the reference's decode-only
+        contract (attention.py:187-194) and its optional RoPE on the query
+        (cos/sin/position, kernels/paged_attn_triton.py:135-139).
+        """
+        if backend not in _BACKENDS:
+            raise ValueError(f"unknown attention backend: {backend!r}")
+        if backend == "triton_flash":
+            if not causal:
+                raise ValueError("triton_flash supports causal decode only")
+            if (self.window if window is None else window) is not None:
+                raise ValueError("triton_flash does not support a sliding window")
+            if query.shape[1] != 1:
+                raise ValueError("triton_flash is decode-only (q_len == 1)")
+            if k_cache.dtype == torch.float8_e4m3fn or v_cache.dtype == torch.float8_e4m3fn:
+                raise ValueError("triton_flash does not support an FP8 KV cache")
+            if query.device.type != "cuda":
+                raise RuntimeError("triton_flash requires CUDA tensors (a ROCm GPU device)")
+            if cos is not None and sin is not None and position is not None:
+                query = _rope_query(query, cos, sin, position)
+            return paged_attention(query, k_cache, v_cache, block_table, context_lens,
+                                   causal=True, window=None, scale=scale)
+        window = self.window if window is None else window
+        return paged_attention(query, k_cache, v_cache, block_table, context_lens,
+                               causal=causal, window=window, scale=scale)
+
+    __call__ = forward
+
+
+def _rope_query(query: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                position: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE of a decode query [B, 1, H, D] at per-row positions, in fp32."""
+    B = query.shape[0]
+    pos = torch.as_tensor(position, device=query.device).reshape(-1).to(torch.long)[:B]
+    cs = cos.to(query.device).index_select(0, pos).to(torch.float32)[:, None, None, :]
+    sn = sin.to(query.device).index_select(0, pos).to(torch.float32)[:, None, None, :]
+    qf = query.to(torch.float32)
+    return (qf * cs + _rotate_half(qf) * sn).to(query.dtype)
+
+
+def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    block_table, context_lens, *, causal: bool = True, window: int | None = None,
+                    scale: float | None = None, max_context: int | None = None,
+                    workspace: torch.Tensor | None = None, out: torch.Tensor | None = None
+                    ) -> torch.Tensor:
+    """Functional form of PagedAttention.forward on the HIP kernels.
+
+    ``max_context`` bounds context_lens; when context_lens is a device tensor
+    and it is None, the table capacity (width * block_size) is used so that no
+    device->host read happens (the call is then safe to capture in a graph).
+    ``workspace``/``out`` let a caller pass preallocated buffers.
+    """
+    _require_gpu(query, "query")
+    _require_gpu(k_cache, "k_cache")
+    _require_gpu(v_cache, "v_cache")
+    if query.ndim != 4 or k_cache.ndim != 4:
+        raise ValueError("query must be [batch, q_len, heads, head_dim] and the caches "
+                         "[num_blocks, block_size, kv_heads, head_dim]")
+    if k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype or \
+            k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share shape, dtype and strides")
+    B, q_len, H, D = query.shape
+    nb, bs, KVH, Dk = k_cache.shape
+    if Dk != D:
+        raise ValueError(f"head_dim mismatch: query {D}, cache {Dk}")
+    if H % KVH:
+        raise ValueError("num_heads must be a multiple of num_kv_heads")
+    if k_cache.stride(3) != 1:
+        raise ValueError("cache head_dim must be contiguous")
+    if window is not None and window <= 0:
+        raise ValueError("window must be positive")
+    dev = query.device
+    q = query.contiguous()
+    table = block_table_i32(block_table, dev)
+    if table.shape[0] != B:
+        raise ValueError(f"block_table has {table.shape[0]} rows for a batch of {B}")
+    lens, host_max = context_lens_i32(context_lens, dev, B)
+    W = table.shape[1]
+    cap = W * bs
+    if max_context is None:
+        max_context = cap if host_max is None else host_max
+    if host_max is not None and host_max > cap:
+        raise ValueError(f"context length {host_max} exceeds the block table capacity {cap}")
+    max_context = max(0, min(int(max_context), cap))
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    qcode = nat.dtype_code(query.dtype)
+    kvcode = nat.dtype_code(k_cache.dtype)
+    L = nat.lib()
+    ws_bytes = L.msattn_workspace_bytes(B, q_len, H, KVH, D, max_context)
+    if ws_bytes == 0:
+        raise ValueError("unsupported attention geometry")
+    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    if out is None:
+        out = torch.empty((B, q_len, H, D), dtype=query.dtype, device=dev)
+    status = L.msattn_paged_attention(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+        k_cache.stride(1), k_cache.stride(2), table.data_ptr(), lens.data_ptr(), out.data_ptr(),
+        workspace.data_ptr(), ws_bytes, B, q_len, H, KVH, D, bs, nb, W, max_context,
+        1 if causal else 0, int(window or 0), float(scale), qcode, kvcode,
+        nat.stream_handle(dev))
+    nat.check("msattn_paged_attention", status)
+    return out
+
+
+def gather_kv(cache: torch.Tensor, block_table, context_lens, max_context: int | None = None
+              ) -> torch.Tensor:
+    """[batch, max_ctx, kv_heads, head_dim] rows gathered through the block table.
+
+    The addressing of PagedAttention._gather (miniserve/attention.py:155-171),
+    done by the library's gather kernel: positions at or past a row's context
+    length read page 0; holes give zero rows.
+    """
+    _require_gpu(cache, "cache")
+    dev = cache.device
+    table = block_table_i32(block_table, dev)
+    B = table.shape[0]
+    lens, host_max = context_lens_i32(context_lens, dev, B)
+    if max_context is None:
+        max_context = host_max if host_max is not None else table.shape[1] * cache.shape[1]
+    nb, bs, KVH, D = cache.shape
+    out = torch.empty((B, max_context, KVH, D), dtype=cache.dtype, device=dev)
+    status = nat.lib().msattn_gather_kv(
+        cache.data_ptr(), cache.stride(0), cache.stride(1), cache.stride(2), table.data_ptr(),
+        lens.data_ptr(), out.data_ptr(), B, max_context, KVH, D, bs, nb, table.shape[1],
+        nat.dtype_code(cache.dtype), nat.stream_handle(dev))
+    nat.check("msattn_gather_kv", status)
+    return out

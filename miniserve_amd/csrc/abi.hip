@@ -1,0 +1,301 @@
+// C ABI of libmsattn.so (declared in include/msattn.h): argument checks,
+// partition policy and kernel dispatch. No exception crosses this boundary.
+#include <cmath>
+#include <cstdint>
+
+#include "kernels.h"
+#include "msattn.h"
+
+namespace {
+
+using namespace msattn;
+
+constexpr int kPartitionChoices[] = {512, 256, 128};
+constexpr int64_t kTargetSlots = 1024;  // workgroup slots wanted in a launch
+
+bool dtype_ok(int d) { return d >= MSATTN_F32 && d <= MSATTN_FP8_E4M3; }
+int dtype_bytes(int d) { return d == MSATTN_F32 ? 4 : (d == MSATTN_FP8_E4M3 ? 1 : 2); }
+bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
+
+bool geometry_ok(int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                 int max_context) {
+  if (batch <= 0 || q_len <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return false;
+  if (num_heads % num_kv_heads) return false;
+  if (max_context < 0) return false;
+  if (head_dim % 4) return false;
+  const int64_t rows = static_cast<int64_t>(batch) * q_len * num_heads;
+  return rows < (int64_t(1) << 31);
+}
+
+int rows_per_tile(int rows_per_kvh) { return rows_per_kvh >= 8 ? 8 : next_pow2(rows_per_kvh); }
+
+int choose_partition(int batch, int q_len, int num_heads, int num_kv_heads, int max_context) {
+  const int G = num_heads / num_kv_heads;
+  const int rows = q_len * G;
+  const int RT = rows_per_tile(rows);
+  const int64_t base = static_cast<int64_t>(batch) * num_kv_heads * ceil_div(rows, RT);
+  for (int part : kPartitionChoices) {
+    const int64_t parts = max_context > 0 ? (max_context + part - 1) / part : 1;
+    if (base * parts >= kTargetSlots) return part;
+  }
+  return kPartitionChoices[sizeof(kPartitionChoices) / sizeof(int) - 1];
+}
+
+struct Layout {
+  int part;
+  int max_parts;
+  int64_t rows;
+  size_t ml_bytes;   // rounded up to 256
+  size_t acc_bytes;
+};
+
+Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                        int max_context) {
+  Layout L;
+  L.part = choose_partition(batch, q_len, num_heads, num_kv_heads, max_context);
+  L.max_parts = max_context > 0 ? ceil_div(max_context, L.part) : 1;
+  L.rows = static_cast<int64_t>(batch) * q_len * num_heads;
+  const size_t ml = static_cast<size_t>(L.rows) * L.max_parts * 2 * sizeof(float);
+  L.ml_bytes = (ml + 255) / 256 * 256;
+  L.acc_bytes = static_cast<size_t>(L.rows) * L.max_parts * head_dim * sizeof(float);
+  return L;
+}
+
+int hip_status(hipError_t e) { return e == hipSuccess ? MSATTN_OK : MSATTN_ERR_HIP; }
+
+hipError_t dispatch_split(const SplitParams& p, int q_dtype, int kv_dtype, int D, int RT,
+                          hipStream_t s, bool* sup) {
+  *sup = false;
+  if (q_dtype == MSATTN_F32 && kv_dtype == MSATTN_F32) return launch_split<float, float>(p, D, RT, s, sup);
+  if (q_dtype == MSATTN_F16 && kv_dtype == MSATTN_F16) return launch_split<_Float16, _Float16>(p, D, RT, s, sup);
+  if (q_dtype == MSATTN_BF16 && kv_dtype == MSATTN_BF16) return launch_split<bf16_t, bf16_t>(p, D, RT, s, sup);
+  if (q_dtype == MSATTN_F32 && kv_dtype == MSATTN_FP8_E4M3) return launch_split<float, fp8_t>(p, D, RT, s, sup);
+  if (q_dtype == MSATTN_F16 && kv_dtype == MSATTN_FP8_E4M3) return launch_split<_Float16, fp8_t>(p, D, RT, s, sup);
+  if (q_dtype == MSATTN_BF16 && kv_dtype == MSATTN_FP8_E4M3) return launch_split<bf16_t, fp8_t>(p, D, RT, s, sup);
+  return hipSuccess;
+}
+
+int check_cache_args(const void* k_cache, const void* v_cache, int64_t blk, int64_t slot,
+                     int64_t head, int kv_dtype, int block_size, int num_blocks, int table_width) {
+  if (!k_cache || !v_cache) return MSATTN_ERR_INVALID_ARG;
+  if (block_size <= 0 || num_blocks <= 0 || table_width <= 0) return MSATTN_ERR_INVALID_ARG;
+  if (blk < 0 || slot < 0 || head < 0) return MSATTN_ERR_INVALID_ARG;
+  const int eb = dtype_bytes(kv_dtype);
+  if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return MSATTN_ERR_INVALID_ARG;
+  if ((blk * eb) % 16 || (slot * eb) % 16 || (head * eb) % 16) return MSATTN_ERR_INVALID_ARG;
+  return MSATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int msattn_abi_version(void) { return MSATTN_ABI_VERSION; }
+
+const char* msattn_status_string(int status) {
+  switch (status) {
+    case MSATTN_OK: return "ok";
+    case MSATTN_ERR_INVALID_ARG: return "invalid argument";
+    case MSATTN_ERR_UNSUPPORTED: return "unsupported geometry or dtype";
+    case MSATTN_ERR_WORKSPACE: return "workspace too small";
+    case MSATTN_ERR_HIP: return "HIP error";
+    default: return "unknown status";
+  }
+}
+
+int msattn_partition_tokens(int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                            int max_context) {
+  if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context)) return -1;
+  return choose_partition(batch, q_len, num_heads, num_kv_heads, max_context);
+}
+
+size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                              int max_context) {
+  if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context)) return 0;
+  const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
+  return L.ml_bytes + L.acc_bytes;
+}
+
+int msattn_paged_attention_partials(const void* query, const void* k_cache, const void* v_cache,
+                                    int64_t cache_block_stride, int64_t cache_slot_stride,
+                                    int64_t cache_head_stride, const int32_t* block_table,
+                                    const int32_t* context_lens, void* workspace,
+                                    size_t workspace_bytes, int batch, int q_len, int num_heads,
+                                    int num_kv_heads, int head_dim, int block_size,
+                                    int num_blocks, int table_width, int max_context, int causal,
+                                    int window, float scale, int q_dtype, int kv_dtype,
+                                    void* stream) {
+  if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
+  if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
+    return MSATTN_ERR_INVALID_ARG;
+  if (!dtype_ok(q_dtype) || q_dtype == MSATTN_FP8_E4M3 || !dtype_ok(kv_dtype))
+    return MSATTN_ERR_INVALID_ARG;
+  if (!std::isfinite(scale)) return MSATTN_ERR_INVALID_ARG;
+  const int rc = check_cache_args(k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                                  cache_head_stride, kv_dtype, block_size, num_blocks, table_width);
+  if (rc != MSATTN_OK) return rc;
+  if (!aligned(query, dtype_bytes(q_dtype)) || !aligned(workspace, 16)) return MSATTN_ERR_INVALID_ARG;
+  const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
+  if (workspace_bytes < L.ml_bytes + L.acc_bytes) return MSATTN_ERR_WORKSPACE;
+
+  const int G = num_heads / num_kv_heads;
+  const int rows = q_len * G;
+  const int RT = rows_per_tile(rows);
+  SplitParams p;
+  p.q = query;
+  p.k = k_cache;
+  p.v = v_cache;
+  p.table = block_table;
+  p.lens = context_lens;
+  p.ml = static_cast<float*>(workspace);
+  p.acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.ml_bytes);
+  p.blk_stride = cache_block_stride;
+  p.slot_stride = cache_slot_stride;
+  p.head_stride = cache_head_stride;
+  p.batch = batch;
+  p.q_len = q_len;
+  p.H = num_heads;
+  p.KVH = num_kv_heads;
+  p.G = G;
+  p.bs = block_size;
+  p.num_blocks = num_blocks;
+  p.W = table_width;
+  p.max_ctx = max_context;
+  p.max_parts = L.max_parts;
+  p.part = L.part;
+  p.causal = causal ? 1 : 0;
+  p.window = window > 0 ? window : 0;
+  p.scale_log2 = scale * kLog2e;
+  p.rows_per_kvh = rows;
+  p.rtiles = ceil_div(rows, RT);
+  const int64_t gx = static_cast<int64_t>(p.max_parts) * num_kv_heads * p.rtiles;
+  if (gx >= (int64_t(1) << 31) || batch > 65535) return MSATTN_ERR_UNSUPPORTED;
+
+  bool sup = false;
+  const hipError_t e = dispatch_split(p, q_dtype, kv_dtype, head_dim, RT,
+                                      static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return MSATTN_ERR_UNSUPPORTED;
+  return hip_status(e);
+}
+
+int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
+                          const int32_t* context_lens, void* out, int batch, int q_len,
+                          int num_heads, int num_kv_heads, int head_dim, int max_context,
+                          int q_dtype, void* stream) {
+  if (!workspace || !context_lens || !out) return MSATTN_ERR_INVALID_ARG;
+  if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
+    return MSATTN_ERR_INVALID_ARG;
+  if (!dtype_ok(q_dtype) || q_dtype == MSATTN_FP8_E4M3) return MSATTN_ERR_INVALID_ARG;
+  if (head_dim > 1024) return MSATTN_ERR_UNSUPPORTED;
+  if (!aligned(out, dtype_bytes(q_dtype)) || !aligned(workspace, 16)) return MSATTN_ERR_INVALID_ARG;
+  const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
+  if (workspace_bytes < L.ml_bytes + L.acc_bytes) return MSATTN_ERR_WORKSPACE;
+  MergeParams p;
+  p.ml = static_cast<const float*>(workspace);
+  p.acc = reinterpret_cast<const float*>(static_cast<const char*>(workspace) + L.ml_bytes);
+  p.lens = context_lens;
+  p.out = out;
+  p.rows = L.rows;
+  p.rows_per_b = q_len * num_heads;
+  p.D = head_dim;
+  p.max_parts = L.max_parts;
+  p.part = L.part;
+  p.max_ctx = max_context;
+  bool sup = false;
+  const hipError_t e = launch_merge(p, q_dtype, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return MSATTN_ERR_UNSUPPORTED;
+  return hip_status(e);
+}
+
+int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
+                           int64_t cache_block_stride, int64_t cache_slot_stride,
+                           int64_t cache_head_stride, const int32_t* block_table,
+                           const int32_t* context_lens, void* out, void* workspace,
+                           size_t workspace_bytes, int batch, int q_len, int num_heads,
+                           int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                           int table_width, int max_context, int causal, int window,
+                           float scale, int q_dtype, int kv_dtype, void* stream) {
+  if (!out) return MSATTN_ERR_INVALID_ARG;
+  if (!aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
+  const int rc = msattn_paged_attention_partials(
+      query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
+      block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
+      num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
+      scale, q_dtype, kv_dtype, stream);
+  if (rc != MSATTN_OK) return rc;
+  return msattn_merge_partials(workspace, workspace_bytes, context_lens, out, batch, q_len,
+                               num_heads, num_kv_heads, head_dim, max_context, q_dtype, stream);
+}
+
+int msattn_write_kv(void* k_cache, void* v_cache, int64_t cache_block_stride,
+                    int64_t cache_slot_stride, int64_t cache_head_stride, const void* k,
+                    const void* v, const int32_t* block_table, const int32_t* starts, int batch,
+                    int tokens, int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                    int table_width, int src_dtype, int kv_dtype, void* stream) {
+  if (!k_cache || !v_cache || !k || !v || !block_table || !starts) return MSATTN_ERR_INVALID_ARG;
+  if (batch <= 0 || tokens < 0 || num_kv_heads <= 0 || head_dim <= 0) return MSATTN_ERR_INVALID_ARG;
+  if (block_size <= 0 || num_blocks <= 0 || table_width <= 0) return MSATTN_ERR_INVALID_ARG;
+  if (cache_block_stride < 0 || cache_slot_stride < 0 || cache_head_stride < 0)
+    return MSATTN_ERR_INVALID_ARG;
+  if (!dtype_ok(src_dtype) || !dtype_ok(kv_dtype)) return MSATTN_ERR_INVALID_ARG;
+  if (src_dtype == MSATTN_FP8_E4M3 && kv_dtype != MSATTN_FP8_E4M3) return MSATTN_ERR_UNSUPPORTED;
+  if (!aligned(k_cache, dtype_bytes(kv_dtype)) || !aligned(v_cache, dtype_bytes(kv_dtype)) ||
+      !aligned(k, dtype_bytes(src_dtype)) || !aligned(v, dtype_bytes(src_dtype)))
+    return MSATTN_ERR_INVALID_ARG;
+  if (tokens == 0) return MSATTN_OK;
+  WriteKVParams p;
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.k = k;
+  p.v = v;
+  p.table = block_table;
+  p.starts = starts;
+  p.blk_stride = cache_block_stride;
+  p.slot_stride = cache_slot_stride;
+  p.head_stride = cache_head_stride;
+  p.batch = batch;
+  p.tokens = tokens;
+  p.KVH = num_kv_heads;
+  p.D = head_dim;
+  p.bs = block_size;
+  p.num_blocks = num_blocks;
+  p.W = table_width;
+  bool sup = false;
+  const hipError_t e = launch_write_kv(p, src_dtype, kv_dtype, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return MSATTN_ERR_UNSUPPORTED;
+  return hip_status(e);
+}
+
+int msattn_gather_kv(const void* cache, int64_t cache_block_stride, int64_t cache_slot_stride,
+                     int64_t cache_head_stride, const int32_t* block_table,
+                     const int32_t* context_lens, void* out, int batch, int max_context,
+                     int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                     int table_width, int kv_dtype, void* stream) {
+  if (!cache || !block_table || !context_lens || !out) return MSATTN_ERR_INVALID_ARG;
+  if (batch <= 0 || max_context < 0 || num_kv_heads <= 0 || head_dim <= 0) return MSATTN_ERR_INVALID_ARG;
+  if (block_size <= 0 || num_blocks <= 0 || table_width <= 0) return MSATTN_ERR_INVALID_ARG;
+  if (cache_block_stride < 0 || cache_slot_stride < 0 || cache_head_stride < 0)
+    return MSATTN_ERR_INVALID_ARG;
+  if (!dtype_ok(kv_dtype)) return MSATTN_ERR_INVALID_ARG;
+  const int eb = dtype_bytes(kv_dtype);
+  if (!aligned(cache, eb) || !aligned(out, eb)) return MSATTN_ERR_INVALID_ARG;
+  if (max_context == 0) return MSATTN_OK;
+  GatherParams p;
+  p.cache = cache;
+  p.table = block_table;
+  p.lens = context_lens;
+  p.out = out;
+  p.blk_stride = cache_block_stride;
+  p.slot_stride = cache_slot_stride;
+  p.head_stride = cache_head_stride;
+  p.batch = batch;
+  p.max_ctx = max_context;
+  p.KVH = num_kv_heads;
+  p.D = head_dim;
+  p.bs = block_size;
+  p.num_blocks = num_blocks;
+  p.W = table_width;
+  return hip_status(launch_gather(p, eb, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

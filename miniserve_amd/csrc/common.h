@@ -1,0 +1,165 @@
+// Shared device helpers for the msattn HIP kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace msattn {
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------------------
+// Element types. Storage types only; all arithmetic is fp32.
+//   float      fp32
+//   _Float16   fp16 (IEEE binary16)
+//   bf16_t     bfloat16 bits
+//   fp8_t      OCP float8 e4m3fn bits (no infinities, 0x7f/0xff are NaN)
+// ---------------------------------------------------------------------------
+struct bf16_t { uint16_t bits; };
+struct fp8_t { uint8_t bits; };
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h16) {
+  return __uint_as_float(h16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits, NaN -> 0x7fc0 (torch's rule).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Exact decode of one e4m3fn byte.
+__device__ __forceinline__ float fp8e4m3_to_f32(uint32_t x) {
+  const uint32_t sign = (x & 0x80u) << 24;
+  const uint32_t e = (x >> 3) & 0xfu;
+  const uint32_t m = x & 0x7u;
+  if (e == 0) {
+    const float v = static_cast<float>(m) * 0x1p-9f;  // subnormal: m * 2^-9
+    return __uint_as_float(__float_as_uint(v) | sign);
+  }
+  if (e == 15 && m == 7) return __uint_as_float(sign | 0x7fc00000u);
+  return __uint_as_float(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+// fp32 -> e4m3fn, round to nearest even; |x| >= 480 and NaN give NaN (0x7f|sign),
+// which is the rule torch.Tensor.to(torch.float8_e4m3fn) applies.
+__device__ __forceinline__ uint8_t f32_to_fp8e4m3(float f) {
+  uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  u &= 0x7fffffffu;
+  if (u >= 0x43f00000u) return static_cast<uint8_t>(sign | 0x7fu);  // >= 480 or NaN
+  if (u < 0x3c800000u) {
+    // below 2^-6: subnormal range, quantum 2^-9. Exact RNE through the fp32 adder:
+    // adding 2^-9 * 2^23 * 2^... is avoided; scale by 2^9 and round to integer.
+    const float a = __uint_as_float(u) * 512.0f;  // exact (power of two scale)
+    const float r = __builtin_rintf(a);           // RNE to integer 0..8
+    return static_cast<uint8_t>(sign | static_cast<uint32_t>(r));
+  }
+  // normal: keep 3 mantissa bits with RNE, rebias exponent 127 -> 7.
+  const uint32_t mant_odd = (u >> 20) & 1u;
+  u += 0x7ffffu + mant_odd;
+  const uint32_t e = (u >> 23) - 120u;
+  const uint32_t m = (u >> 20) & 0x7u;
+  return static_cast<uint8_t>(sign | (e << 3) | m);
+}
+
+template <typename T> struct Elt;
+template <> struct Elt<float> {
+  static constexpr int kBytes = 4;
+  static constexpr int kCode = 0;
+  __device__ static float load(const float* p) { return *p; }
+  __device__ static void store(float* p, float v) { *p = v; }
+};
+template <> struct Elt<_Float16> {
+  static constexpr int kBytes = 2;
+  static constexpr int kCode = 1;
+  __device__ static float load(const _Float16* p) { return static_cast<float>(*p); }
+  __device__ static void store(_Float16* p, float v) { *p = static_cast<_Float16>(v); }
+};
+template <> struct Elt<bf16_t> {
+  static constexpr int kBytes = 2;
+  static constexpr int kCode = 2;
+  __device__ static float load(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
+  __device__ static void store(bf16_t* p, float v) { p->bits = f32_to_bf16_bits(v); }
+};
+template <> struct Elt<fp8_t> {
+  static constexpr int kBytes = 1;
+  static constexpr int kCode = 3;
+  __device__ static float load(const fp8_t* p) { return fp8e4m3_to_f32(p->bits); }
+  __device__ static void store(fp8_t* p, float v) { p->bits = f32_to_fp8e4m3(v); }
+};
+
+// Unpack one 16-byte chunk (four dwords) of KV elements into fp32.
+template <typename T> struct Chunk;
+template <> struct Chunk<float> {
+  static constexpr int kElems = 4;
+  __device__ static void unpack(const uint4& c, float* o) {
+    o[0] = __uint_as_float(c.x); o[1] = __uint_as_float(c.y);
+    o[2] = __uint_as_float(c.z); o[3] = __uint_as_float(c.w);
+  }
+};
+template <> struct Chunk<bf16_t> {
+  static constexpr int kElems = 8;
+  __device__ static void unpack(const uint4& c, float* o) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+template <> struct Chunk<_Float16> {
+  static constexpr int kElems = 8;
+  __device__ static void unpack(const uint4& c, float* o) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = static_cast<uint16_t>(w[i] & 0xffffu);
+      const uint16_t hi = static_cast<uint16_t>(w[i] >> 16);
+      o[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
+      o[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
+    }
+  }
+};
+template <> struct Chunk<fp8_t> {
+  static constexpr int kElems = 16;
+  __device__ static void unpack(const uint4& c, float* o) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[4 * i + j] = fp8e4m3_to_f32((w[i] >> (8 * j)) & 0xffu);
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Cross-lane reductions over aligned groups of `Width` lanes (power of two).
+// ---------------------------------------------------------------------------
+template <int Width>
+__device__ __forceinline__ float group_sum(float x) {
+#pragma unroll
+  for (int o = Width / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, kWave);
+  return x;
+}
+
+template <int Width>
+__device__ __forceinline__ float group_max(float x) {
+#pragma unroll
+  for (int o = Width / 2; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));
+  return x;
+}
+
+__host__ __device__ constexpr int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+__host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace msattn

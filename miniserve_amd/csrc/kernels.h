@@ -1,0 +1,46 @@
+// Host-side launch interface shared by the msattn translation units.
+#pragma once
+
+#include "common.h"
+#include "split_kernel.h"
+
+namespace msattn {
+
+struct MergeParams {
+  const float* ml;
+  const float* acc;
+  const int32_t* lens;
+  void* out;
+  int64_t rows;   // batch * q_len * H
+  int rows_per_b; // q_len * H
+  int D, max_parts, part, max_ctx;
+};
+
+hipError_t launch_merge(const MergeParams& p, int q_dtype, hipStream_t stream, bool* supported);
+
+struct WriteKVParams {
+  void* k_cache;
+  void* v_cache;
+  const void* k;
+  const void* v;
+  const int32_t* table;
+  const int32_t* starts;
+  int64_t blk_stride, slot_stride, head_stride;
+  int batch, tokens, KVH, D, bs, num_blocks, W;
+};
+
+hipError_t launch_write_kv(const WriteKVParams& p, int src_dtype, int dst_dtype,
+                           hipStream_t stream, bool* supported);
+
+struct GatherParams {
+  const void* cache;
+  const int32_t* table;
+  const int32_t* lens;
+  void* out;
+  int64_t blk_stride, slot_stride, head_stride;
+  int batch, max_ctx, KVH, D, bs, num_blocks, W;
+};
+
+hipError_t launch_gather(const GatherParams& p, int elt_bytes, hipStream_t stream);
+
+}  // namespace msattn

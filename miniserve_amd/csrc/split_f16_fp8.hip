@@ -1,0 +1,37 @@
+// Split-K partial kernels instantiated for query _Float16, KV cache fp8_t.
+// Head dims compiled: 16, 32, 64, 96, 128, 256; rows per tile 1, 2, 4, 8.
+#include "split_kernel.h"
+
+namespace msattn {
+
+template <>
+hipError_t launch_split<_Float16, fp8_t>(const SplitParams& p, int D, int RT, hipStream_t stream,
+                                    bool* supported) {
+  *supported = true;
+  switch (D) {
+    case 16:
+      MSATTN_SPLIT_RT(_Float16, fp8_t, 16)
+      break;
+    case 32:
+      MSATTN_SPLIT_RT(_Float16, fp8_t, 32)
+      break;
+    case 64:
+      MSATTN_SPLIT_RT(_Float16, fp8_t, 64)
+      break;
+    case 96:
+      MSATTN_SPLIT_RT(_Float16, fp8_t, 96)
+      break;
+    case 128:
+      MSATTN_SPLIT_RT(_Float16, fp8_t, 128)
+      break;
+    case 256:
+      MSATTN_SPLIT_RT(_Float16, fp8_t, 256)
+      break;
+    default:
+      break;
+  }
+  *supported = false;
+  return hipSuccess;
+}
+
+}  // namespace msattn

@@ -1,0 +1,349 @@
+// Split-K paged attention partials for gfx950 (templates; instantiated per dtype
+// pair in split_*.hip).
+//
+// One workgroup (4 waves) owns one (sequence b, KV head, row tile, context
+// partition). A row tile packs up to RT query rows that read the same KV head:
+// the `group` GQA heads of that KV head, times the q_len query tokens. The
+// workgroup walks the partition's tokens through the block table and writes a
+// partial (m, l, acc) per row:
+//   m   = max_k  s_k              with s_k = scale * log2(e) * q . K[k]
+//   l   = sum_k  2^(s_k - m)
+//   acc = sum_k  2^(s_k - m) V[k]
+// over the row's unmasked keys in the partition. merge.hip combines them.
+//
+// Phases (barriers between them):
+//   0  page-table walk: one byte offset per token of the partition into LDS
+//      (holes and positions outside every row's key range get -1);
+//   1  scores: each wave streams K rows with 16-byte loads, LPR lanes per row,
+//      so one wave load instruction covers TPI = 64 / LPR tokens; per-lane dot
+//      products are summed across the LPR lanes;
+//   2  softmax statistics per row over the partition (wave reductions);
+//   3  P.V: the same token walk over V, fp32 accumulators per lane, reduced
+//      across lanes and waves through LDS.
+//
+// The algorithm is the split decomposition of kernels/paged_attn_triton.py
+// (_split_kernel :176-248, reference restatement :102-171); the masking rules
+// are PagedAttention.build_mask (miniserve/attention.py:135-153).
+#pragma once
+
+#include <climits>
+
+#include "common.h"
+
+namespace msattn {
+
+constexpr int kSplitThreads = 256;
+constexpr int kSplitWaves = kSplitThreads / kWave;
+constexpr int kPartMax = 512;
+
+struct SplitParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* table;
+  const int32_t* lens;
+  float* ml;   // [rows][max_parts][2]
+  float* acc;  // [rows][max_parts][D]
+  int64_t blk_stride, slot_stride, head_stride;  // elements
+  int batch, q_len, H, KVH, G;
+  int bs, num_blocks, W;
+  int max_ctx, max_parts, part;
+  int causal, window;
+  float scale_log2;
+  int rows_per_kvh;  // q_len * G
+  int rtiles;        // ceil(rows_per_kvh / RT)
+};
+
+template <typename QT, typename KT, int D, int RT>
+__global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams p) {
+  using CK = Chunk<KT>;
+  constexpr int EPL = CK::kElems;                      // KV elements per 16 B
+  static_assert((D * Elt<KT>::kBytes) % 16 == 0, "row must be whole 16-byte chunks");
+  constexpr int CHUNKS = D * Elt<KT>::kBytes / 16;     // 16-byte chunks per row
+  constexpr int LPR = next_pow2(CHUNKS);               // lanes per K/V row
+  static_assert(LPR <= kWave, "row wider than a wave");
+  constexpr int TPI = kWave / LPR;                     // tokens per wave instruction
+  constexpr int U = TPI >= 8 ? 2 : 4;                  // load instructions in flight
+  constexpr int SC_SCORES = kPartMax * RT;
+  constexpr int SC_REDUCE = kSplitWaves * RT * D;
+  constexpr int SC = SC_SCORES > SC_REDUCE ? SC_SCORES : SC_REDUCE;
+
+  __shared__ int64_t s_off[kPartMax];
+  __shared__ float s_sc[SC];
+  __shared__ float s_m[RT];
+  __shared__ float s_l[RT];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int w = tid / kWave;
+
+  // blockIdx.x = part + max_parts * (kvh + KVH * rtile); blockIdx.z = b.
+  const int part = static_cast<int>(blockIdx.x % static_cast<unsigned>(p.max_parts));
+  const int rest = static_cast<int>(blockIdx.x / static_cast<unsigned>(p.max_parts));
+  const int kvh = rest % p.KVH;
+  const int rtile = rest / p.KVH;
+  const int b = blockIdx.z;
+
+  int ctx = p.lens[b];
+  ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
+  const int nparts = ctx > 0 ? ceil_div(ctx, p.part) : 1;
+  if (part >= nparts) return;
+
+  const int row0 = rtile * RT;
+  const int nrows = min(RT, p.rows_per_kvh - row0);
+
+  // Per-row key ranges [lo, hi) (attention.py:143-153 with q_pos = ctx - q_len + i).
+  int lo_r[RT], hi_r[RT];
+  int lo_all = INT_MAX, hi_all = INT_MIN;
+  int64_t orow[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    lo_r[r] = 0;
+    hi_r[r] = 0;
+    orow[r] = 0;
+    if (r < nrows) {
+      const int gr = row0 + r;
+      const int i = gr / p.G;
+      const int g = gr - i * p.G;
+      const int qpos = ctx - p.q_len + i;
+      int hi = p.causal ? min(ctx, qpos + 1) : ctx;
+      int lo = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
+      if (hi < lo) hi = lo;
+      lo_r[r] = lo;
+      hi_r[r] = hi;
+      if (hi > lo) {
+        lo_all = min(lo_all, lo);
+        hi_all = max(hi_all, hi);
+      }
+      orow[r] = (static_cast<int64_t>(b) * p.q_len + i) * p.H + (kvh * p.G + g);
+    }
+  }
+
+  const int tok0 = part * p.part;
+  const int tok1 = min(tok0 + p.part, ctx);
+  const int a0 = max(tok0, lo_all);
+  const int a1 = min(tok1, hi_all);
+  if (a1 <= a0) {  // nothing to attend to in this partition: m = -inf, l = 0
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      if (r < nrows && tid == r) {
+        float* ml = p.ml + (orow[r] * p.max_parts + part) * 2;
+        ml[0] = -INFINITY;
+        ml[1] = 0.0f;
+      }
+    }
+    return;
+  }
+  const int n_tok = tok1 - tok0;
+
+  // Phase 0: page-table walk (attention.py:163-171; paged_attn_triton.py:228-231).
+  for (int t = tid; t < n_tok; t += kSplitThreads) {
+    const int tok = tok0 + t;
+    int64_t off = -1;
+    if (tok >= a0 && tok < a1) {
+      const int pg = tok / p.bs;
+      const int slot = tok - pg * p.bs;
+      if (pg < p.W) {
+        const int phys = p.table[static_cast<int64_t>(b) * p.W + pg];
+        if (phys >= 0 && phys < p.num_blocks)
+          off = static_cast<int64_t>(phys) * p.blk_stride +
+                static_cast<int64_t>(slot) * p.slot_stride +
+                static_cast<int64_t>(kvh) * p.head_stride;
+      }
+    }
+    s_off[t] = off;
+  }
+
+  // Query rows for this lane's chunk of dims, pre-scaled by scale*log2(e).
+  const int c = lane % LPR;
+  const int tg = lane / LPR;
+  const bool c_ok = c < CHUNKS;
+  float qreg[RT][EPL];
+  {
+    const QT* qp = static_cast<const QT*>(p.q);
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) qreg[r][e] = 0.0f;
+      if (r < nrows && c_ok) {
+        const QT* src = qp + orow[r] * D + c * EPL;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) qreg[r][e] = Elt<QT>::load(src + e) * p.scale_log2;
+      }
+    }
+  }
+  __syncthreads();
+
+  const int nslots = ceil_div(n_tok, TPI);
+  const KT* kbase = static_cast<const KT*>(p.k);
+  const KT* vbase = static_cast<const KT*>(p.v);
+
+  // Phase 1: scores into s_sc[t * RT + r].
+  for (int s0 = w; s0 < nslots; s0 += kSplitWaves * U) {
+    uint4 raw[U];
+    int64_t offs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u * kSplitWaves;
+      const int t = s * TPI + tg;
+      const int64_t off = (s < nslots && t < n_tok) ? s_off[t] : -1;
+      offs[u] = off;
+      raw[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (off >= 0 && c_ok) raw[u] = *reinterpret_cast<const uint4*>(kbase + off + c * EPL);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float kf[EPL];
+      CK::unpack(raw[u], kf);
+      float dot[RT];
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        float a = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) a = fmaf(qreg[r][e], kf[e], a);
+        dot[r] = group_sum<LPR>(a);
+      }
+      const int s = s0 + u * kSplitWaves;
+      const int t = s * TPI + tg;
+      if (c == 0 && s < nslots && t < n_tok) {
+        const int tok = tok0 + t;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+          const bool ok = offs[u] >= 0 && tok >= lo_r[r] && tok < hi_r[r];
+          s_sc[t * RT + r] = ok ? dot[r] : -INFINITY;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // Phase 2: per-row max and sum over the partition; scores become weights.
+  for (int r = w; r < RT; r += kSplitWaves) {
+    float mx = -INFINITY;
+    for (int t = lane; t < n_tok; t += kWave) mx = fmaxf(mx, s_sc[t * RT + r]);
+    mx = group_max<kWave>(mx);
+    float sum = 0.0f;
+    for (int t = lane; t < n_tok; t += kWave) {
+      const float pr = mx == -INFINITY ? 0.0f : exp2f(s_sc[t * RT + r] - mx);
+      s_sc[t * RT + r] = pr;
+      sum += pr;
+    }
+    sum = group_sum<kWave>(sum);
+    if (lane == 0) {
+      s_m[r] = mx;
+      s_l[r] = sum;
+    }
+  }
+  __syncthreads();
+
+  // Phase 3: acc[r][:] = sum_t w[t][r] V[t][:].
+  float acc[RT][EPL];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[r][e] = 0.0f;
+
+  for (int s0 = w; s0 < nslots; s0 += kSplitWaves * U) {
+    uint4 raw[U];
+    int tt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u * kSplitWaves;
+      const int t = s * TPI + tg;
+      const int64_t off = (s < nslots && t < n_tok) ? s_off[t] : -1;
+      tt[u] = off >= 0 ? t : -1;
+      raw[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (off >= 0 && c_ok) raw[u] = *reinterpret_cast<const uint4*>(vbase + off + c * EPL);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (tt[u] >= 0) {
+        float vf[EPL];
+        CK::unpack(raw[u], vf);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+          const float pr = s_sc[tt[u] * RT + r];
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[r][e] = fmaf(pr, vf[e], acc[r][e]);
+        }
+      }
+    }
+  }
+
+  // Reduce over the TPI token groups of the wave (lanes c, c + LPR, ...).
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float a = acc[r][e];
+#pragma unroll
+      for (int o = LPR; o < kWave; o <<= 1) a += __shfl_xor(a, o, kWave);
+      acc[r][e] = a;
+    }
+  __syncthreads();  // every wave is done reading weights from s_sc
+  if (tg == 0 && c_ok) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) s_sc[(w * RT + r) * D + c * EPL + e] = acc[r][e];
+  }
+  __syncthreads();
+
+  for (int idx = tid; idx < nrows * D; idx += kSplitThreads) {
+    const int r = idx / D;
+    const int d = idx - r * D;
+    float a = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < kSplitWaves; ++ww) a += s_sc[(ww * RT + r) * D + d];
+    int64_t orr = 0;
+#pragma unroll
+    for (int rr = 0; rr < RT; ++rr)
+      if (rr == r) orr = orow[rr];
+    p.acc[(orr * p.max_parts + part) * D + d] = a;
+  }
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    if (r < nrows && tid == r) {
+      float* ml = p.ml + (orow[r] * p.max_parts + part) * 2;
+      ml[0] = s_m[r];
+      ml[1] = s_l[r];
+    }
+  }
+}
+
+// Host-side launch for one dtype pair; defined in split_<pair>.hip.
+template <typename QT, typename KT>
+hipError_t launch_split(const SplitParams& p, int D, int RT, hipStream_t stream, bool* supported);
+
+template <typename QT, typename KT, int D, int RT>
+hipError_t launch_split_one(const SplitParams& p, hipStream_t stream) {
+  const unsigned gx = static_cast<unsigned>(p.max_parts) * static_cast<unsigned>(p.KVH) *
+                      static_cast<unsigned>(p.rtiles);
+  dim3 grid(gx, 1, static_cast<unsigned>(p.batch));
+  hipLaunchKernelGGL((split_kernel<QT, KT, D, RT>), grid, dim3(kSplitThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+#define MSATTN_SPLIT_RT(QT, KT, D)                                           \
+  switch (RT) {                                                              \
+    case 1: return launch_split_one<QT, KT, D, 1>(p, stream);                \
+    case 2: return launch_split_one<QT, KT, D, 2>(p, stream);                \
+    case 4: return launch_split_one<QT, KT, D, 4>(p, stream);                \
+    case 8: return launch_split_one<QT, KT, D, 8>(p, stream);                \
+    default: break;                                                          \
+  }
+
+// Explicit specializations, one per compiled dtype pair (split_<pair>.hip).
+#define MSATTN_DECLARE_SPLIT(QT, KT)                                                   \
+  template <>                                                                          \
+  hipError_t launch_split<QT, KT>(const SplitParams& p, int D, int RT, hipStream_t stream, \
+                                  bool* supported);
+MSATTN_DECLARE_SPLIT(float, float)
+MSATTN_DECLARE_SPLIT(_Float16, _Float16)
+MSATTN_DECLARE_SPLIT(bf16_t, bf16_t)
+MSATTN_DECLARE_SPLIT(float, fp8_t)
+MSATTN_DECLARE_SPLIT(_Float16, fp8_t)
+MSATTN_DECLARE_SPLIT(bf16_t, fp8_t)
+#undef MSATTN_DECLARE_SPLIT
+
+}  // namespace msattn

@@ -1,0 +1,95 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol the header
+declares, and rejects bad arguments with status codes before touching the GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from miniserve_amd import _native as nat
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "msattn.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^[a-z][\w \*]*?\b(msattn_\w+)\(", text, flags=re.M)))
+
+
+def test_header_declares_the_bound_api():
+    names = declared_functions()
+    assert names == sorted(nat.SIGNATURES), names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nat.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_status_strings():
+    lib = nat.lib()
+    assert lib.msattn_abi_version() == 1
+    for code, text in [(0, b"ok"), (1, b"invalid argument"), (3, b"workspace too small"),
+                       (99, b"unknown status")]:
+        assert lib.msattn_status_string(code) == text
+
+
+@pytest.mark.parametrize("B,q_len,H,KVH,D,ctx,part", [
+    (64, 1, 32, 8, 128, 8192, 512),     # C3
+    (8, 1, 32, 8, 128, 131072, 512),    # C4
+    (32, 1, 14, 2, 64, 2048, 128),      # C2: few (row, head) units -> smaller partitions
+    (4, 1, 14, 2, 64, 512, 128),        # C1
+])
+def test_partition_policy(B, q_len, H, KVH, D, ctx, part):
+    lib = nat.lib()
+    assert lib.msattn_partition_tokens(B, q_len, H, KVH, D, ctx) == part
+    parts = -(-ctx // part)
+    ml = B * q_len * H * parts * 2 * 4
+    ml = -(-ml // 256) * 256
+    assert lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) == ml + B * q_len * H * parts * D * 4
+
+
+def test_workspace_rejects_bad_geometry():
+    lib = nat.lib()
+    assert lib.msattn_workspace_bytes(1, 1, 6, 4, 64, 16) == 0     # H % KVH != 0
+    assert lib.msattn_workspace_bytes(1, 1, 4, 4, 66, 16) == 0     # head_dim % 4 != 0
+    assert lib.msattn_partition_tokens(0, 1, 4, 4, 64, 16) == -1
+
+
+def _attn_args(**over):
+    buf = ctypes.create_string_buffer(1 << 16)
+    p = ctypes.addressof(buf)
+    p16 = (p + 15) // 16 * 16
+    args = dict(query=p16, k=p16, v=p16, bstride=16 * 2 * 64, sstride=2 * 64, hstride=64,
+                table=p16, lens=p16, out=p16, ws=p16, ws_bytes=1 << 15, batch=1, q_len=1, H=4,
+                KVH=2, D=64, bs=16, nb=4, W=1, max_ctx=16, causal=1, window=0, scale=0.125,
+                qd=nat.F32, kvd=nat.F32, stream=None)
+    args.update(over)
+    return buf, list(args.values())
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(query=None), nat.ERR_INVALID_ARG),
+    (dict(H=6, KVH=4), nat.ERR_INVALID_ARG),
+    (dict(batch=0), nat.ERR_INVALID_ARG),
+    (dict(qd=nat.FP8_E4M3), nat.ERR_INVALID_ARG),
+    (dict(kvd=7), nat.ERR_INVALID_ARG),
+    (dict(scale=float("nan")), nat.ERR_INVALID_ARG),
+    (dict(sstride=2 * 64 + 1), nat.ERR_INVALID_ARG),      # row not 16-byte aligned
+    (dict(ws_bytes=16), nat.ERR_WORKSPACE),
+    (dict(D=40, bstride=16 * 2 * 40, sstride=2 * 40, hstride=40), nat.ERR_UNSUPPORTED),
+    (dict(qd=nat.F32, kvd=nat.BF16), nat.ERR_UNSUPPORTED),
+])
+def test_paged_attention_argument_errors(over, status):
+    """Every error path returns before any HIP call, so it runs without a GPU."""
+    buf, args = _attn_args(**over)
+    assert nat.lib().msattn_paged_attention(*args) == status
+
+
+def test_check_maps_status_to_exceptions():
+    with pytest.raises(ValueError, match="workspace too small"):
+        nat.check("f", nat.ERR_WORKSPACE)
+    with pytest.raises(nat.MsattnError):
+        nat.check("f", nat.ERR_HIP)
+    nat.check("f", nat.OK)

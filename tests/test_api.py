@@ -1,0 +1,83 @@
+"""CPU checks of the PagedAttention interface (constructor contract, mask, errors)."""
+import pytest
+import torch
+
+from miniserve_amd import PagedAttention
+from oracle import paged_sdpa
+
+
+@pytest.mark.parametrize("kwargs,msg", [
+    (dict(num_heads=0, num_kv_heads=1, head_dim=8), "num_heads must be positive"),
+    (dict(num_heads=6, num_kv_heads=4, head_dim=8), "multiple of num_kv_heads"),
+    (dict(num_heads=4, num_kv_heads=2, head_dim=7), "positive even integer"),
+    (dict(num_heads=4, num_kv_heads=2, head_dim=None), "positive even integer"),
+    (dict(num_heads=4, num_kv_heads=2, head_dim=8, window=0), "window must be positive"),
+])
+def test_constructor_contract(kwargs, msg):
+    """The ValueErrors of miniserve/attention.py:81-92."""
+    with pytest.raises(ValueError, match=msg):
+        PagedAttention(**kwargs, num_blocks=4, block_size=16)
+
+
+def test_constructor_blocks():
+    with pytest.raises(ValueError, match="num_blocks and block_size"):
+        PagedAttention(4, 2, 8, num_blocks=0, block_size=16)
+
+
+def test_group_and_cache_layout():
+    """GQA KAT of tests/test_parity.py:135-136."""
+    pa = PagedAttention(32, 8, 64, num_blocks=12, block_size=8, kv_dtype=torch.float32)
+    assert pa.group == 4
+    kc, vc = pa.allocate_kv_cache()
+    assert kc.shape == (12, 8, 8, 64) and vc.dtype == torch.float32 and not kc.any()
+
+
+def test_fp8_cache_bytes():
+    pa8 = PagedAttention(4, 2, 32, num_blocks=8, block_size=8, kv_dtype=torch.float8_e4m3fn)
+    kc8, _ = pa8.allocate_kv_cache()
+    assert kc8.dtype == torch.float8_e4m3fn and kc8.element_size() == 1
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("window", [None, 64, 5])
+def test_build_mask_matches_oracle(causal, window):
+    pa = PagedAttention(4, 4, 16, num_blocks=4, block_size=16)
+    lens = torch.tensor([512, 300, 1])
+    got = pa.build_mask(lens, 2, window, causal)
+    assert torch.equal(got, paged_sdpa.build_mask(lens, 2, window, causal))
+
+
+def test_build_mask_window_kat():
+    pa = PagedAttention(4, 4, 16, num_blocks=4, block_size=16)
+    mask = pa.build_mask(torch.tensor([512, 300]), 2, 64)
+    assert not mask[0, 1, :448].any() and mask[0, 1, 448:512].all()
+
+
+def test_backend_contract_errors():
+    """The contract errors of attention.py:187-194, 231-232, raised before any device work."""
+    pa = PagedAttention(4, 4, 16, num_blocks=4, block_size=16, dtype=torch.float32)
+    kc, vc = pa.allocate_kv_cache()
+    q = torch.zeros(1, 1, 4, 16)
+    table = torch.zeros(1, 1, dtype=torch.long)
+    with pytest.raises(ValueError, match="decode-only"):
+        pa.forward(torch.zeros(1, 2, 4, 16), kc, vc, table, [8], backend="triton_flash")
+    with pytest.raises(ValueError, match="sliding window"):
+        pa.forward(q, kc, vc, table, [8], window=4, backend="triton_flash")
+    with pytest.raises(ValueError, match="causal decode only"):
+        pa.forward(q, kc, vc, table, [8], causal=False, backend="triton_flash")
+    with pytest.raises(ValueError, match="unknown attention backend"):
+        pa.forward(q, kc, vc, table, [8], backend="nope")
+    with pytest.raises(RuntimeError, match="requires CUDA"):
+        pa.forward(q, kc, vc, table, [8], backend="triton_flash")
+
+
+def test_cpu_tensors_fail_loudly():
+    """No CPU path: forward and write_kv on CPU tensors raise instead of falling back."""
+    pa = PagedAttention(4, 2, 16, num_blocks=4, block_size=16)
+    kc, vc = pa.allocate_kv_cache()
+    with pytest.raises(RuntimeError, match="GPU"):
+        pa.forward(torch.zeros(1, 1, 4, 16, dtype=torch.float16), kc, vc,
+                   torch.zeros(1, 1, dtype=torch.long), [1])
+    with pytest.raises(RuntimeError, match="GPU"):
+        pa.write_kv(kc, vc, torch.zeros(1, 1, 2, 16), torch.zeros(1, 1, 2, 16),
+                    torch.zeros(1, 1, dtype=torch.long))

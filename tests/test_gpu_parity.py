@@ -1,0 +1,381 @@
+"""GPU parity: the HIP path (libmsattn.so through PagedAttention) against the oracle.
+
+Bars (written into each test):
+  * gather / write_kv addressing: bit-exact (torch.equal);
+  * fp32: max-abs error <= 1e-4 against the float64 oracle;
+  * bf16 / fp16: max|out - ref| / max|ref| <= 2e-2 against the float64 oracle
+    on the same (already rounded) inputs;
+  * the reference's own gates where it states them (tests/test_parity.py:120-192,
+    tests/test_triton_parity.py:55-123).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from miniserve_amd import PagedAttention, gather_kv, paged_attention
+from miniserve_amd.workloads import make_workload
+from oracle import dense, paged_sdpa, split_k
+
+pytestmark = pytest.mark.gpu
+
+FP32_ATOL = 1e-4
+BF16_REL = 2e-2
+
+
+def rel_err(out: torch.Tensor, ref: np.ndarray) -> float:
+    o = out.double().cpu().numpy()
+    return float(np.abs(o - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def abs_err(out: torch.Tensor, ref: np.ndarray) -> float:
+    return float(np.abs(out.double().cpu().numpy() - ref).max())
+
+
+def note(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+
+
+def scenario(h, kv_heads, d, lens, q_len=1, block_size=8, dtype=torch.float32, seed=0,
+             scale=1.0, kv_dtype=None, scatter=True):
+    """CPU inputs: seeded q + dense k/v written into a paged cache by the oracle."""
+    g = torch.Generator().manual_seed(seed)
+    kv_dtype = dtype if kv_dtype is None else kv_dtype
+    batch, max_l = len(lens), max(lens)
+    nblocks = max(1, (max_l + block_size - 1) // block_size)
+    q = (torch.randn(batch, q_len, h, d, generator=g) * scale).to(dtype)
+    k = torch.randn(batch, max_l, kv_heads, d, generator=g) * scale
+    v = torch.randn(batch, max_l, kv_heads, d, generator=g) * scale
+    pool = batch * nblocks
+    kc = torch.zeros(pool, block_size, kv_heads, d, dtype=kv_dtype)
+    vc = torch.zeros(pool, block_size, kv_heads, d, dtype=kv_dtype)
+    order = torch.randperm(pool, generator=g) if scatter else torch.arange(pool)
+    table = order.view(batch, nblocks).clone()
+    for i, length in enumerate(lens):
+        paged_sdpa.write_kv(kc, vc, k[i:i + 1, :length], v[i:i + 1, :length], table[i:i + 1], 0)
+    return q, kc, vc, table, lens
+
+
+def run_hip(device, q, kc, vc, table, lens, **kw):
+    return paged_attention(q.to(device), kc.to(device), vc.to(device), table, lens, **kw)
+
+
+# ------------------------------------------------------------------ addressing
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
+def test_gather_bit_exact(device, dtype):
+    note(f"gather {dtype}")
+    g = torch.Generator().manual_seed(21)
+    nb, bs, kvh, d = 40, 16, 2, 64
+    bits = {torch.float32: torch.int32, torch.bfloat16: torch.int16,
+            torch.float8_e4m3fn: torch.uint8}[dtype]
+    if bits == torch.uint8:
+        raw = torch.randint(0, 256, (nb, bs, kvh, d), generator=g, dtype=torch.uint8)
+    else:
+        info = torch.iinfo(bits)
+        raw = torch.randint(info.min, info.max, (nb, bs, kvh, d), generator=g, dtype=bits)
+    cache = raw.view(dtype)
+    table = torch.randperm(nb, generator=g)[:36].view(3, 12)
+    lens = [190, 17, 1]
+    got = gather_kv(cache.to(device), table, lens, max_context=190)
+    want = paged_sdpa.gather(cache, table, torch.tensor(lens), 190)
+    assert torch.equal(got.cpu().view(bits), want.view(bits))
+
+
+@pytest.mark.parametrize("src,dst", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                     (torch.float32, torch.bfloat16), (torch.float32, torch.float16),
+                                     (torch.float16, torch.float32)])
+def test_write_kv_bit_exact(device, src, dst):
+    note(f"write_kv {src}->{dst}")
+    g = torch.Generator().manual_seed(22)
+    nb, bs, kvh, d = 30, 16, 2, 32
+    pa = PagedAttention(4, kvh, d, num_blocks=nb, block_size=bs, kv_dtype=dst, device=device)
+    kc, vc = pa.allocate_kv_cache()
+    k = (torch.randn(3, 20, kvh, d, generator=g) * 3).to(src)
+    v = (torch.randn(3, 20, kvh, d, generator=g) * 3).to(src)
+    table = torch.randperm(nb, generator=g)[:9].view(3, 3)
+    starts = [0, 5, 27]
+    pa.write_kv(kc, vc, k.to(device), v.to(device), table.to(device), start=starts)
+    kc_ref = torch.zeros(nb, bs, kvh, d, dtype=dst)
+    vc_ref = torch.zeros(nb, bs, kvh, d, dtype=dst)
+    paged_sdpa.write_kv(kc_ref, vc_ref, k, v, table, start=starts)
+    assert torch.equal(kc.cpu(), kc_ref) and torch.equal(vc.cpu(), vc_ref)
+
+
+def test_write_kv_skips_holes(device):
+    """Pad rows (table -1) write nothing -- unlike the reference's wraparound."""
+    note("write_kv holes")
+    pa = PagedAttention(2, 2, 16, num_blocks=4, block_size=16, kv_dtype=torch.float32,
+                        device=device)
+    kc, vc = pa.allocate_kv_cache()
+    k = torch.ones(2, 1, 2, 16, device=device)
+    table = torch.tensor([[1], [-1]], device=device)
+    pa.write_kv(kc, vc, k, k, table, start=[3, 0])
+    assert kc[1, 3].eq(1).all() and kc.sum().item() == 32 and vc.sum().item() == 32
+
+
+# ------------------------------------------------------------------ reference gates
+
+def test_mha_ragged_q_len3(device):
+    """tests/test_parity.py:120-128 (MHA, ragged, q_len 3, block 8) at 1e-4."""
+    note("mha q_len=3")
+    q, kc, vc, table, lens = scenario(8, 8, 16, [8, 13, 21], q_len=3)
+    out = run_hip(device, q, kc, vc, table, lens)
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens)
+    assert abs_err(out, ref) < FP32_ATOL
+
+
+def test_gqa_32_8(device):
+    """tests/test_parity.py:131-141 (GQA 32q/8kv, D 64): gate 1e-3, checked at 1e-4."""
+    note("gqa 32/8")
+    q, kc, vc, table, lens = scenario(32, 8, 64, [32, 47])
+    out = run_hip(device, q, kc, vc, table, lens)
+    assert abs_err(out, dense.paged_attention_f64(q, kc, vc, table, lens)) < FP32_ATOL
+
+
+def test_mqa(device):
+    """tests/test_parity.py:144-153 (MQA 8q/1kv, D 32)."""
+    note("mqa")
+    q, kc, vc, table, lens = scenario(8, 1, 32, [16, 23])
+    out = run_hip(device, q, kc, vc, table, lens)
+    assert abs_err(out, dense.paged_attention_f64(q, kc, vc, table, lens)) < FP32_ATOL
+
+
+def test_sliding_window(device):
+    """tests/test_parity.py:156-171: window 64 over ctx 512, q_len 2, block 16."""
+    note("window")
+    q, kc, vc, table, lens = scenario(4, 4, 16, [512, 300], q_len=2, block_size=16)
+    pa = PagedAttention(4, 4, 16, num_blocks=kc.shape[0], block_size=16, window=64,
+                        dtype=torch.float32, kv_dtype=torch.float32, device=device)
+    out = pa.forward(q.to(device), kc.to(device), vc.to(device), table, lens)
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens, window=64)
+    assert abs_err(out, ref) < FP32_ATOL
+
+
+def test_fp8_kv_vs_fp16(device):
+    """tests/test_parity.py:174-192: FP8 e4m3 cache within 5e-2 of the FP16 cache."""
+    note("fp8")
+    kw = dict(q_len=1, block_size=8, dtype=torch.float16, seed=3, scale=0.25, scatter=False)
+    q, kc16, vc16, table, lens = scenario(4, 2, 32, [16, 24], kv_dtype=torch.float16, **kw)
+    q8, kc8, vc8, _, _ = scenario(4, 2, 32, [16, 24], kv_dtype=torch.float8_e4m3fn, **kw)
+    assert torch.equal(q, q8)
+    out16 = run_hip(device, q, kc16, vc16, table, lens)
+    out8 = run_hip(device, q8, kc8, vc8, table, lens)
+    assert (out16.float() - out8.float()).abs().max().item() < 5e-2
+    # and the fp8 path itself matches the float64 oracle on the fp8 values
+    ref8 = dense.paged_attention_f64(q8, kc8, vc8, table, lens)
+    assert rel_err(out8, ref8) < BF16_REL
+
+
+def test_triton_flash_backend_and_rope(device):
+    """backend="triton_flash" keeps the reference contract and its fused-RoPE result
+    (tests/test_triton_parity.py:71-81, :165-177)."""
+    note("triton_flash rope")
+    ctx, D = 300, 64
+    q, kc, vc, table, _ = scenario(4, 2, D, [ctx], block_size=16)
+    inv = 1.0 / (10000 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    emb = torch.outer(torch.arange(ctx + 1, dtype=torch.float32), inv)
+    emb = torch.cat([emb, emb], dim=-1)
+    cos, sin = torch.cos(emb), torch.sin(emb)
+    pos = torch.tensor([ctx - 1])
+    pa = PagedAttention(4, 2, D, num_blocks=kc.shape[0], block_size=16, dtype=torch.float32,
+                        kv_dtype=torch.float32, device=device)
+    got = pa.forward(q.to(device), kc.to(device), vc.to(device), table, [ctx],
+                     backend="triton_flash", cos=cos.to(device), sin=sin.to(device),
+                     position=pos.to(device))
+    ref = split_k.split_k_decode(q, kc, vc, table, [ctx], cos=cos, sin=sin, position=pos)
+    assert (got.cpu() - ref).abs().max().item() < 1e-4
+
+
+def test_shape_fuzz_50(device):
+    """Seeds 1000+i as tests/test_triton_parity.py:110-123, HIP vs float64 oracle."""
+    for i in range(50):
+        gen = torch.Generator().manual_seed(1000 + i)
+        B = int(torch.randint(1, 4, (1,), generator=gen))
+        KVH = int(torch.randint(1, 3, (1,), generator=gen))
+        factor = int(torch.randint(1, 5, (1,), generator=gen))
+        H, D = KVH * factor, int(torch.randint(2, 5, (1,), generator=gen)) * 8
+        ctx = int(torch.randint(1, 65, (1,), generator=gen))
+        bs = (8, 16, 32)[int(torch.randint(0, 3, (1,), generator=gen))]
+        note(f"fuzz #{i} B={B} H={H} KVH={KVH} D={D} ctx={ctx} bs={bs}")
+        q, kc, vc, table, lens = scenario(H, KVH, D, [ctx] * B, block_size=bs, seed=i)
+        out = run_hip(device, q, kc, vc, table, lens)
+        err = abs_err(out, dense.paged_attention_f64(q, kc, vc, table, lens))
+        assert err < FP32_ATOL, f"shape #{i}: err {err}"
+
+
+# ------------------------------------------------------------------ edge cases
+
+def test_ragged_zero_and_one(device):
+    """Ragged lens [64, 17, 33] (tests/test_triton_parity.py:99-107), plus context 0
+    (zeros) and context 1 (exactly V[0])."""
+    note("ragged 0/1")
+    q, kc, vc, table, _ = scenario(4, 2, 16, [64, 64, 64, 64, 64], block_size=16)
+    lens = [64, 17, 33, 0, 1]
+    out = run_hip(device, q, kc, vc, table, lens).cpu()
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens)
+    assert abs_err(out, ref) < FP32_ATOL
+    assert not out[3].any()
+    for h in range(4):
+        assert torch.equal(out[4, 0, h], vc[table[4, 0], 0, h // 2])
+
+
+def test_nan_poisoned_tail_is_never_read(device):
+    """Slots past each row's length hold NaN; the output must stay finite and exact."""
+    note("nan tail")
+    q, kc, vc, table, lens = scenario(8, 2, 64, [37, 100, 16], block_size=16, seed=5)
+    kc, vc = kc.clone(), vc.clone()
+    for b, L in enumerate(lens):
+        for pos in range(L, table.shape[1] * 16):
+            kc[table[b, pos // 16], pos % 16] = float("nan")
+            vc[table[b, pos // 16], pos % 16] = float("nan")
+    out = run_hip(device, q, kc, vc, table, lens)
+    assert torch.isfinite(out).all()
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens)
+    assert abs_err(out, ref) < FP32_ATOL
+
+
+def test_holes_are_masked(device):
+    """A -1 page inside the context is a hole: its tokens drop out of the softmax."""
+    note("holes")
+    q, kc, vc, table, lens = scenario(4, 2, 32, [64], block_size=16, seed=12)
+    holed = table.clone()
+    holed[0, 1] = -1
+    out = run_hip(device, q, kc, vc, holed, lens)
+    keep_pages = [table[0, 0], table[0, 2], table[0, 3]]
+    kc2 = torch.stack([kc[p] for p in keep_pages])
+    vc2 = torch.stack([vc[p] for p in keep_pages])
+    ref = dense.paged_attention_f64(q, kc2, vc2, torch.tensor([[0, 1, 2]]), [48])
+    assert abs_err(out, ref) < FP32_ATOL
+
+
+def test_partition_invariance(device):
+    """max_context changes the partition size; the result may not change beyond fp32 noise."""
+    note("partition invariance")
+    q, kc, vc, table, lens = scenario(8, 2, 64, [2000, 1500, 700], block_size=16, seed=13)
+    a = run_hip(device, q, kc, vc, table, lens, max_context=2000)
+    b = run_hip(device, q, kc, vc, table, lens, max_context=table.shape[1] * 16)
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens)
+    assert abs_err(a, ref) < FP32_ATOL and abs_err(b, ref) < FP32_ATOL
+    assert (a - b).abs().max().item() < 1e-5
+
+
+def test_deterministic(device):
+    note("determinism")
+    q, kc, vc, table, lens = scenario(32, 8, 128, [3000, 1000], block_size=16, seed=14,
+                                      dtype=torch.bfloat16)
+    a = run_hip(device, q, kc, vc, table, lens)
+    b = run_hip(device, q, kc, vc, table, lens)
+    assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ benchmark configs
+
+@pytest.fixture(scope="module")
+def c3():
+    note("building C3 inputs")
+    return make_workload(3)
+
+
+def check_workload(device, w, rows=None):
+    q = w.query
+    kc, vc = w.k_caches[0], w.v_caches[0]
+    note(f"{w.name}: B={w.batch} q_len={w.q_len} H={w.num_heads} KVH={w.num_kv_heads} "
+         f"D={w.head_dim} max_ctx={max(w.lens)} dtype={w.dtype}")
+    out = paged_attention(q.to(device), kc.to(device), vc.to(device), w.table, w.lens)
+    ref = dense.paged_attention_f64(q, kc, vc, w.table, w.lens, rows=rows)
+    sel = list(range(w.batch)) if rows is None else rows
+    o = out.cpu()[sel]
+    r = ref[sel]
+    if w.dtype == torch.float32:
+        err = abs_err(o, r)
+        note(f"{w.name} max-abs {err:.3e}")
+        assert err < FP32_ATOL
+    else:
+        err = rel_err(o, r)
+        note(f"{w.name} max-rel {err:.3e}")
+        assert err < BF16_REL
+    return out
+
+
+def test_c1_fp32(device):
+    check_workload(device, make_workload(1))
+
+
+def test_c2_layer0_bf16(device):
+    check_workload(device, make_workload(2, layers=1))
+
+
+def test_c3_bf16(device, c3):
+    check_workload(device, c3)
+
+
+def test_c3_shared_rows_consistent(device, c3):
+    """Size-independent property at full C3 size: a row's result depends only on its own
+    query, table and length -- running a sub-batch reproduces the same rows bit-exactly."""
+    kc, vc = c3.k_caches[0].to(device), c3.v_caches[0].to(device)
+    full = paged_attention(c3.query.to(device), kc, vc, c3.table, c3.lens,
+                           max_context=max(c3.lens))
+    sub = [5, 17, 40]
+    part = paged_attention(c3.query[sub].to(device), kc, vc, c3.table[sub],
+                           [c3.lens[i] for i in sub], max_context=max(c3.lens))
+    assert torch.equal(full[sub], part)
+
+
+def test_c4_long_context_rows(device):
+    w = make_workload(4, values_device=device)
+    w.query = w.query.cpu()
+    w.k_caches = [w.k_caches[0].cpu()]
+    w.v_caches = [w.v_caches[0].cpu()]
+    check_workload(device, w, rows=[0, 7])
+
+
+def test_c5_decode(device):
+    check_workload(device, make_workload(5, part="decode"))
+
+
+def test_c5_prefill_chunk(device):
+    check_workload(device, make_workload(5, part="prefill"))
+
+
+# ------------------------------------------------------------------ graphs
+
+def test_graph_capture_replay(device):
+    """The call is capture-safe: replays with new inputs match eager every time."""
+    note("graph capture")
+    H, KVH, D, bs = 32, 8, 128, 16
+    q, kc, vc, table, lens = scenario(H, KVH, D, [900, 1700, 33, 2048], block_size=bs, seed=15,
+                                      dtype=torch.bfloat16)
+    kc, vc = kc.to(device), vc.to(device)
+    static_q = q.to(device)
+    static_table = table.to(device=device, dtype=torch.int32)
+    static_lens = torch.tensor(lens, dtype=torch.int32, device=device)
+    cap = table.shape[1] * bs
+    ws_bytes = 64 << 20
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty_like(static_q)
+
+    def step():
+        paged_attention(static_q, kc, vc, static_table, static_lens, max_context=cap,
+                        workspace=ws, out=out)
+
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream(device).wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    g = torch.Generator().manual_seed(16)
+    for rep in range(4):
+        new_lens = [int(x) for x in torch.randint(0, cap + 1, (4,), generator=g)]
+        static_q.copy_(torch.randn(q.shape, generator=g).to(torch.bfloat16))
+        static_lens.copy_(torch.tensor(new_lens, dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = paged_attention(static_q, kc, vc, static_table, new_lens, max_context=cap)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay {rep}"
