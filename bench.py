@@ -43,7 +43,36 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="instead of the decode bench, time a plain streaming kernel "
+                         "(out = in * 1 over 1 GiB fp32): the measured HBM ceiling and the "
+                         "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
+
+
+def stream_probe(steps: int):
+    """1 GiB fp32 read + 1 GiB written per dispatch by torch's elementwise multiply."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    n = (1 << 30) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        torch.mul(src, 1.0, out=dst)
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    gbs = 2 * (1 << 30) / (ms * 1e-3) / 1e9
+    print(json.dumps({"metric": "streaming kernel HBM bandwidth (read + write)",
+                      "value": round(gbs, 1), "unit": "GB/s", "ms_per_dispatch": round(ms, 4),
+                      "bytes_read_per_dispatch": 1 << 30, "bytes_written_per_dispatch": 1 << 30,
+                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
 
 
 def main():
@@ -54,6 +83,9 @@ def main():
                                    "exactly one GPU (--gpus 1); multi-GPU figures are not "
                                    "produced", "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.stream_probe:
+        stream_probe(args.steps)
+        return
 
     import torch
 

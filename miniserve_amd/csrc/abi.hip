@@ -3,6 +3,7 @@
 #include <cmath>
 #include <cstdint>
 
+#include "decode_mfma.h"
 #include "kernels.h"
 #include "msattn.h"
 
@@ -140,7 +141,11 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
 
   const int G = num_heads / num_kv_heads;
   const int rows = q_len * G;
-  const int RT = rows_per_tile(rows);
+  // MFMA path: bf16/fp16 KV read by a same-typed query, head_dim 64 or 128, pages
+  // holding whole 16-token tiles. Everything else takes the generic kernel.
+  const bool use_mfma = q_dtype == kv_dtype && (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
+                        (head_dim == 64 || head_dim == 128) && block_size % 16 == 0;
+  const int RT = use_mfma ? (rows >= 16 ? 16 : next_pow2(rows)) : rows_per_tile(rows);
   SplitParams p;
   p.q = query;
   p.k = k_cache;
@@ -172,8 +177,15 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
   if (gx >= (int64_t(1) << 31) || batch > 65535) return MSATTN_ERR_UNSUPPORTED;
 
   bool sup = false;
-  const hipError_t e = dispatch_split(p, q_dtype, kv_dtype, head_dim, RT,
-                                      static_cast<hipStream_t>(stream), &sup);
+  hipError_t e = hipSuccess;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_mfma && q_dtype == MSATTN_BF16) {
+    e = launch_decode_mfma<bf16_t>(p, head_dim, RT, st, &sup);
+  } else if (use_mfma) {
+    e = launch_decode_mfma<_Float16>(p, head_dim, RT, st, &sup);
+  } else {
+    e = dispatch_split(p, q_dtype, kv_dtype, head_dim, RT, st, &sup);
+  }
   if (!sup) return MSATTN_ERR_UNSUPPORTED;
   return hip_status(e);
 }

@@ -1,0 +1,414 @@
+// Paged decode partials with MFMA scores (gfx950, bf16/fp16 KV, head_dim 64 or 128).
+//
+// Same contract and workspace output as split_kernel (split_kernel.h): one
+// workgroup per (sequence b, KV head, row tile, context partition), writing the
+// partial (m, l, acc) of each query row over the partition's keys.
+//
+// Differences from split_kernel, which make this the fast path:
+//  * Tiles of 16 tokens (one page slice) are processed with an online softmax;
+//    each wave owns a contiguous run of tiles and keeps the next tile's K and V
+//    loads in flight while it computes the current one (no block barrier until
+//    the final combine).
+//  * S = K Q^T for a tile is D/32 v_mfma_f32_16x16x32 instructions: the K rows
+//    are the A operand straight from their 16-byte global loads (lane l holds
+//    K[token pi(l%16)][dims 8*(4j + l/16) .. +8] for MFMA j) and the packed query
+//    rows are the B operand (lane l holds Q[row l%16][the same dims]). Lane
+//    (g = l/16, n = l%16) receives the scores of query row n for the tile tokens
+//    pi(4g + r), r = 0..3.
+//  * pi is chosen so that the 16-lane row g that holds those scores is also the
+//    row whose V lanes need them: V is loaded with LPR = D/8 lanes per token row,
+//    and the tokens of V lanes in DPP row g are exactly {pi(4g + r)}. The P.V
+//    FMAs then take P[n][token] from lane 16g + n through DPP row_newbcast,
+//    without LDS traffic.
+//  * The 4 waves' (m, l, acc) are combined in LDS once at the end.
+//
+// Masking, key ranges and the partial format follow split_kernel and hence
+// kernels/paged_attn_triton.py:176-248 and miniserve/attention.py:135-153.
+#pragma once
+
+#include <type_traits>
+#include <utility>
+
+#include "split_kernel.h"
+
+namespace msattn {
+
+typedef __bf16 mf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mf_f16x8 __attribute__((ext_vector_type(8)));
+typedef float mf_f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16_t> {
+  __device__ static mf_f32x4 mac(const uint4& a, const uint4& b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mf_bf16x8, a),
+                                                   __builtin_bit_cast(mf_bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<_Float16> {
+  __device__ static mf_f32x4 mac(const uint4& a, const uint4& b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf_f16x8, a),
+                                                  __builtin_bit_cast(mf_f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// Value of `v` in lane 16 * (lane / 16) + N (DPP row_newbcast).
+template <int N>
+__device__ __forceinline__ float row_bcast(float v) {
+  static_assert(N >= 0 && N < 16, "row_newbcast source lane");
+  const int x = __float_as_int(v);
+  return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x150 + N, 0xF, 0xF, false));
+}
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Raw buffer loads through a per-tile descriptor: a tile whose descriptor has
+// num_records = 0 (a hole, or a tile past the wave's range) reads zeros and
+// moves no memory, so the tile loop needs no branch around its loads.
+typedef unsigned int mf_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufferRsrcWord3 = 0x00020000;  // gfx9-family raw buffer, 32-bit format
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
+                                           kBufferRsrcWord3);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const mf_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_off), 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+constexpr int kMfmaThreads = 256;
+constexpr int kMfmaWaves = kMfmaThreads / kWave;
+constexpr int kMaxTilesPerWave = kPartMax / 16 / kMfmaWaves;  // partitions are <= kPartMax tokens
+
+// Token (within a 16-token tile) whose score lands in MFMA row i = 4g + r.
+template <int D>
+__host__ __device__ constexpr int tile_token(int i) {
+  constexpr int LPR = D / 8;      // V lanes per token row
+  constexpr int TPI = 64 / LPR;   // tokens per V load instruction
+  constexpr int APR = 16 / LPR;   // token groups per 16-lane row
+  const int g = i / 4, r = i % 4;
+  return TPI * (r / APR) + g * APR + (r % APR);
+}
+
+template <typename T, int D, int RT>
+__global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitParams p) {
+  static_assert(D == 64 || D == 128, "MFMA decode handles head_dim 64 and 128");
+  static_assert(RT >= 1 && RT <= 16, "at most 16 query rows per tile");
+  constexpr int JD = D / 32;        // MFMAs per tile
+  constexpr int LPR = D / 8;        // V lanes per token row
+  constexpr int TPI = 64 / LPR;     // V tokens per load instruction
+  constexpr int NJ = 16 / TPI;      // V load instructions per tile
+  constexpr int APR = 16 / LPR;     // token groups per 16-lane row
+
+  __shared__ float s_red[kMfmaWaves][RT][D];
+  __shared__ float s_ml[kMfmaWaves][RT][2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  // wave index, made visibly wave-uniform so loop control stays scalar
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int g = lane >> 4;   // MFMA lane group
+  const int n = lane & 15;   // MFMA column = query row of the tile
+  const int va = lane / LPR; // V token group
+  const int vc = lane % LPR; // V 16-byte chunk
+
+  // blockIdx.x = kvh + KVH * (part + max_parts * rtile); blockIdx.z = b.
+  const unsigned bx = blockIdx.x;
+  const int kvh = static_cast<int>(bx % static_cast<unsigned>(p.KVH));
+  const unsigned rest = bx / static_cast<unsigned>(p.KVH);
+  const int part = static_cast<int>(rest % static_cast<unsigned>(p.max_parts));
+  const int rtile = static_cast<int>(rest / static_cast<unsigned>(p.max_parts));
+  const int b = blockIdx.z;
+
+  int ctx = p.lens[b];
+  ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
+  const int nparts = ctx > 0 ? ceil_div(ctx, p.part) : 1;
+  if (part >= nparts) return;
+
+  const int row0 = rtile * RT;
+  const int nrows = min(RT, p.rows_per_kvh - row0);
+
+  // Key range of the tile's first and last rows (ranges grow with the query index).
+  const int i_first = row0 / p.G;
+  const int i_last = (row0 + nrows - 1) / p.G;
+  const int lo_all = p.window > 0 ? max(0, ctx - p.q_len + i_first - p.window + 1) : 0;
+  const int hi_all = p.causal ? min(ctx, ctx - p.q_len + i_last + 1) : ctx;
+  const int tok0 = part * p.part;
+  const int a0 = max(tok0, lo_all);
+  const int a1 = min(min(tok0 + p.part, ctx), hi_all);
+
+  // This lane's query row n: key range [lo_n, hi_n) and output row.
+  int lo_n = 0, hi_n = 0;
+  int64_t orow_n = 0;
+  if (n < nrows) {
+    const int gr = row0 + n;
+    const int i = gr / p.G;
+    const int qpos = ctx - p.q_len + i;
+    hi_n = p.causal ? min(ctx, qpos + 1) : ctx;
+    lo_n = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
+    if (hi_n < lo_n) hi_n = lo_n;
+    orow_n = (static_cast<int64_t>(b) * p.q_len + i) * p.H + (kvh * p.G + (gr - i * p.G));
+  }
+
+  if (a1 <= a0) {
+    if (tid < nrows) {
+      float* ml = p.ml + (orow_n * p.max_parts + part) * 2;
+      ml[0] = -INFINITY;
+      ml[1] = 0.0f;
+    }
+    return;
+  }
+
+  // Tiles [t_begin, t_end) of 16 absolute positions; wave w owns a contiguous run.
+  const int t_begin = a0 / 16;
+  const int t_end = ceil_div(a1, 16);
+  const int per_wave = ceil_div(t_end - t_begin, kMfmaWaves);
+  const int tw0 = t_begin + w * per_wave;
+  const int nt = max(0, min(per_wave, t_end - tw0));
+
+  // Page ids of the wave's tiles: lane k holds tile tw0 + k's element offset, or -1
+  // for a hole (a table entry outside [0, num_blocks) or a page past the table).
+  int64_t my_base = -1;
+  if (lane < nt) {
+    const int t = tw0 + lane;
+    const int pg = (t * 16) / p.bs;
+    const int slot0 = t * 16 - pg * p.bs;
+    if (pg < p.W) {
+      const int phys = p.table[static_cast<int64_t>(b) * p.W + pg];
+      if (phys >= 0 && phys < p.num_blocks)
+        my_base = static_cast<int64_t>(phys) * p.blk_stride +
+                  static_cast<int64_t>(slot0) * p.slot_stride +
+                  static_cast<int64_t>(kvh) * p.head_stride;
+    }
+  }
+
+  // Query rows as the MFMA B operand: lane (g, n) holds Q[row n][dims 8*(4j+g) .. +8].
+  uint4 qb[JD];
+  {
+    const T* qp = static_cast<const T*>(p.q);
+#pragma unroll
+    for (int j = 0; j < JD; ++j) {
+      qb[j] = make_uint4(0u, 0u, 0u, 0u);
+      if (n < nrows) qb[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + (4 * j + g) * 8);
+    }
+  }
+
+  // Per-lane byte offsets inside a tile (32-bit: a tile spans 16 slots).
+  constexpr int EB = static_cast<int>(sizeof(T));
+  const uint32_t k_lane_off =
+      static_cast<uint32_t>((tile_token<D>(n) * p.slot_stride + g * 8) * EB);  // + 64*j
+  uint32_t v_lane_off[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    v_lane_off[j] = static_cast<uint32_t>(((TPI * j + va) * p.slot_stride + vc * 8) * EB);
+  const int tile_bytes = static_cast<int>((15 * p.slot_stride + D) * EB);
+
+  const T* kbase = static_cast<const T*>(p.k);
+  const T* vbase = static_cast<const T*>(p.v);
+
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+  float acc[RT][8];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
+
+  // Element offset of the wave's tile k, or -1 (hole, or k >= nt).
+  auto tile_base = [&](int k) -> int64_t {
+    const uint32_t lo = static_cast<uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(my_base)), k));
+    const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
+    return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
+  };
+  auto issue = [&](int64_t base, uint4 (&kb)[JD], uint4 (&vb)[NJ]) {
+    const bool ok = base >= 0;
+    const int64_t b0 = ok ? base : 0;
+    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
+    const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
+#pragma unroll
+    for (int j = 0; j < JD; ++j) kb[j] = buffer_load16(rk, k_lane_off + 64 * j);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) vb[j] = buffer_load16(rv, v_lane_off[j]);
+  };
+
+  auto consume = [&](int k, const uint4 (&kb)[JD], const uint4 (&vb)[NJ], int64_t base) {
+    mf_f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < JD; ++j) s = Mfma16<T>::mac(kb[j], qb[j], s);
+    const int t0 = (tw0 + k) * 16;
+    const bool hole = base < 0;
+    float sc[4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tok = t0 + tile_token<D>(4 * g + r);
+      const bool ok = !hole && tok >= lo_n && tok < hi_n;
+      sc[r] = ok ? s[r] * p.scale_log2 : -INFINITY;
+      mt = fmaxf(mt, sc[r]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float m_new = fmaxf(m_run, mt);
+    const bool live = m_new != -INFINITY;
+    const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+    float pr[4];
+    float psum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = live ? __builtin_amdgcn_exp2f(sc[r] - m_new) : 0.0f;
+      psum += pr[r];
+    }
+    l_run = fmaf(l_run, alpha, psum);
+    m_run = m_new;
+
+    static_for<RT>([&](auto nc) {
+      constexpr int rn = decltype(nc)::value;
+      const float al = row_bcast<rn>(alpha);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[rn][e] *= al;
+    });
+    // Rows outside the tile's key range (partial tiles) may hold anything, even
+    // NaN: their values are replaced by zeros before the weights meet them.
+    const bool partial = t0 < a0 || t0 + 16 > a1;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      float vf[8];
+      uint4 vv = vb[j];
+      if (partial) {  // wave-uniform branch; per-lane selects inside
+        const int vtok = t0 + TPI * j + va;
+        const bool keep = vtok >= a0 && vtok < a1;
+        vv.x = keep ? vv.x : 0u;
+        vv.y = keep ? vv.y : 0u;
+        vv.z = keep ? vv.z : 0u;
+        vv.w = keep ? vv.w : 0u;
+      }
+      Chunk<T>::unpack(vv, vf);
+      static_for<RT>([&](auto nc) {
+        constexpr int rn = decltype(nc)::value;
+        float pb;
+        if constexpr (APR == 1) {
+          pb = row_bcast<rn>(pr[j]);
+        } else {
+          const float b0 = row_bcast<rn>(pr[APR * j]);
+          const float b1 = row_bcast<rn>(pr[APR * j + 1]);
+          pb = (va & 1) ? b1 : b0;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[rn][e] = fmaf(pb, vf[e], acc[rn][e]);
+      });
+    }
+  };
+
+  // Two tiles in flight. The sequence is fully unrolled (a wave owns at most
+  // kMaxTilesPerWave tiles) so every wait for a tile's loads is exact; a load for
+  // tile nt reads nothing (its descriptor has no records).
+  uint4 k0[JD], v0[NJ], k1[JD], v1[NJ];
+  int64_t base0 = tile_base(0);
+  issue(base0, k0, v0);
+#pragma unroll
+  for (int k = 0; k < kMaxTilesPerWave; k += 2) {
+    if (k >= nt) break;
+    const int64_t base1 = tile_base(k + 1);
+    issue(base1, k1, v1);
+    consume(k, k0, v0, base0);
+    if (k + 1 >= nt) break;
+    if (k + 2 < kMaxTilesPerWave) {
+      base0 = tile_base(k + 2);
+      issue(base0, k0, v0);
+    }
+    consume(k + 1, k1, v1, base1);
+  }
+
+  // Wave totals: l over the 4 lane groups, acc over the V token groups.
+  l_run += __shfl_xor(l_run, 16, kWave);
+  l_run += __shfl_xor(l_run, 32, kWave);
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float a = acc[r][e];
+#pragma unroll
+      for (int o = LPR; o < kWave; o <<= 1) a += __shfl_xor(a, o, kWave);
+      acc[r][e] = a;
+    }
+  if (lane < RT) {
+    s_ml[w][lane][0] = m_run;
+    s_ml[w][lane][1] = l_run;
+  }
+  if (va == 0) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_red[w][r][vc * 8 + e] = acc[r][e];
+  }
+  __syncthreads();
+
+  // Combine the waves: rescale each to the common max.
+  for (int idx = tid; idx < nrows * D; idx += kMfmaThreads) {
+    const int r = idx / D;
+    const int d = idx - r * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kMfmaWaves; ++ww) M = fmaxf(M, s_ml[ww][r][0]);
+    float a = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int ww = 0; ww < kMfmaWaves; ++ww) {
+        const float mw = s_ml[ww][r][0];
+        if (mw != -INFINITY) a = fmaf(s_red[ww][r][d], exp2f(mw - M), a);
+      }
+    }
+    const int gr = row0 + r;
+    const int i = gr / p.G;
+    const int64_t orow = (static_cast<int64_t>(b) * p.q_len + i) * p.H + (kvh * p.G + (gr - i * p.G));
+    p.acc[(orow * p.max_parts + part) * D + d] = a;
+  }
+  if (tid < nrows) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kMfmaWaves; ++ww) M = fmaxf(M, s_ml[ww][tid][0]);
+    float L = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int ww = 0; ww < kMfmaWaves; ++ww) {
+        const float mw = s_ml[ww][tid][0];
+        if (mw != -INFINITY) L = fmaf(s_ml[ww][tid][1], exp2f(mw - M), L);
+      }
+    }
+    float* ml = p.ml + (orow_n * p.max_parts + part) * 2;
+    ml[0] = M;
+    ml[1] = L;
+  }
+}
+
+template <typename T, int D, int RT>
+hipError_t launch_decode_mfma_one(const SplitParams& p, hipStream_t stream) {
+  const unsigned gx = static_cast<unsigned>(p.max_parts) * static_cast<unsigned>(p.KVH) *
+                      static_cast<unsigned>(p.rtiles);
+  hipLaunchKernelGGL((decode_mfma_kernel<T, D, RT>), dim3(gx, 1, static_cast<unsigned>(p.batch)),
+                     dim3(kMfmaThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+// Launch for T in {bf16_t, _Float16}; *supported = false when (D, RT) is not compiled.
+template <typename T>
+hipError_t launch_decode_mfma(const SplitParams& p, int D, int RT, hipStream_t stream,
+                              bool* supported);
+
+template <>
+hipError_t launch_decode_mfma<bf16_t>(const SplitParams& p, int D, int RT, hipStream_t stream,
+                                      bool* supported);
+template <>
+hipError_t launch_decode_mfma<_Float16>(const SplitParams& p, int D, int RT, hipStream_t stream,
+                                        bool* supported);
+
+}  // namespace msattn
