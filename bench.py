@@ -214,7 +214,7 @@ def main():
             "algorithmic_bytes_per_layer": per_layer_bytes,
         },
         "roofline": {
-            "kernel": "msattn::split_kernel (partials)",
+            "kernel": "msattn::decode_streamk_kernel (split-K partials)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

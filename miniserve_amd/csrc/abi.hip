@@ -3,7 +3,10 @@
 #include <cmath>
 #include <cstdint>
 
+#include <atomic>
+
 #include "decode_mfma.h"
+#include "decode_streamk.h"
 #include "kernels.h"
 #include "msattn.h"
 
@@ -11,8 +14,16 @@ namespace {
 
 using namespace msattn;
 
-constexpr int kPartitionChoices[] = {512, 256, 128};
-constexpr int64_t kTargetSlots = 1024;  // workgroup slots wanted in a launch
+constexpr int kPartitionChoices[] = {kPartMax, kPartMax / 2, kPartMax / 4};
+#ifndef MSATTN_TARGET_SLOTS
+#define MSATTN_TARGET_SLOTS 1024
+#endif
+constexpr int64_t kTargetSlots = MSATTN_TARGET_SLOTS;  // workgroup slots wanted in a launch
+#ifndef MSATTN_STREAMK_MIN_TILES
+#define MSATTN_STREAMK_MIN_TILES 65536
+#endif
+// Decode launches whose (batch x KV heads x table tiles) reach this use stream-K.
+constexpr int64_t kStreamKMinTiles = MSATTN_STREAMK_MIN_TILES;
 
 bool dtype_ok(int d) { return d >= MSATTN_F32 && d <= MSATTN_FP8_E4M3; }
 int dtype_bytes(int d) { return d == MSATTN_F32 ? 4 : (d == MSATTN_FP8_E4M3 ? 1 : 2); }
@@ -54,7 +65,10 @@ Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, i
                         int max_context) {
   Layout L;
   L.part = choose_partition(batch, q_len, num_heads, num_kv_heads, max_context);
-  L.max_parts = max_context > 0 ? ceil_div(max_context, L.part) : 1;
+  // Slots per row: enough for the partition kernels (one per partition) and for
+  // the stream-K kernel (pieces), plus the end marker.
+  const int by_part = (max_context > 0 ? ceil_div(max_context, L.part) : 1) + 1;
+  L.max_parts = by_part > streamk_slots(max_context) ? by_part : streamk_slots(max_context);
   L.rows = static_cast<int64_t>(batch) * q_len * num_heads;
   const size_t ml = static_cast<size_t>(L.rows) * L.max_parts * 2 * sizeof(float);
   L.ml_bytes = (ml + 255) / 256 * 256;
@@ -63,6 +77,28 @@ Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, i
 }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? MSATTN_OK : MSATTN_ERR_HIP; }
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+int largest_pow2_divisor_upto(int x, int cap) {
+  int u = 1;
+  while (u * 2 <= cap && x % (u * 2) == 0) u *= 2;
+  return u;
+}
 
 hipError_t dispatch_split(const SplitParams& p, int q_dtype, int kv_dtype, int D, int RT,
                           hipStream_t s, bool* sup) {
@@ -173,12 +209,29 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
   p.scale_log2 = scale * kLog2e;
   p.rows_per_kvh = rows;
   p.rtiles = ceil_div(rows, RT);
+  p.sk_group = 1;
+  p.sk_unit_groups = 0;
   const int64_t gx = static_cast<int64_t>(p.max_parts) * num_kv_heads * p.rtiles;
   if (gx >= (int64_t(1) << 31) || batch > 65535) return MSATTN_ERR_UNSUPPORTED;
 
   bool sup = false;
   hipError_t e = hipSuccess;
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  // Decode with enough work to fill the chip: stream-K over every (sequence,
+  // KV head) tile run, one 8-wave workgroup per CU. Small decodes keep the
+  // partition kernel, whose short runs start faster.
+  const int64_t tile_capacity =
+      static_cast<int64_t>(batch) * num_kv_heads * ceil_div(max_context, 16);
+  if (use_mfma && q_len == 1 && batch <= kSkMaxBatch && tile_capacity >= kStreamKMinTiles) {
+    const int units = num_kv_heads * p.rtiles;
+    p.sk_group = largest_pow2_divisor_upto(units, kSkWaves);
+    p.sk_unit_groups = units / p.sk_group;
+    const int grid = device_cus();
+    if (q_dtype == MSATTN_BF16) e = launch_decode_streamk<bf16_t>(p, head_dim, RT, grid, st, &sup);
+    else e = launch_decode_streamk<_Float16>(p, head_dim, RT, grid, st, &sup);
+    if (!sup) return MSATTN_ERR_UNSUPPORTED;
+    return hip_status(e);
+  }
   if (use_mfma && q_dtype == MSATTN_BF16) {
     e = launch_decode_mfma<bf16_t>(p, head_dim, RT, st, &sup);
   } else if (use_mfma) {

@@ -31,6 +31,21 @@
 
 #include "split_kernel.h"
 
+// Tuning knobs (compile-time):
+//   MSATTN_MFMA_WAVES  waves per workgroup;
+//   MSATTN_LOAD_AUX    cache-policy bits of the stream-K kernel's K/V buffer loads
+//                      (2 = nontemporal: the KV stream is read once);
+//   MSATTN_LAZY_RESCALE skip the accumulator rescale when no row's max moved.
+#ifndef MSATTN_MFMA_WAVES
+#define MSATTN_MFMA_WAVES 4
+#endif
+#ifndef MSATTN_LOAD_AUX
+#define MSATTN_LOAD_AUX 2
+#endif
+#ifndef MSATTN_LAZY_RESCALE
+#define MSATTN_LAZY_RESCALE 1
+#endif
+
 namespace msattn {
 
 typedef __bf16 mf_bf16x8 __attribute__((ext_vector_type(8)));
@@ -79,13 +94,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, in
                                            kBufferRsrcWord3);
 }
 
+template <int AUX = 0>
 __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  const mf_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_off), 0, 0);
+  const mf_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_off), 0, AUX);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-constexpr int kMfmaThreads = 256;
-constexpr int kMfmaWaves = kMfmaThreads / kWave;
+constexpr int kMfmaWaves = MSATTN_MFMA_WAVES;
+constexpr int kMfmaThreads = kMfmaWaves * kWave;
 constexpr int kMaxTilesPerWave = kPartMax / 16 / kMfmaWaves;  // partitions are <= kPartMax tokens
 
 // Token (within a 16-token tile) whose score lands in MFMA row i = 4g + r.
@@ -163,6 +179,10 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
       float* ml = p.ml + (orow_n * p.max_parts + part) * 2;
       ml[0] = -INFINITY;
       ml[1] = 0.0f;
+      if (part + 1 == nparts && nparts < p.max_parts) {  // end marker
+        ml[2] = -INFINITY;
+        ml[3] = -1.0f;
+      }
     }
     return;
   }
@@ -270,12 +290,15 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     l_run = fmaf(l_run, alpha, psum);
     m_run = m_new;
 
-    static_for<RT>([&](auto nc) {
-      constexpr int rn = decltype(nc)::value;
-      const float al = row_bcast<rn>(alpha);
+    // alpha is exactly 1 for every row whose running max did not move.
+    if (!MSATTN_LAZY_RESCALE || __any(alpha != 1.0f)) {
+      static_for<RT>([&](auto nc) {
+        constexpr int rn = decltype(nc)::value;
+        const float al = row_bcast<rn>(alpha);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[rn][e] *= al;
-    });
+        for (int e = 0; e < 8; ++e) acc[rn][e] *= al;
+      });
+    }
     // Rows outside the tile's key range (partial tiles) may hold anything, even
     // NaN: their values are replaced by zeros before the weights meet them.
     const bool partial = t0 < a0 || t0 + 16 > a1;
@@ -387,6 +410,10 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     float* ml = p.ml + (orow_n * p.max_parts + part) * 2;
     ml[0] = M;
     ml[1] = L;
+    if (part + 1 == nparts && nparts < p.max_parts) {  // end marker
+      ml[2] = -INFINITY;
+      ml[3] = -1.0f;
+    }
   }
 }
 

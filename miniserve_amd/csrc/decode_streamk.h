@@ -1,0 +1,370 @@
+// Stream-K paged decode (q_len == 1) for gfx950: bf16/fp16 KV, head_dim 64 or 128.
+//
+// Work decomposition. A "unit" is (row tile, KV head): the up-to-16 GQA query
+// rows that read one KV head. Units are grouped UG at a time (UG KV heads side
+// by side); the work of a unit group over sequence b is its T_b 16-token tiles
+// (the tiles of b's key range). Listing every unit group's sequences in order
+// gives `total` slabs. The grid is fixed by the device (one workgroup of
+// kSkWaves waves per CU); the slab list is cut into equal contiguous chunks of
+// c slabs, one per wave sub-group (kSkWaves / UG sub-groups per workgroup),
+// and each of the UG waves of a sub-group walks that chunk for its own KV head.
+// So every wave streams the same amount of KV (no ragged tails), pays its
+// set-up once per run of tiles, and the UG heads of a page are read together.
+//
+// A chunk that crosses sequence boundaries is split into pieces. Piece j of
+// sequence b (counted from the chunk that holds b's first slab) writes its
+// partial (m, l, acc) into workspace slot j of each of its rows; the piece that
+// ends the sequence writes the end marker (m = -inf, l = -1) into the next
+// slot, and merge.hip combines slots up to the marker. Workgroup 0 marks rows
+// whose sequence has no tile (context 0) as empty.
+//
+// The per-tile arithmetic is decode_mfma.h's: MFMA scores, online softmax, P.V
+// with DPP row broadcasts, two tiles' loads in flight through per-tile buffer
+// descriptors. The algorithm is the split decomposition of
+// kernels/paged_attn_triton.py:102-171 with the masking of
+// miniserve/attention.py:135-153 (for q_len == 1: keys in [ctx - window, ctx)).
+#pragma once
+
+#include "decode_mfma.h"
+
+namespace msattn {
+
+constexpr int kSkWaves = 8;
+constexpr int kSkThreads = kSkWaves * kWave;
+constexpr int kSkMaxBatch = 4096;   // sequences per launch on this path
+constexpr int kSkMinChunk = 16;     // tiles: lower bound of a chunk
+constexpr int kSkTableRun = 64;     // tile page ids fetched per table load
+#ifndef MSATTN_SK_UNROLL
+#define MSATTN_SK_UNROLL 2
+#endif
+constexpr int kSkUnroll = MSATTN_SK_UNROLL;  // tiles per loop iteration (even)
+
+// Slots a row needs at most when chunks are >= kSkMinChunk tiles: pieces plus
+// the end marker.
+__host__ __device__ constexpr int streamk_slots(int max_ctx) {
+  return (max_ctx + 15) / 16 / kSkMinChunk + 3;
+}
+
+template <typename T, int D, int RT>
+__global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitParams p) {
+  static_assert(D == 64 || D == 128, "stream-K decode handles head_dim 64 and 128");
+  constexpr int JD = D / 32;
+  constexpr int LPR = D / 8;
+  constexpr int TPI = 64 / LPR;
+  constexpr int NJ = 16 / TPI;
+  constexpr int APR = 16 / LPR;
+  constexpr int EB = static_cast<int>(sizeof(T));
+
+  __shared__ int s_pre[kSkMaxBatch + 1];  // exclusive prefix of T_b
+  __shared__ int s_wsum[kSkWaves];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int va = lane / LPR;
+  const int vc = lane % LPR;
+  const int B = p.batch;
+
+  // ---- tiles per sequence and their exclusive prefix sum (block scan) ----
+  constexpr int kPer = (kSkMaxBatch + kSkThreads - 1) / kSkThreads;
+  int tb[kPer];
+  int my_sum = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int b = tid * kPer + k;
+    int t = 0;
+    if (b < B) {
+      int ctx = p.lens[b];
+      ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
+      const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
+      t = ctx > lo ? ceil_div(ctx, 16) - lo / 16 : 0;
+    }
+    tb[k] = t;
+    my_sum += t;
+  }
+  int incl = my_sum;  // inclusive scan over the wave
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  if (lane == kWave - 1) s_wsum[w] = incl;
+  __syncthreads();
+  int wave_off = 0;
+  int sumT = 0;
+#pragma unroll
+  for (int i = 0; i < kSkWaves; ++i) {
+    const int v = s_wsum[i];
+    if (i < w) wave_off += v;
+    sumT += v;
+  }
+  {
+    int run = wave_off + incl - my_sum;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int b = tid * kPer + k;
+      if (b < B) s_pre[b] = run;
+      run += tb[k];
+    }
+    if (tid == 0) s_pre[B] = sumT;
+  }
+  __syncthreads();
+
+  // Rows of sequences without any tile: end marker in slot 0.
+  if (blockIdx.x == 0) {
+    for (int idx = tid; idx < B * p.H; idx += kSkThreads) {
+      const int b = idx / p.H;
+      if (s_pre[b + 1] == s_pre[b]) {
+        float* ml = p.ml + static_cast<int64_t>(idx) * p.max_parts * 2;
+        ml[0] = -INFINITY;
+        ml[1] = -1.0f;
+      }
+    }
+  }
+  if (sumT == 0) return;
+
+  // ---- chunking ----
+  const int UG = p.sk_group;                 // KV heads per unit group (divides kSkWaves)
+  const int SG = kSkWaves / UG;              // sub-groups per workgroup
+  const int64_t total = static_cast<int64_t>(p.sk_unit_groups) * sumT;
+  const int64_t nsub = static_cast<int64_t>(gridDim.x) * SG;
+  const int64_t c = max(static_cast<int64_t>(kSkMinChunk), (total + nsub - 1) / nsub);
+  const int sg = w / UG;
+  const int ul = w - sg * UG;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * SG + sg;
+  int64_t s = r * c;
+  const int64_t s_end = min(s + c, total);
+
+  const T* kbase = static_cast<const T*>(p.k);
+  const T* vbase = static_cast<const T*>(p.v);
+  const uint32_t k_lane_tok = static_cast<uint32_t>(tile_token<D>(n));
+  const int tile_bytes = static_cast<int>((15 * p.slot_stride + D) * EB);
+
+  while (s < s_end) {
+    // Locate the piece: unit group ug, sequence b (largest b with s_pre[b] <= o).
+    const int ug = static_cast<int>(s / sumT);
+    const int o = static_cast<int>(s - static_cast<int64_t>(ug) * sumT);
+    int lo_b = 0, hi_b = B;  // s_pre[lo_b] <= o < s_pre[hi_b]
+    while (hi_b - lo_b > 1) {
+      const int mid = (lo_b + hi_b) >> 1;
+      if (s_pre[mid] <= o) lo_b = mid; else hi_b = mid;
+    }
+    const int b = lo_b;
+    const int64_t seg_start = static_cast<int64_t>(ug) * sumT + s_pre[b];
+    const int64_t seg_end = static_cast<int64_t>(ug) * sumT + s_pre[b + 1];
+    const int64_t pe = min(s_end, seg_end);
+    const int piece = static_cast<int>(r - seg_start / c);
+    const bool last = pe == seg_end;
+
+    const int unit = ug * UG + ul;          // unit = rtile * KVH + kvh
+    const int kvh = unit % p.KVH;
+    const int rtile = unit / p.KVH;
+    int ctx = p.lens[b];
+    ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
+    const int lo_key = p.window > 0 ? max(0, ctx - p.window) : 0;
+    const int t_first = lo_key / 16 + static_cast<int>(s - seg_start);
+    const int ntiles = static_cast<int>(pe - s);
+    const int a0 = max(lo_key, t_first * 16);
+    const int a1 = min(ctx, (t_first + ntiles) * 16);
+
+    // Rows of this unit: query row n of the tile is head kvh * G + rtile * RT + n.
+    const int row0 = rtile * RT;
+    const int nrows = min(RT, p.G - row0);
+    int64_t orow_n = 0;
+    if (n < nrows) orow_n = static_cast<int64_t>(b) * p.H + kvh * p.G + row0 + n;
+    uint4 qb[JD];
+    {
+      const T* qp = static_cast<const T*>(p.q);
+#pragma unroll
+      for (int j = 0; j < JD; ++j) {
+        qb[j] = make_uint4(0u, 0u, 0u, 0u);
+        if (n < nrows) qb[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + (4 * j + g) * 8);
+      }
+    }
+
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+    float acc[RT][8];
+#pragma unroll
+    for (int rr = 0; rr < RT; ++rr)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[rr][e] = 0.0f;
+
+    for (int run0 = 0; run0 < ntiles; run0 += kSkTableRun) {
+      const int nt = min(kSkTableRun, ntiles - run0);
+      // lane k: element offset of tile t_first + run0 + k, or -1 for a hole / k >= nt
+      int64_t my_base = -1;
+      if (lane < nt) {
+        const int t = t_first + run0 + lane;
+        const int pg = (t * 16) / p.bs;
+        const int slot0 = t * 16 - pg * p.bs;
+        if (pg < p.W) {
+          const int phys = p.table[static_cast<int64_t>(b) * p.W + pg];
+          if (phys >= 0 && phys < p.num_blocks)
+            my_base = static_cast<int64_t>(phys) * p.blk_stride +
+                      static_cast<int64_t>(slot0) * p.slot_stride +
+                      static_cast<int64_t>(kvh) * p.head_stride;
+        }
+      }
+      auto tile_base = [&](int k) -> int64_t {
+        if (k >= nt) return -1;
+        const uint32_t lo = static_cast<uint32_t>(
+            __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(my_base)), k));
+        const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
+        return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
+      };
+      auto issue = [&](int64_t base, uint4 (&kb)[JD], uint4 (&vb)[NJ]) {
+        const bool ok = base >= 0;
+        const int64_t b0 = ok ? base : 0;
+        const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
+        const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
+        const uint32_t koff = (k_lane_tok * static_cast<uint32_t>(p.slot_stride) + g * 8) * EB;
+#pragma unroll
+        for (int j = 0; j < JD; ++j) kb[j] = buffer_load16<MSATTN_LOAD_AUX>(rk, koff + 64 * j);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          vb[j] = buffer_load16<MSATTN_LOAD_AUX>(
+              rv, ((static_cast<uint32_t>(TPI * j + va) * static_cast<uint32_t>(p.slot_stride)) +
+                   vc * 8) * EB);
+      };
+      auto consume = [&](int k, const uint4 (&kb)[JD], const uint4 (&vb)[NJ], int64_t base) {
+        mf_f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < JD; ++j) sv = Mfma16<T>::mac(kb[j], qb[j], sv);
+        const int t0 = (t_first + run0 + k) * 16;
+        const bool hole = base < 0;
+        float sc[4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int tok = t0 + tile_token<D>(4 * g + q);
+          const bool ok = !hole && n < nrows && tok >= a0 && tok < a1;
+          sc[q] = ok ? sv[q] * p.scale_log2 : -INFINITY;
+          mt = fmaxf(mt, sc[q]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+        const float m_new = fmaxf(m_run, mt);
+        const bool live = m_new != -INFINITY;
+        const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        float pr[4];
+        float psum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          pr[q] = live ? __builtin_amdgcn_exp2f(sc[q] - m_new) : 0.0f;
+          psum += pr[q];
+        }
+        l_run = fmaf(l_run, alpha, psum);
+        m_run = m_new;
+        if (!MSATTN_LAZY_RESCALE || __any(alpha != 1.0f)) {
+          static_for<RT>([&](auto nc) {
+            constexpr int rn = decltype(nc)::value;
+            const float al = row_bcast<rn>(alpha);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[rn][e] *= al;
+          });
+        }
+        const bool partial = hole || t0 < a0 || t0 + 16 > a1;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          float vf[8];
+          uint4 vv = vb[j];
+          if (partial) {
+            const int vtok = t0 + TPI * j + va;
+            const bool keep = !hole && vtok >= a0 && vtok < a1;
+            vv.x = keep ? vv.x : 0u;
+            vv.y = keep ? vv.y : 0u;
+            vv.z = keep ? vv.z : 0u;
+            vv.w = keep ? vv.w : 0u;
+          }
+          Chunk<T>::unpack(vv, vf);
+          static_for<RT>([&](auto nc) {
+            constexpr int rn = decltype(nc)::value;
+            float pb;
+            if constexpr (APR == 1) {
+              pb = row_bcast<rn>(pr[j]);
+            } else {
+              const float b0 = row_bcast<rn>(pr[APR * j]);
+              const float b1 = row_bcast<rn>(pr[APR * j + 1]);
+              pb = (va & 1) ? b1 : b0;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[rn][e] = fmaf(pb, vf[e], acc[rn][e]);
+          });
+        }
+      };
+
+      // Tiles in groups of kSkUnroll, two in flight; a tile index >= nt reads nothing
+      // and adds nothing (its descriptor has no records, all its keys are masked).
+      uint4 k0[JD], v0[NJ], k1[JD], v1[NJ];
+      int64_t base0 = tile_base(0);
+      issue(base0, k0, v0);
+      for (int k = 0; k < nt; k += kSkUnroll) {
+#pragma unroll
+        for (int kk = 0; kk < kSkUnroll; kk += 2) {
+          const int64_t base1 = tile_base(k + kk + 1);
+          issue(base1, k1, v1);
+          consume(k + kk, k0, v0, base0);
+          base0 = tile_base(k + kk + 2);
+          issue(base0, k0, v0);
+          consume(k + kk + 1, k1, v1, base1);
+        }
+      }
+    }
+
+    // ---- wave totals and the piece's partial ----
+    l_run += __shfl_xor(l_run, 16, kWave);
+    l_run += __shfl_xor(l_run, 32, kWave);
+#pragma unroll
+    for (int rr = 0; rr < RT; ++rr)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = acc[rr][e];
+#pragma unroll
+        for (int oo = LPR; oo < kWave; oo <<= 1) a += __shfl_xor(a, oo, kWave);
+        acc[rr][e] = a;
+      }
+    if (va == 0 && piece < p.max_parts) {
+#pragma unroll
+      for (int rr = 0; rr < RT; ++rr) {
+        if (rr < nrows) {
+          const int64_t orow = static_cast<int64_t>(b) * p.H + kvh * p.G + row0 + rr;
+          float* dst = p.acc + (orow * p.max_parts + piece) * D + vc * 8;
+          *reinterpret_cast<float4*>(dst) = make_float4(acc[rr][0], acc[rr][1], acc[rr][2], acc[rr][3]);
+          *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[rr][4], acc[rr][5], acc[rr][6], acc[rr][7]);
+        }
+      }
+    }
+    if (lane < nrows && piece < p.max_parts) {
+      float* ml = p.ml + (orow_n * p.max_parts + piece) * 2;
+      ml[0] = m_run;
+      ml[1] = l_run;
+      if (last && piece + 1 < p.max_parts) {
+        ml[2] = -INFINITY;
+        ml[3] = -1.0f;
+      }
+    }
+    s = pe;
+  }
+}
+
+template <typename T, int D, int RT>
+hipError_t launch_decode_streamk_one(const SplitParams& p, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_streamk_kernel<T, D, RT>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kSkThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_decode_streamk(const SplitParams& p, int D, int RT, int grid, hipStream_t stream,
+                                 bool* supported);
+template <>
+hipError_t launch_decode_streamk<bf16_t>(const SplitParams& p, int D, int RT, int grid,
+                                         hipStream_t stream, bool* supported);
+template <>
+hipError_t launch_decode_streamk<_Float16>(const SplitParams& p, int D, int RT, int grid,
+                                           hipStream_t stream, bool* supported);
+
+}  // namespace msattn

@@ -5,11 +5,13 @@
 // partition). A row tile packs up to RT query rows that read the same KV head:
 // the `group` GQA heads of that KV head, times the q_len query tokens. The
 // workgroup walks the partition's tokens through the block table and writes a
-// partial (m, l, acc) per row:
+// partial (m, l, acc) per row into workspace slot `part`:
 //   m   = max_k  s_k              with s_k = scale * log2(e) * q . K[k]
 //   l   = sum_k  2^(s_k - m)
 //   acc = sum_k  2^(s_k - m) V[k]
-// over the row's unmasked keys in the partition. merge.hip combines them.
+// over the row's unmasked keys in the partition. The slot after a row's last
+// partition gets the end marker (m = -inf, l = -1) unless it is past the
+// workspace. merge.hip combines a row's slots up to that marker.
 //
 // Phases (barriers between them):
 //   0  page-table walk: one byte offset per token of the partition into LDS
@@ -34,7 +36,11 @@ namespace msattn {
 
 constexpr int kSplitThreads = 256;
 constexpr int kSplitWaves = kSplitThreads / kWave;
-constexpr int kPartMax = 512;
+// Largest context partition (tokens) one workgroup covers.
+#ifndef MSATTN_PART_MAX
+#define MSATTN_PART_MAX 512
+#endif
+constexpr int kPartMax = MSATTN_PART_MAX;
 
 struct SplitParams {
   const void* q;
@@ -52,6 +58,8 @@ struct SplitParams {
   float scale_log2;
   int rows_per_kvh;  // q_len * G
   int rtiles;        // ceil(rows_per_kvh / RT)
+  int sk_group;        // stream-K: KV-head units per unit group
+  int sk_unit_groups;  // stream-K: number of unit groups
 };
 
 template <typename QT, typename KT, int D, int RT>
@@ -130,6 +138,10 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
         float* ml = p.ml + (orow[r] * p.max_parts + part) * 2;
         ml[0] = -INFINITY;
         ml[1] = 0.0f;
+        if (part + 1 == nparts && nparts < p.max_parts) {  // end marker
+          ml[2] = -INFINITY;
+          ml[3] = -1.0f;
+        }
       }
     }
     return;
@@ -307,6 +319,10 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
       float* ml = p.ml + (orow[r] * p.max_parts + part) * 2;
       ml[0] = s_m[r];
       ml[1] = s_l[r];
+      if (part + 1 == nparts && nparts < p.max_parts) {  // end marker
+        ml[2] = -INFINITY;
+        ml[3] = -1.0f;
+      }
     }
   }
 }

@@ -44,10 +44,11 @@ def test_abi_version_and_status_strings():
 def test_partition_policy(B, q_len, H, KVH, D, ctx, part):
     lib = nat.lib()
     assert lib.msattn_partition_tokens(B, q_len, H, KVH, D, ctx) == part
-    parts = -(-ctx // part)
-    ml = B * q_len * H * parts * 2 * 4
+    # slots per row: one per partition or stream-K piece, plus the end marker
+    slots = max(-(-ctx // part) + 1, -(-ctx // 16) // 16 + 3)
+    ml = B * q_len * H * slots * 2 * 4
     ml = -(-ml // 256) * 256
-    assert lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) == ml + B * q_len * H * parts * D * 4
+    assert lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) == ml + B * q_len * H * slots * D * 4
 
 
 def test_workspace_rejects_bad_geometry():

@@ -270,6 +270,89 @@ def test_deterministic(device):
     assert torch.equal(a, b)
 
 
+# ------------------------------------------------------------------ stream-K decode path
+
+def wide_table_case(H, KVH, D, lens, dtype, width_pages, seed):
+    """Scattered pages for `lens` inside a block table `width_pages` wide: a wide table
+    (large capacity) routes bf16/fp16 decode to the stream-K kernel."""
+    g = torch.Generator().manual_seed(seed)
+    need = sum((L + 15) // 16 for L in lens)
+    pool = max(need, 1) + 7
+    q = torch.randn(len(lens), 1, H, D, generator=g).to(dtype)
+    kc = torch.randn(pool, 16, KVH, D, generator=g).to(dtype)
+    vc = torch.randn(pool, 16, KVH, D, generator=g).to(dtype)
+    perm = torch.randperm(pool, generator=g)
+    table = torch.zeros(len(lens), width_pages, dtype=torch.long)
+    cur = 0
+    for b, L in enumerate(lens):
+        n = (L + 15) // 16
+        table[b, :n] = perm[cur:cur + n]
+        cur += n
+    return q, kc, vc, table
+
+
+@pytest.mark.parametrize("H,KVH,D,dtype,window", [
+    (14, 2, 64, torch.bfloat16, None),     # Qwen2.5-0.5B geometry, G = 7
+    (28, 4, 128, torch.bfloat16, None),    # Qwen2.5-7B geometry, G = 7
+    (32, 8, 128, torch.float16, None),     # Llama-3-8B geometry in fp16
+    (32, 8, 128, torch.bfloat16, 100),     # windowed decode
+    (8, 8, 64, torch.bfloat16, None),      # MHA, G = 1
+    (32, 1, 128, torch.bfloat16, None),    # MQA, G = 32: two row tiles per KV head
+])
+def test_streamk_decode(device, H, KVH, D, dtype, window):
+    lens = [0, 1, 16, 17, 300, 1234, 77, 4096, 5, 2048, 999, 33]
+    width = 65536 // (len(lens) * KVH) + 1  # capacity past the stream-K threshold
+    note(f"stream-K H={H} KVH={KVH} D={D} {dtype} window={window}")
+    q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=H + D)
+    out = run_hip(device, q, kc, vc, table, lens, window=window, max_context=width * 16)
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens, window=window)
+    err = rel_err(out, ref)
+    note(f"stream-K max-rel {err:.3e}")
+    assert err < BF16_REL
+    assert not out[0].any()  # context 0 -> zeros
+    for h in range(H):      # context 1 -> V[0] of the row's KV head (rounded to dtype)
+        assert torch.equal(out[1, 0, h].cpu(), vc[table[1, 0], 0, h // (H // KVH)])
+
+
+def test_streamk_graph_replays(device):
+    """Stream-K decode captured in a graph: replays with new lengths match eager bit-exactly."""
+    note("stream-K graph")
+    H, KVH, D = 32, 8, 128
+    lens = [3000, 17, 5000, 0, 800, 4096, 1, 2500]
+    width = 1024
+    q, kc, vc, table = wide_table_case(H, KVH, D, [width * 16] * len(lens), torch.bfloat16,
+                                       width, seed=5)
+    kc, vc = kc.to(device), vc.to(device)
+    sq = q.to(device)
+    stable = table.to(device=device, dtype=torch.int32)
+    slens = torch.tensor(lens, dtype=torch.int32, device=device)
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+    out = torch.empty_like(sq)
+    cap = width * 16
+
+    def step():
+        paged_attention(sq, kc, vc, stable, slens, max_context=cap, workspace=ws, out=out)
+
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream(device).wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    g = torch.Generator().manual_seed(6)
+    for rep in range(4):
+        new = [int(x) for x in torch.randint(0, cap + 1, (len(lens),), generator=g)]
+        slens.copy_(torch.tensor(new, dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = paged_attention(sq, kc, vc, stable, new, max_context=cap)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay {rep}"
+
+
 # ------------------------------------------------------------------ benchmark configs
 
 @pytest.fixture(scope="module")
@@ -311,16 +394,20 @@ def test_c3_bf16(device, c3):
     check_workload(device, c3)
 
 
-def test_c3_batch_permutation_bit_exact(device, c3):
+def test_c3_batch_permutation(device, c3):
     """Size-independent property at full C3 size: a row's result depends only on its own
-    query, table and length, so permuting the batch permutes the output bit-exactly
-    (same batch size, hence the same partitioning)."""
+    query, table and length. Permuting the batch permutes the output up to summation
+    order (the work split follows the batch order): within 2 bf16 ulps of the row's
+    magnitude, and both results within the oracle bar."""
     kc, vc = c3.k_caches[0].to(device), c3.v_caches[0].to(device)
     full = paged_attention(c3.query.to(device), kc, vc, c3.table, c3.lens)
     perm = torch.randperm(c3.batch, generator=torch.Generator().manual_seed(3))
     permuted = paged_attention(c3.query[perm].to(device), kc, vc, c3.table[perm],
                                [c3.lens[i] for i in perm.tolist()])
-    assert torch.equal(full[perm.to(device)], permuted)
+    a = full[perm.to(device)].float()
+    b = permuted.float()
+    scale = a.abs().amax(dim=-1, keepdim=True).clamp_min(1e-30)
+    assert ((a - b).abs() / scale).max().item() <= 2 * 2.0 ** -8
 
 
 def test_c4_long_context_rows(device):
