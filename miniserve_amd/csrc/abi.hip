@@ -7,6 +7,7 @@
 
 #include "decode_mfma.h"
 #include "decode_streamk.h"
+#include "prefill_mfma.h"
 #include "kernels.h"
 #include "msattn.h"
 
@@ -282,6 +283,55 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
                            float scale, int q_dtype, int kv_dtype, void* stream) {
   if (!out) return MSATTN_ERR_INVALID_ARG;
   if (!aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
+  // Chunked prefill (more than one 16-row tile of query rows per KV head): the MFMA
+  // prefill kernel writes the normalised output directly.
+  if (q_len > 1 && q_dtype == kv_dtype && (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
+      head_dim == 128 && block_size % 16 == 0 && batch <= 65535 && num_heads > 0 &&
+      num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
+      static_cast<int64_t>(q_len) * (num_heads / num_kv_heads) > 16) {
+    if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
+    if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
+      return MSATTN_ERR_INVALID_ARG;
+    if (!std::isfinite(scale)) return MSATTN_ERR_INVALID_ARG;
+    const int rc = check_cache_args(k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                                    cache_head_stride, kv_dtype, block_size, num_blocks,
+                                    table_width);
+    if (rc != MSATTN_OK) return rc;
+    if (!aligned(query, 16)) return MSATTN_ERR_INVALID_ARG;
+    const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
+    if (workspace_bytes < L.ml_bytes + L.acc_bytes) return MSATTN_ERR_WORKSPACE;
+    PrefillParams pp;
+    pp.q = query;
+    pp.k = k_cache;
+    pp.v = v_cache;
+    pp.table = block_table;
+    pp.lens = context_lens;
+    pp.out = out;
+    pp.blk_stride = cache_block_stride;
+    pp.slot_stride = cache_slot_stride;
+    pp.head_stride = cache_head_stride;
+    pp.batch = batch;
+    pp.q_len = q_len;
+    pp.H = num_heads;
+    pp.KVH = num_kv_heads;
+    pp.G = num_heads / num_kv_heads;
+    pp.bs = block_size;
+    pp.num_blocks = num_blocks;
+    pp.W = table_width;
+    pp.max_ctx = max_context;
+    pp.causal = causal ? 1 : 0;
+    pp.window = window > 0 ? window : 0;
+    pp.scale_log2 = scale * kLog2e;
+    pp.rows_per_kvh = q_len * pp.G;
+    pp.rblocks = ceil_div(pp.rows_per_kvh, kPfRows);
+    if (static_cast<int64_t>(pp.rblocks) * num_kv_heads >= (int64_t(1) << 31)) return MSATTN_ERR_UNSUPPORTED;
+    bool sup = false;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const hipError_t e = q_dtype == MSATTN_BF16 ? launch_prefill_mfma<bf16_t>(pp, head_dim, st, &sup)
+                                                : launch_prefill_mfma<_Float16>(pp, head_dim, st, &sup);
+    if (!sup) return MSATTN_ERR_UNSUPPORTED;
+    return hip_status(e);
+  }
   const int rc = msattn_paged_attention_partials(
       query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
       block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,

@@ -353,6 +353,35 @@ def test_streamk_graph_replays(device):
         assert torch.equal(replayed, eager), f"replay {rep}"
 
 
+# ------------------------------------------------------------------ chunked prefill (MFMA)
+
+@pytest.mark.parametrize("H,KVH,q_len,lens,dtype,causal,window", [
+    (28, 4, 512, [4608, 4608], torch.bfloat16, True, None),   # C5 prefill shape
+    (28, 4, 100, [100, 1000, 357], torch.bfloat16, True, None),
+    (32, 8, 17, [17, 40, 3000], torch.bfloat16, True, None),
+    (32, 8, 64, [64, 700], torch.float16, True, None),
+    (8, 8, 33, [33, 90], torch.bfloat16, False, None),        # non-causal
+    (28, 4, 200, [1200, 300], torch.bfloat16, True, 128),     # sliding window
+    (16, 2, 80, [50, 2000], torch.bfloat16, True, None),      # context shorter than the chunk
+])
+def test_prefill_mfma(device, H, KVH, q_len, lens, dtype, causal, window):
+    note(f"prefill H={H} KVH={KVH} q_len={q_len} lens={lens} {dtype} causal={causal} window={window}")
+    D = 128
+    g = torch.Generator().manual_seed(q_len + H)
+    width = max((L + 15) // 16 for L in lens) + 3
+    q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=q_len)
+    q = torch.randn(len(lens), q_len, H, D, generator=g).to(dtype)
+    out = run_hip(device, q, kc, vc, table, lens, causal=causal, window=window)
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens, causal=causal, window=window)
+    err = rel_err(out, ref)
+    note(f"prefill max-rel {err:.3e}")
+    assert err < BF16_REL
+    # rows whose key set is empty are zeros (first rows when the context is shorter)
+    for b, L in enumerate(lens):
+        if causal and L < q_len:
+            assert not out[b, : q_len - L].any()
+
+
 # ------------------------------------------------------------------ benchmark configs
 
 @pytest.fixture(scope="module")
