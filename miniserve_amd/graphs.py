@@ -1,0 +1,181 @@
+"""Bucketed hipGraph decode over the paged-attention path.
+
+Restates GraphedDecodeRunner (miniserve/model_runner.py:224-336) for the attention
+path alone. A decode step over L layers is, per layer:
+    write_kv(new k, v at position ctx[b])    (miniserve/attention.py:111-133)
+    forward(q, caches, table, ctx + 1)       (miniserve/attention.py:205-250)
+captured once per (bucket, input set) as a hipGraph through torch.cuda.CUDAGraph.
+Batches that are not a bucket size replay the next larger bucket with pad rows.
+
+Kept from the reference: sorted buckets starting at 1 (ValueError otherwise), two
+alternating static input sets (double buffering) with a `replay_log`, a shared graph
+memory pool, static buffers sized for the largest bucket, `memory_report()`.
+
+Differences, deliberate:
+  * buckets go up to 64 by default (the bs-64 decode configuration);
+  * every input the step reads lives in device buffers (int32 block tables, context
+    lengths, write positions): the captured step never reads the host, which the
+    reference's `.tolist()` and `int(...)` reads (model_runner.py:273,
+    attention.py:131, :236) would;
+  * pad rows (table -1, ctx 0) are true no-ops: write_kv skips hole pages and a
+    row with no key gets zeros, where the reference's pad rows write into and read
+    from the cache's last page.
+"""
+from __future__ import annotations
+
+from typing import List, Sequence
+
+import torch
+
+from . import _native as nat
+from .attention import PagedAttention, paged_attention
+
+
+class DecodeLayer:
+    """One layer's paged-attention state: the reference's _LayerState
+    (miniserve/model_runner.py:88-95) without a block table of its own."""
+
+    __slots__ = ("pa", "k_cache", "v_cache")
+
+    def __init__(self, pa: PagedAttention, k_cache: torch.Tensor, v_cache: torch.Tensor):
+        self.pa, self.k_cache, self.v_cache = pa, k_cache, v_cache
+
+
+class GraphedDecodeRunner:
+    """Bucketed hipGraph decode: one graph per bucket and input set, shared pool."""
+
+    def __init__(self, layers: Sequence[DecodeLayer], table_width: int,
+                 buckets: Sequence[int] = (1, 2, 4, 8, 16, 32, 64),
+                 dtype: torch.dtype | None = None) -> None:
+        buckets = list(buckets)
+        if not buckets or sorted(buckets) != buckets or buckets[0] < 1:
+            raise ValueError("buckets must be sorted, start at 1")
+        if not layers:
+            raise ValueError("at least one layer is needed")
+        self.layers = list(layers)
+        self.buckets = tuple(buckets)
+        self.max_batch = self.buckets[-1]
+        self.table_width = int(table_width)
+        self.replay_log: List[tuple[int, int]] = []
+        self._buf_idx = 0
+        self._graphs: dict[int, list] = {}
+        self._pool = None
+        pa0 = self.layers[0].pa
+        kc0 = self.layers[0].k_cache
+        if kc0.device.type != "cuda":
+            raise RuntimeError("GraphedDecodeRunner needs caches on a ROCm GPU device")
+        self._device = kc0.device
+        self.block_size = kc0.shape[1]
+        self.num_heads = pa0.num_heads
+        self.num_kv_heads = kc0.shape[2]
+        self.head_dim = kc0.shape[3]
+        self.dtype = dtype or pa0.dtype
+        L, Bm, H, KVH, D = (len(self.layers), self.max_batch, self.num_heads,
+                            self.num_kv_heads, self.head_dim)
+        dev = self._device
+
+        def input_set():
+            return {
+                "q": torch.zeros((L, Bm, 1, H, D), dtype=self.dtype, device=dev),
+                "k": torch.zeros((L, Bm, 1, KVH, D), dtype=self.dtype, device=dev),
+                "v": torch.zeros((L, Bm, 1, KVH, D), dtype=self.dtype, device=dev),
+                "table": torch.full((Bm, self.table_width), -1, dtype=torch.int32, device=dev),
+                "start": torch.zeros((Bm,), dtype=torch.int32, device=dev),
+                "lens": torch.zeros((Bm,), dtype=torch.int32, device=dev),
+            }
+
+        self._in = [input_set() for _ in range(2)]
+        self._out = torch.zeros((L, Bm, 1, H, D), dtype=self.dtype, device=dev)
+        self.max_context = self.table_width * self.block_size
+        ws_bytes = max(nat.lib().msattn_workspace_bytes(b, 1, H, KVH, D, self.max_context)
+                       for b in self.buckets)
+        self._ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+
+    # ---------------------------------------------------------------- step
+    def _run_static(self, buf: dict, bucket: int) -> None:
+        """One decode step over every layer, on static buffers only (captured)."""
+        table = buf["table"][:bucket]
+        start = buf["start"][:bucket]
+        lens = buf["lens"][:bucket]
+        for li, layer in enumerate(self.layers):
+            layer.pa.write_kv(layer.k_cache, layer.v_cache, buf["k"][li, :bucket],
+                              buf["v"][li, :bucket], table, start=start)
+            paged_attention(buf["q"][li, :bucket], layer.k_cache, layer.v_cache, table, lens,
+                            window=layer.pa.window, max_context=self.max_context,
+                            workspace=self._ws, out=self._out[li, :bucket])
+
+    def _bucket_fn(self, bucket: int, set_idx: int):
+        """Capture the step for (bucket, input set); returns its replay callable."""
+        dev = self._device
+        buf = self._in[set_idx]
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):  # warm-up outside capture
+            self._run_static(buf, bucket)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        self._pool = self._pool or torch.cuda.graph_pool_handle()
+        with torch.cuda.graph(graph, pool=self._pool):
+            self._run_static(buf, bucket)
+        return graph.replay
+
+    # ---------------------------------------------------------------- API
+    def decode(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+               tables: Sequence[Sequence[int]], ctx: Sequence[int],
+               use_graph: bool = True) -> torch.Tensor:
+        """One decode step for len(ctx) real rows.
+
+        q [L, B, 1, H, D], k/v [L, B, 1, KVH, D]: the new token of every row and layer;
+        tables: page ids per row; ctx: tokens already cached per row. Row b's new k/v
+        land at position ctx[b] and it attends over ctx[b] + 1 tokens. Returns the
+        attention output [L, B, 1, H, D]. Pad rows are padded to the bucket with
+        table -1 and ctx 0 and produce nothing.
+        """
+        B = len(ctx)
+        if B > self.max_batch:
+            raise ValueError(f"batch {B} > max bucket {self.max_batch}")
+        if B == 0:
+            raise ValueError("empty batch")
+        bucket = next(b for b in self.buckets if b >= B)
+        if use_graph and bucket not in self._graphs:  # capture both sets lazily
+            self._graphs[bucket] = [self._bucket_fn(bucket, i) for i in range(2)]
+        idx = self._buf_idx
+        self._buf_idx = 1 - self._buf_idx
+        buf = self._in[idx]
+        buf["q"][:, :B].copy_(q)
+        buf["k"][:, :B].copy_(k)
+        buf["v"][:, :B].copy_(v)
+        host_table = torch.full((self.max_batch, self.table_width), -1, dtype=torch.int32)
+        for b, row in enumerate(tables):
+            row = list(row)
+            if len(row) > self.table_width:
+                raise ValueError(f"row {b}: {len(row)} pages > table width {self.table_width}")
+            host_table[b, : len(row)] = torch.tensor(row, dtype=torch.int32)
+        start = torch.zeros(self.max_batch, dtype=torch.int32)
+        start[:B] = torch.tensor([int(c) for c in ctx], dtype=torch.int32)
+        lens = torch.zeros(self.max_batch, dtype=torch.int32)
+        lens[:B] = start[:B] + 1
+        if int(lens.max()) > self.max_context:
+            raise ValueError(f"context {int(lens.max())} > table capacity {self.max_context}")
+        buf["table"].copy_(host_table)
+        buf["start"].copy_(start)
+        buf["lens"].copy_(lens)
+        if use_graph:
+            self._graphs[bucket][idx]()
+        else:
+            self._run_static(buf, bucket)  # eager reference on the same buffers
+        self.replay_log.append((len(self.replay_log), idx))
+        return self._out[:, :B].clone()
+
+    def memory_report(self) -> dict:
+        """Static footprint: inputs are max-bucket-sized and shared by every bucket's
+        graphs, so the total tracks the largest bucket, not the number of buckets."""
+        nb = lambda t: t.element_size() * t.numel()
+        per_set = sum(nb(t) for t in self._in[0].values())
+        out_b = nb(self._out) + nb(self._ws)
+        max_fp = per_set + out_b
+        total = 2 * per_set + out_b
+        return {"per_input_set_bytes": per_set, "output_bytes": out_b,
+                "max_bucket_footprint_bytes": max_fp, "total_static_bytes": total,
+                "total_over_max": total / max_fp, "buckets_captured": sorted(self._graphs),
+                "shared_pool": self._pool is not None}

@@ -81,3 +81,12 @@ def test_cpu_tensors_fail_loudly():
     with pytest.raises(RuntimeError, match="GPU"):
         pa.write_kv(kc, vc, torch.zeros(1, 1, 2, 16), torch.zeros(1, 1, 2, 16),
                     torch.zeros(1, 1, dtype=torch.long))
+
+
+def test_graph_runner_bucket_contract():
+    """miniserve/model_runner.py:243-244: buckets must be sorted and start at 1."""
+    from miniserve_amd.graphs import GraphedDecodeRunner
+    with pytest.raises(ValueError, match="sorted, start at 1"):
+        GraphedDecodeRunner([object()], table_width=4, buckets=(4, 2))
+    with pytest.raises(ValueError, match="sorted, start at 1"):
+        GraphedDecodeRunner([object()], table_width=4, buckets=(0, 2))
