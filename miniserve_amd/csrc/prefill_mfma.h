@@ -49,17 +49,23 @@ struct PrefillParams {
   int rblocks;       // ceil(rows_per_kvh / kPfRows)
 };
 
+typedef float pf_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 pf_bf2 __attribute__((ext_vector_type(2)));
+typedef _Float16 pf_h2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> one packed 16-bit pair (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32,
+// round to nearest even).
 template <typename T> struct Pack2;
 template <> struct Pack2<bf16_t> {
   __device__ static uint32_t pack(float a, float b) {
-    return static_cast<uint32_t>(f32_to_bf16_bits(a)) | (static_cast<uint32_t>(f32_to_bf16_bits(b)) << 16);
+    const pf_f2 x = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, pf_bf2));
   }
 };
 template <> struct Pack2<_Float16> {
   __device__ static uint32_t pack(float a, float b) {
-    const _Float16 x = static_cast<_Float16>(a), y = static_cast<_Float16>(b);
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, x)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, y)) << 16);
+    const pf_f2 x = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, pf_h2));
   }
 };
 
@@ -113,6 +119,18 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     if (hi_n < lo_n) hi_n = lo_n;
     orow = (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
   }
+  // Keys every row of this wave sees: [wave_lo, wave_hi) (rows grow with the query).
+  int wave_lo = 0, wave_hi = 0;
+  {
+    const int wr0 = row0 + w * 16;
+    const int wr1 = min(wr0 + 16, p.rows_per_kvh) - 1;
+    if (wr1 >= wr0) {
+      const int qa = ctx - p.q_len + wr0 / p.G;  // first row's query position
+      const int qb_ = ctx - p.q_len + wr1 / p.G; // last row's
+      wave_hi = p.causal ? min(ctx, qa + 1) : ctx;
+      wave_lo = p.window > 0 ? max(0, qb_ - p.window + 1) : 0;
+    }
+  }
   uint4 qb[JD];
   {
     const T* qp = static_cast<const T*>(p.q);
@@ -123,11 +141,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     }
   }
 
-  float acc[ND][4];
+  mf_f32x4 acc[ND];
 #pragma unroll
-  for (int t = 0; t < ND; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
+  for (int t = 0; t < ND; ++t) acc[t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY;
   float l_run = 0.0f;
 
@@ -201,24 +217,37 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     __syncthreads();  // this step's K/V rows are in LDS
 
     const int t_base = step * kPfStep;
+    // Keys of this step all visible to every row of the wave: no per-key mask.
+    const bool full = t_base >= wave_lo && t_base + kPfStep <= wave_hi;
     // ---- S^T for the wave's 16 rows: 4 slices of 16 tokens ----
     float sc[4][4];
     float mt = -INFINITY;
+    mf_f32x4 sv[4];
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) sv[sl] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+    // k-step outer, slices inner: four independent LDS reads, then four MFMAs
+#pragma unroll
+    for (int j = 0; j < JD; ++j) {
+      uint4 ka[4];
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl)
+        ka[sl] = *reinterpret_cast<const uint4*>(&s_k[(16 * sl + n) * RS + 32 * j + 8 * g]);
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) sv[sl] = Mfma16<T>::mac(ka[sl], qb[j], sv[sl]);
+    }
 #pragma unroll
     for (int sl = 0; sl < 4; ++sl) {
-      mf_f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < JD; ++j) {
-        const uint4 ka = *reinterpret_cast<const uint4*>(&s_k[(16 * sl + n) * RS + 32 * j + 8 * g]);
-        s = Mfma16<T>::mac(ka, qb[j], s);
+      for (int r = 0; r < 4; ++r) sc[sl][r] = sv[sl][r] * p.scale_log2;
+      if (!full) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = t_base + 16 * sl + 4 * g + r;
+          sc[sl][r] = (tok >= lo_n && tok < hi_n) ? sc[sl][r] : -INFINITY;
+        }
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tok = t_base + 16 * sl + 4 * g + r;
-        const bool ok = tok >= lo_n && tok < hi_n;
-        sc[sl][r] = ok ? s[r] * p.scale_log2 : -INFINITY;
-        mt = fmaxf(mt, sc[sl][r]);
-      }
+      for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sc[sl][r]);
     }
     mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
     mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
@@ -243,10 +272,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     }
     l_run = fmaf(l_run, alpha, psum);
     m_run = m_new;
+    if (__any(alpha != 1.0f)) {  // alpha is exactly 1 for rows whose max did not move
 #pragma unroll
-    for (int t = 0; t < ND; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] *= alpha;
+      for (int t = 0; t < ND; ++t) acc[t] *= alpha;
+    }
 
     // ---- O^T += V^T P^T: A = V^T via transposed LDS reads ----
     // Lane s of a 16-lane group names 4 dims (4 * (s & 3) ..) of token (s >> 2) + base;
@@ -255,26 +284,21 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     const int tr_dim = 4 * (lane & 3);  // 4 * (s & 3)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
+      const int tok0 = 32 * ks + 4 * g + tr_tok;        // e = 0..3: slice 2ks
+      const int tok1 = 32 * ks + 16 + 4 * g + tr_tok;   // e = 4..7: slice 2ks + 1
+      uint4 va[ND];  // all eight dim tiles' operands first, then the MFMAs
 #pragma unroll
       for (int t = 0; t < ND; ++t) {
-        const int tok0 = 32 * ks + 4 * g + tr_tok;        // e = 0..3: slice 2ks
-        const int tok1 = 32 * ks + 16 + 4 * g + tr_tok;   // e = 4..7: slice 2ks + 1
         const pf_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (lds_s4*)(&s_v[tok0 * RS + 16 * t + tr_dim]));
         const pf_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (lds_s4*)(&s_v[tok1 * RS + 16 * t + tr_dim]));
-        uint4 va;
-        va.x = static_cast<uint16_t>(lo.x) | (static_cast<uint32_t>(static_cast<uint16_t>(lo.y)) << 16);
-        va.y = static_cast<uint16_t>(lo.z) | (static_cast<uint32_t>(static_cast<uint16_t>(lo.w)) << 16);
-        va.z = static_cast<uint16_t>(hi.x) | (static_cast<uint32_t>(static_cast<uint16_t>(hi.y)) << 16);
-        va.w = static_cast<uint16_t>(hi.z) | (static_cast<uint32_t>(static_cast<uint16_t>(hi.w)) << 16);
-        mf_f32x4 o = {acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
-        o = Mfma16<T>::mac(va, pb[ks], o);
-        acc[t][0] = o[0];
-        acc[t][1] = o[1];
-        acc[t][2] = o[2];
-        acc[t][3] = o[3];
+        const uint2 lo2 = __builtin_bit_cast(uint2, lo);
+        const uint2 hi2 = __builtin_bit_cast(uint2, hi);
+        va[t] = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
       }
+#pragma unroll
+      for (int t = 0; t < ND; ++t) acc[t] = Mfma16<T>::mac(va[t], pb[ks], acc[t]);
     }
   }
 
@@ -285,9 +309,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     T* op = static_cast<T*>(p.out) + orow * D;
 #pragma unroll
-    for (int t = 0; t < ND; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) Elt<T>::store(op + 16 * t + 4 * g + r, acc[t][r] * inv);
+    for (int t = 0; t < ND; ++t) {
+      const uint2 pk = make_uint2(Pack2<T>::pack(acc[t][0] * inv, acc[t][1] * inv),
+                                  Pack2<T>::pack(acc[t][2] * inv, acc[t][3] * inv));
+      *reinterpret_cast<uint2*>(op + 16 * t + 4 * g) = pk;
+    }
   }
 }
 
