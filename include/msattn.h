@@ -67,8 +67,8 @@ int msattn_partition_tokens(int batch, int q_len, int num_heads, int num_kv_head
                             int head_dim, int max_context);
 
 /*
- * Bytes of caller-owned device workspace msattn_paged_attention needs.
- * Replaces the per-call torch.empty partial buffers of
+ * Bytes of caller-owned device workspace msattn_paged_attention needs (a size
+ * that depends on the geometry only). Replaces the per-call torch.empty partial buffers of
  * kernels/paged_attn_triton.py:320-323.
  */
 size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_heads,
@@ -97,11 +97,13 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
 
 /*
  * First half of msattn_paged_attention: writes the split-K partials (running
- * max m, sum l and unnormalised accumulator per context partition) into the
- * workspace. The workspace layout is: float ml[rows][max_parts][2] followed by
- * float acc[rows][max_parts][head_dim], rows = batch * q_len * num_heads
- * ordered like `out`, max_parts = ceil(max_context / partition), m in base-2
- * units (m = max of scale * log2(e) * q.k). Replaces _split_kernel
+ * max m, sum l and unnormalised accumulator per slice of context) into the
+ * workspace, m in base-2 units (m = max of scale * log2(e) * q.k). The workspace
+ * is opaque to the caller: a header naming the layout the launch chose (one slot
+ * per context partition, closed by an end marker; or, for large decodes, stream-K
+ * pieces located through a prefix sum of per-sequence tiles), then float (m, l)
+ * pairs and float accumulators, each region 256-byte aligned. Only
+ * msattn_merge_partials reads it, for the same geometry. Replaces _split_kernel
  * (kernels/paged_attn_triton.py:176-248).
  */
 int msattn_paged_attention_partials(const void* query, const void* k_cache, const void* v_cache,
@@ -116,8 +118,9 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
 
 /*
  * Second half of msattn_paged_attention: log-sum-exp merge of the partials in
- * `workspace` into `out` (q_dtype). Replaces _merge_kernel
- * (kernels/paged_attn_triton.py:250-284).
+ * `workspace` into `out` (q_dtype). Rows with no key get zeros. The geometry must
+ * be the one the partials call was given; context_lens is that call's array.
+ * Replaces _merge_kernel (kernels/paged_attn_triton.py:250-284).
  */
 int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
                           const int32_t* context_lens, void* out, int batch, int q_len,

@@ -54,26 +54,62 @@ int choose_partition(int batch, int q_len, int num_heads, int num_kv_heads, int 
   return kPartitionChoices[sizeof(kPartitionChoices) / sizeof(int) - 1];
 }
 
+int largest_pow2_divisor_upto(int x, int cap) {
+  int u = 1;
+  while (u * 2 <= cap && x % (u * 2) == 0) u *= 2;
+  return u;
+}
+
+// Stream-K grid: one 8-wave workgroup per CU (MI355X has 256 CUs); devices with
+// fewer CUs launch fewer.
+constexpr int kSkGrid = 256;
+#ifndef MSATTN_SK_MIN_CHUNK
+#define MSATTN_SK_MIN_CHUNK 4
+#endif
+constexpr int kSkMinChunk = MSATTN_SK_MIN_CHUNK;  // stream-K: smallest chunk (tiles)
+
+int mfma_rows_per_tile(int rows_per_kvh) { return rows_per_kvh >= 16 ? 16 : next_pow2(rows_per_kvh); }
+
+// Workspace: [header][ml: slots x 2 floats][acc: slots x head_dim floats], each
+// region 256-byte aligned. Slots cover both partial layouts: rows x max_parts for
+// the partition kernels, and pieces x UG x RT for stream-K decode, where pieces
+// <= chunks + NUG * batch and chunks <= min(grid * 8 / UG, tiles / min chunk).
 struct Layout {
   int part;
   int max_parts;
   int64_t rows;
-  size_t ml_bytes;   // rounded up to 256
+  int64_t slots;
+  size_t hdr_bytes;
+  size_t ml_bytes;
   size_t acc_bytes;
+  size_t total() const { return hdr_bytes + ml_bytes + acc_bytes; }
 };
+
+size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
 Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
                         int max_context) {
   Layout L;
   L.part = choose_partition(batch, q_len, num_heads, num_kv_heads, max_context);
-  // Slots per row: enough for the partition kernels (one per partition) and for
-  // the stream-K kernel (pieces), plus the end marker.
-  const int by_part = (max_context > 0 ? ceil_div(max_context, L.part) : 1) + 1;
-  L.max_parts = by_part > streamk_slots(max_context) ? by_part : streamk_slots(max_context);
+  // Partition kernels: one slot per partition plus the end marker.
+  L.max_parts = (max_context > 0 ? ceil_div(max_context, L.part) : 1) + 1;
   L.rows = static_cast<int64_t>(batch) * q_len * num_heads;
-  const size_t ml = static_cast<size_t>(L.rows) * L.max_parts * 2 * sizeof(float);
-  L.ml_bytes = (ml + 255) / 256 * 256;
-  L.acc_bytes = static_cast<size_t>(L.rows) * L.max_parts * head_dim * sizeof(float);
+  L.slots = L.rows * L.max_parts;
+  if (q_len == 1 && batch <= kSkMaxBatch) {
+    const int RT = mfma_rows_per_tile(num_heads / num_kv_heads);
+    const int units = num_kv_heads * ceil_div(num_heads / num_kv_heads, RT);
+    const int UG = largest_pow2_divisor_upto(units, kSkWaves);
+    const int64_t segments = static_cast<int64_t>(units / UG) * batch;
+    const int64_t tiles = segments * ceil_div(max_context, 16);
+    const int64_t by_grid = static_cast<int64_t>(kSkGrid) * (kSkWaves / UG);
+    const int64_t by_size = (tiles + kSkMinChunk - 1) / kSkMinChunk;
+    const int64_t chunks = by_grid < by_size ? by_grid : by_size;
+    const int64_t sk = streamk_pieces(chunks, segments) * UG * RT;
+    if (sk > L.slots) L.slots = sk;
+  }
+  L.hdr_bytes = round256(sizeof(int) * (kHdrPrefix + static_cast<size_t>(batch) + 1));
+  L.ml_bytes = round256(static_cast<size_t>(L.slots) * 2 * sizeof(float));
+  L.acc_bytes = static_cast<size_t>(L.slots) * head_dim * sizeof(float);
   return L;
 }
 
@@ -93,12 +129,6 @@ int device_cus() {
     n = 256;
   if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
   return n;
-}
-
-int largest_pow2_divisor_upto(int x, int cap) {
-  int u = 1;
-  while (u * 2 <= cap && x % (u * 2) == 0) u *= 2;
-  return u;
 }
 
 hipError_t dispatch_split(const SplitParams& p, int q_dtype, int kv_dtype, int D, int RT,
@@ -151,7 +181,7 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
                               int max_context) {
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context)) return 0;
   const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
-  return L.ml_bytes + L.acc_bytes;
+  return L.total();
 }
 
 int msattn_paged_attention_partials(const void* query, const void* k_cache, const void* v_cache,
@@ -174,7 +204,7 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
   if (rc != MSATTN_OK) return rc;
   if (!aligned(query, dtype_bytes(q_dtype)) || !aligned(workspace, 16)) return MSATTN_ERR_INVALID_ARG;
   const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
-  if (workspace_bytes < L.ml_bytes + L.acc_bytes) return MSATTN_ERR_WORKSPACE;
+  if (workspace_bytes < L.total()) return MSATTN_ERR_WORKSPACE;
 
   const int G = num_heads / num_kv_heads;
   const int rows = q_len * G;
@@ -182,15 +212,17 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
   // holding whole 16-token tiles. Everything else takes the generic kernel.
   const bool use_mfma = q_dtype == kv_dtype && (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
                         (head_dim == 64 || head_dim == 128) && block_size % 16 == 0;
-  const int RT = use_mfma ? (rows >= 16 ? 16 : next_pow2(rows)) : rows_per_tile(rows);
+  const int RT = use_mfma ? mfma_rows_per_tile(rows) : rows_per_tile(rows);
+  char* ws = static_cast<char*>(workspace);
   SplitParams p;
+  p.hdr = reinterpret_cast<int*>(ws);
   p.q = query;
   p.k = k_cache;
   p.v = v_cache;
   p.table = block_table;
   p.lens = context_lens;
-  p.ml = static_cast<float*>(workspace);
-  p.acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.ml_bytes);
+  p.ml = reinterpret_cast<float*>(ws + L.hdr_bytes);
+  p.acc = reinterpret_cast<float*>(ws + L.hdr_bytes + L.ml_bytes);
   p.blk_stride = cache_block_stride;
   p.slot_stride = cache_slot_stride;
   p.head_stride = cache_head_stride;
@@ -212,6 +244,7 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
   p.rtiles = ceil_div(rows, RT);
   p.sk_group = 1;
   p.sk_unit_groups = 0;
+  p.sk_min_chunk = kSkMinChunk;
   const int64_t gx = static_cast<int64_t>(p.max_parts) * num_kv_heads * p.rtiles;
   if (gx >= (int64_t(1) << 31) || batch > 65535) return MSATTN_ERR_UNSUPPORTED;
 
@@ -227,7 +260,7 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
     const int units = num_kv_heads * p.rtiles;
     p.sk_group = largest_pow2_divisor_upto(units, kSkWaves);
     p.sk_unit_groups = units / p.sk_group;
-    const int grid = device_cus();
+    const int grid = device_cus() < kSkGrid ? device_cus() : kSkGrid;
     if (q_dtype == MSATTN_BF16) e = launch_decode_streamk<bf16_t>(p, head_dim, RT, grid, st, &sup);
     else e = launch_decode_streamk<_Float16>(p, head_dim, RT, grid, st, &sup);
     if (!sup) return MSATTN_ERR_UNSUPPORTED;
@@ -255,18 +288,20 @@ int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
   if (head_dim > 1024) return MSATTN_ERR_UNSUPPORTED;
   if (!aligned(out, dtype_bytes(q_dtype)) || !aligned(workspace, 16)) return MSATTN_ERR_INVALID_ARG;
   const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
-  if (workspace_bytes < L.ml_bytes + L.acc_bytes) return MSATTN_ERR_WORKSPACE;
+  if (workspace_bytes < L.total()) return MSATTN_ERR_WORKSPACE;
+  const char* ws = static_cast<const char*>(workspace);
   MergeParams p;
-  p.ml = static_cast<const float*>(workspace);
-  p.acc = reinterpret_cast<const float*>(static_cast<const char*>(workspace) + L.ml_bytes);
-  p.lens = context_lens;
+  p.hdr = reinterpret_cast<const int*>(ws);
+  p.ml = reinterpret_cast<const float*>(ws + L.hdr_bytes);
+  p.acc = reinterpret_cast<const float*>(ws + L.hdr_bytes + L.ml_bytes);
   p.out = out;
   p.rows = L.rows;
-  p.rows_per_b = q_len * num_heads;
+  p.batch = batch;
+  p.H = num_heads;
+  p.KVH = num_kv_heads;
+  p.G = num_heads / num_kv_heads;
   p.D = head_dim;
   p.max_parts = L.max_parts;
-  p.part = L.part;
-  p.max_ctx = max_context;
   bool sup = false;
   const hipError_t e = launch_merge(p, q_dtype, static_cast<hipStream_t>(stream), &sup);
   if (!sup) return MSATTN_ERR_UNSUPPORTED;
@@ -299,7 +334,7 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
     if (rc != MSATTN_OK) return rc;
     if (!aligned(query, 16)) return MSATTN_ERR_INVALID_ARG;
     const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
-    if (workspace_bytes < L.ml_bytes + L.acc_bytes) return MSATTN_ERR_WORKSPACE;
+    if (workspace_bytes < L.total()) return MSATTN_ERR_WORKSPACE;
     PrefillParams pp;
     pp.q = query;
     pp.k = k_cache;

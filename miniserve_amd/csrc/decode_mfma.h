@@ -136,6 +136,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   const int va = lane / LPR; // V token group
   const int vc = lane % LPR; // V 16-byte chunk
 
+  if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) p.hdr[kHdrKind] = 0;
   // blockIdx.x = kvh + KVH * (part + max_parts * rtile); blockIdx.z = b.
   const unsigned bx = blockIdx.x;
   const int kvh = static_cast<int>(bx % static_cast<unsigned>(p.KVH));

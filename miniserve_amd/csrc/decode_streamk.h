@@ -11,12 +11,12 @@
 // So every wave streams the same amount of KV (no ragged tails), pays its
 // set-up once per run of tiles, and the UG heads of a page are read together.
 //
-// A chunk that crosses sequence boundaries is split into pieces. Piece j of
-// sequence b (counted from the chunk that holds b's first slab) writes its
-// partial (m, l, acc) into workspace slot j of each of its rows; the piece that
-// ends the sequence writes the end marker (m = -inf, l = -1) into the next
-// slot, and merge.hip combines slots up to the marker. Workgroup 0 marks rows
-// whose sequence has no tile (context 0) as empty.
+// A chunk that crosses sequence boundaries is split into pieces. With
+// segment index seg = ug * B + b, the piece of chunk r inside segment seg has the
+// id r + seg: ids are unique and below n_chunks + NUG * B, whatever the lengths.
+// Each piece stores, for each of its UG units' rows, the partial (m, l, acc) at
+// [id][unit in group][row]. Workgroup 0 writes the layout (chunk size, prefix sums
+// of T_b) into the workspace header; merge.hip finds a row's pieces from it.
 //
 // The per-tile arithmetic is decode_mfma.h's: MFMA scores, online softmax, P.V
 // with DPP row broadcasts, two tiles' loads in flight through per-tile buffer
@@ -32,17 +32,15 @@ namespace msattn {
 constexpr int kSkWaves = 8;
 constexpr int kSkThreads = kSkWaves * kWave;
 constexpr int kSkMaxBatch = 4096;   // sequences per launch on this path
-constexpr int kSkMinChunk = 16;     // tiles: lower bound of a chunk
 constexpr int kSkTableRun = 64;     // tile page ids fetched per table load
 #ifndef MSATTN_SK_UNROLL
 #define MSATTN_SK_UNROLL 2
 #endif
 constexpr int kSkUnroll = MSATTN_SK_UNROLL;  // tiles per loop iteration (even)
 
-// Slots a row needs at most when chunks are >= kSkMinChunk tiles: pieces plus
-// the end marker.
-__host__ __device__ constexpr int streamk_slots(int max_ctx) {
-  return (max_ctx + 15) / 16 / kSkMinChunk + 3;
+// Pieces a launch can produce: one per chunk plus one per segment boundary.
+__host__ __device__ constexpr int64_t streamk_pieces(int64_t n_chunks, int64_t n_segments) {
+  return n_chunks + n_segments;
 }
 
 template <typename T, int D, int RT>
@@ -112,25 +110,28 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
   }
   __syncthreads();
 
-  // Rows of sequences without any tile: end marker in slot 0.
-  if (blockIdx.x == 0) {
-    for (int idx = tid; idx < B * p.H; idx += kSkThreads) {
-      const int b = idx / p.H;
-      if (s_pre[b + 1] == s_pre[b]) {
-        float* ml = p.ml + static_cast<int64_t>(idx) * p.max_parts * 2;
-        ml[0] = -INFINITY;
-        ml[1] = -1.0f;
-      }
-    }
-  }
-  if (sumT == 0) return;
-
   // ---- chunking ----
   const int UG = p.sk_group;                 // KV heads per unit group (divides kSkWaves)
   const int SG = kSkWaves / UG;              // sub-groups per workgroup
   const int64_t total = static_cast<int64_t>(p.sk_unit_groups) * sumT;
   const int64_t nsub = static_cast<int64_t>(gridDim.x) * SG;
-  const int64_t c = max(static_cast<int64_t>(kSkMinChunk), (total + nsub - 1) / nsub);
+  const int64_t c = max(static_cast<int64_t>(p.sk_min_chunk), (total + nsub - 1) / nsub);
+
+  // Workgroup 0 publishes the layout for the merge.
+  if (blockIdx.x == 0) {
+    if (tid == 0) {
+      p.hdr[kHdrKind] = 1;
+      p.hdr[kHdrSumT] = sumT;
+      p.hdr[kHdrChunk] = static_cast<int>(c);
+      p.hdr[kHdrNsub] = static_cast<int>(nsub);
+      p.hdr[kHdrUG] = UG;
+      p.hdr[kHdrNUG] = p.sk_unit_groups;
+      p.hdr[kHdrB] = B;
+      p.hdr[kHdrRT] = RT;
+    }
+    for (int b = tid; b <= B; b += kSkThreads) p.hdr[kHdrPrefix + b] = s_pre[b];
+  }
+  if (sumT == 0) return;
   const int sg = w / UG;
   const int ul = w - sg * UG;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * SG + sg;
@@ -155,8 +156,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
     const int64_t seg_start = static_cast<int64_t>(ug) * sumT + s_pre[b];
     const int64_t seg_end = static_cast<int64_t>(ug) * sumT + s_pre[b + 1];
     const int64_t pe = min(s_end, seg_end);
-    const int piece = static_cast<int>(r - seg_start / c);
-    const bool last = pe == seg_end;
+    const int64_t pid = r + static_cast<int64_t>(ug) * B + b;  // piece id
 
     const int unit = ug * UG + ul;          // unit = rtile * KVH + kvh
     const int kvh = unit % p.KVH;
@@ -326,25 +326,21 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
         for (int oo = LPR; oo < kWave; oo <<= 1) a += __shfl_xor(a, oo, kWave);
         acc[rr][e] = a;
       }
-    if (va == 0 && piece < p.max_parts) {
+    const int64_t slot0 = (pid * UG + ul) * RT;  // this unit's rows in the piece
+    if (va == 0) {
 #pragma unroll
       for (int rr = 0; rr < RT; ++rr) {
         if (rr < nrows) {
-          const int64_t orow = static_cast<int64_t>(b) * p.H + kvh * p.G + row0 + rr;
-          float* dst = p.acc + (orow * p.max_parts + piece) * D + vc * 8;
+          float* dst = p.acc + (slot0 + rr) * D + vc * 8;
           *reinterpret_cast<float4*>(dst) = make_float4(acc[rr][0], acc[rr][1], acc[rr][2], acc[rr][3]);
           *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[rr][4], acc[rr][5], acc[rr][6], acc[rr][7]);
         }
       }
     }
-    if (lane < nrows && piece < p.max_parts) {
-      float* ml = p.ml + (orow_n * p.max_parts + piece) * 2;
+    if (lane < nrows) {
+      float* ml = p.ml + (slot0 + lane) * 2;
       ml[0] = m_run;
       ml[1] = l_run;
-      if (last && piece + 1 < p.max_parts) {
-        ml[2] = -INFINITY;
-        ml[3] = -1.0f;
-      }
     }
     s = pe;
   }

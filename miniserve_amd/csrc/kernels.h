@@ -7,13 +7,13 @@
 namespace msattn {
 
 struct MergeParams {
+  const int* hdr;     // workspace header written by the partials kernel
   const float* ml;
   const float* acc;
-  const int32_t* lens;
   void* out;
-  int64_t rows;   // batch * q_len * H
-  int rows_per_b; // q_len * H
-  int D, max_parts, part, max_ctx;
+  int64_t rows;       // batch * q_len * H
+  int batch, H, KVH, G, D;
+  int max_parts;      // slots per row of the partition layout
 };
 
 hipError_t launch_merge(const MergeParams& p, int q_dtype, hipStream_t stream, bool* supported);

@@ -1,117 +1,154 @@
-// Log-sum-exp merge of split-K partials (one workgroup per output row).
+// Log-sum-exp merge of split-K partials into the attention output.
 //
-// A row's partials sit in workspace slots 0, 1, ... up to the first end marker
-// (l = -1) or the last slot. With M = max_j m_j and w_j = 2^(m_j - M):
+// One wave per output row (4 rows per workgroup). The workspace header says how
+// the partials kernel laid its partials out:
+//   kind 0 (partition kernels): a row's partials sit in its slots 0, 1, ... up to
+//     the first end marker (l = -1) or the last slot;
+//   kind 1 (stream-K decode): a decode row (b, h) belongs to unit u = rtile * KVH + kvh
+//     (rtile = (h % G) / RT), unit group ug = u / UG; its segment ug * B + b spans
+//     positions [ug * sumT + P_b, ... + T_b) of the chunked work list, and the chunk r
+//     holding a piece of it stored that piece at id r + ug * B + b.
+// With running max M and weights w_j = 2^(m_j - M):
 //   out = sum_j w_j acc_j / sum_j w_j l_j
-// which is the merge of kernels/paged_attn_triton.py:_merge_kernel (:250-284)
-// and of flash_decode_reference's running update (:155-170), in base 2. Slots
-// with m = -inf (no visible key) carry no weight. Rows with no key at all
-// (context 0, or fully masked) get zeros, the value flash_decode_reference
-// returns for L <= 0 (:143-144).
+// which is the merge of kernels/paged_attn_triton.py:_merge_kernel (:250-284) and
+// of flash_decode_reference's running update (:155-170), in base 2. Partials with
+// m = -inf carry no weight; rows with no key at all get zeros (the value
+// flash_decode_reference returns for L <= 0, :143-144).
 #include "kernels.h"
 
 namespace msattn {
 
 constexpr int kMergeThreads = 256;
 constexpr int kMergeWaves = kMergeThreads / kWave;
+constexpr int kMergeMaxDims = 4;  // dims per lane: head_dim <= 256
+constexpr int kMergeBatch = 8;    // acc rows loaded together
 
 template <typename QT>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams p) {
-  __shared__ float s_w[kMergeThreads];
-  __shared__ float s_red[kMergeThreads * 4];
-  __shared__ float s_wave[kMergeWaves];
-  __shared__ int s_end[kMergeWaves];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kMergeWaves + w;
+  if (row >= p.rows) return;
+  const int D = p.D;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wv = tid / kWave;
-  const int64_t row = blockIdx.x;
-  const float* ml = p.ml + row * p.max_parts * 2;
-  const float* acc = p.acc + row * p.max_parts * p.D;
-
-  // Number of filled slots: index of the first end marker.
-  int first_end = p.max_parts;
-  for (int j = tid; j < p.max_parts; j += kMergeThreads)
-    if (ml[2 * j + 1] == -1.0f) first_end = min(first_end, j);
+  // Header and this row's prefix entries are read up front, in one round trip.
+  int hv[8];
 #pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) first_end = min(first_end, __shfl_xor(first_end, o, kWave));
-  if (lane == 0) s_end[wv] = first_end;
-  __syncthreads();
-  int n = s_end[0];
-#pragma unroll
-  for (int i = 1; i < kMergeWaves; ++i) n = min(n, s_end[i]);
+  for (int i = 0; i < 8; ++i) hv[i] = p.hdr[i];
+  const int b = static_cast<int>(row / p.H);  // the sequence when q_len == 1
+  const int bh = b < p.batch ? b : p.batch - 1;  // header holds batch + 1 prefixes
+  const int pb = p.hdr[kHdrPrefix + bh];
+  const int pe = p.hdr[kHdrPrefix + bh + 1];
 
-  float m = -INFINITY;
-  for (int j = tid; j < n; j += kMergeThreads) m = fmaxf(m, ml[2 * j]);
-  m = group_max<kWave>(m);
-  if (lane == 0) s_wave[wv] = m;
-  __syncthreads();
-  float M = s_wave[0];
-#pragma unroll
-  for (int i = 1; i < kMergeWaves; ++i) M = fmaxf(M, s_wave[i]);
-
-  const int DV = p.D / 4;               // float4 columns per row
-  const int PS = kMergeThreads / DV;    // slots handled side by side
-  const int ps = tid / DV;
-  const int d4 = tid - ps * DV;
-  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-  float L = 0.0f;
-  for (int base = 0; base < n; base += kMergeThreads) {
-    const int cnt = min(kMergeThreads, n - base);
-    __syncthreads();
-    if (tid < cnt) {
-      const float mp = ml[2 * (base + tid)];
-      const float lp = ml[2 * (base + tid) + 1];
-      const float wgt = (mp == -INFINITY) ? 0.0f : exp2f(mp - M);
-      s_w[tid] = wgt;
-      L = fmaf(wgt, lp, L);
+  // Partial j of this row sits at slot base + j * stride; n bounds the count.
+  int64_t base = 0, stride = 1;
+  int64_t n = 0;
+  const bool markers = hv[kHdrKind] == 0;
+  if (markers) {
+    base = row * p.max_parts;
+    n = p.max_parts;
+  } else {
+    const int B = hv[kHdrB];
+    const int sumT = hv[kHdrSumT];
+    const int c = hv[kHdrChunk];
+    const int UG = hv[kHdrUG];
+    const int RT = hv[kHdrRT];
+    const int h = static_cast<int>(row - static_cast<int64_t>(b) * p.H);
+    const int kvh = h / p.G;
+    const int gi = h - kvh * p.G;
+    const int unit = (gi / RT) * p.KVH + kvh;
+    const int ug = unit / UG;
+    const int ul = unit - ug * UG;
+    if (pe > pb) {
+      const int64_t seg_start = static_cast<int64_t>(ug) * sumT + pb;
+      const int64_t r0 = seg_start / c;
+      n = (seg_start + (pe - pb) - 1) / c - r0 + 1;
+      base = ((r0 + static_cast<int64_t>(ug) * B + b) * UG + ul) * RT + gi % RT;
+      stride = static_cast<int64_t>(UG) * RT;
     }
-    __syncthreads();
-    if (ps < PS) {
-      for (int j = ps; j < cnt; j += PS) {
-        const float wgt = s_w[j];
-        if (wgt != 0.0f) {
-          const float4 x =
-              *reinterpret_cast<const float4*>(acc + static_cast<int64_t>(base + j) * p.D + 4 * d4);
-          a.x = fmaf(wgt, x.x, a.x);
-          a.y = fmaf(wgt, x.y, a.y);
-          a.z = fmaf(wgt, x.z, a.z);
-          a.w = fmaf(wgt, x.w, a.w);
-        }
+  }
+
+  float acc[kMergeMaxDims];
+#pragma unroll
+  for (int k = 0; k < kMergeMaxDims; ++k) acc[k] = 0.0f;
+  float M = -INFINITY;
+  float L = 0.0f;
+  // 64 partials at a time: lane j loads (m, l) of partial j0 + j, the wave takes
+  // their max and weights, then folds the acc rows kMergeBatch at a time with all
+  // of a batch's loads in flight together.
+  for (int64_t j0 = 0; j0 < n; j0 += kWave) {
+    const int64_t j = j0 + lane;
+    float m = -INFINITY, l = 0.0f;
+    if (j < n) {
+      const float2 v = *reinterpret_cast<const float2*>(p.ml + (base + j * stride) * 2);
+      m = v.x;
+      l = v.y;
+    }
+    int cnt = static_cast<int>(n - j0 < kWave ? n - j0 : kWave);
+    bool end = false;
+    if (markers) {  // the first end marker (l = -1) closes the row
+      const uint64_t mk = __ballot(j < n && l == -1.0f);
+      if (mk) {
+        cnt = __builtin_ctzll(mk);
+        end = true;
       }
     }
-  }
-  L = group_sum<kWave>(L);
-  __syncthreads();
-  if (lane == 0) s_wave[wv] = L;
-  if (ps < PS) {
-    s_red[ps * p.D + 4 * d4 + 0] = a.x;
-    s_red[ps * p.D + 4 * d4 + 1] = a.y;
-    s_red[ps * p.D + 4 * d4 + 2] = a.z;
-    s_red[ps * p.D + 4 * d4 + 3] = a.w;
-  }
-  __syncthreads();
-  float Lt = 0.0f;
+    if (lane >= cnt) m = -INFINITY;
+    const float mb = group_max<kWave>(m);
+    if (mb != -INFINITY) {
+      const float Mn = fmaxf(M, mb);
+      const float a = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M = -inf
+      const float wj = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - Mn);
+      L = L * a + group_sum<kWave>(wj * l);
 #pragma unroll
-  for (int i = 0; i < kMergeWaves; ++i) Lt += s_wave[i];
-  const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
-  QT* out = static_cast<QT*>(p.out) + row * p.D;
-  for (int d = tid; d < p.D; d += kMergeThreads) {
-    float s = 0.0f;
-    for (int i = 0; i < PS; ++i) s += s_red[i * p.D + d];
-    Elt<QT>::store(out + d, s * inv);
+      for (int k = 0; k < kMergeMaxDims; ++k) acc[k] *= a;
+      for (int i0 = 0; i0 < cnt; i0 += kMergeBatch) {
+        float x[kMergeBatch][kMergeMaxDims];
+        float wv[kMergeBatch];
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+          const int i = i0 + u < cnt ? i0 + u : cnt - 1;  // stays on a real partial
+          wv[u] = i0 + u < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                                __builtin_bit_cast(int, wj), i))
+                               : 0.0f;
+          const float* arow = p.acc + (base + (j0 + i) * stride) * D;
+#pragma unroll
+          for (int k = 0; k < kMergeMaxDims; ++k) {
+            const int d = lane + kWave * k;
+            x[u][k] = d < D ? arow[d] : 0.0f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+#pragma unroll
+          for (int k = 0; k < kMergeMaxDims; ++k)  // weight 0: partial without keys
+            acc[k] += wv[u] != 0.0f ? wv[u] * x[u][k] : 0.0f;
+        }
+      }
+      M = Mn;
+    }
+    if (end) break;
+  }
+
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  QT* out = static_cast<QT*>(p.out) + row * D;
+#pragma unroll
+  for (int k = 0; k < kMergeMaxDims; ++k) {
+    const int d = lane + kWave * k;
+    if (d < D) Elt<QT>::store(out + d, acc[k] * inv);
   }
 }
 
 template <typename QT>
 static hipError_t launch_merge_t(const MergeParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL(merge_kernel<QT>, dim3(static_cast<unsigned>(p.rows)), dim3(kMergeThreads), 0,
-                     stream, p);
+  const unsigned blocks = static_cast<unsigned>((p.rows + kMergeWaves - 1) / kMergeWaves);
+  hipLaunchKernelGGL(merge_kernel<QT>, dim3(blocks), dim3(kMergeThreads), 0, stream, p);
   return hipGetLastError();
 }
 
 hipError_t launch_merge(const MergeParams& p, int q_dtype, hipStream_t stream, bool* supported) {
-  *supported = true;
+  *supported = p.D <= kWave * kMergeMaxDims;
+  if (!*supported) return hipSuccess;
   switch (q_dtype) {
     case 0: return launch_merge_t<float>(p, stream);
     case 1: return launch_merge_t<_Float16>(p, stream);

@@ -42,7 +42,18 @@ constexpr int kSplitWaves = kSplitThreads / kWave;
 #endif
 constexpr int kPartMax = MSATTN_PART_MAX;
 
+// Workspace header (first bytes of every workspace): which partial layout the
+// partials kernel used, so the merge can read it back.
+//   hdr[0] kind: 0 = per-row slots closed by end markers (partition kernels);
+//                1 = stream-K pieces (decode_streamk.h)
+//   kind 1 also: hdr[1] sumT, [2] chunk c, [3] sub-ranges, [4] UG, [5] NUG, [6] B,
+//   [7] RT, and hdr[kHdrPrefix + b] = tiles of sequences before b (b = 0..B).
+constexpr int kHdrPrefix = 64;
+constexpr int kHdrKind = 0, kHdrSumT = 1, kHdrChunk = 2, kHdrNsub = 3, kHdrUG = 4,
+              kHdrNUG = 5, kHdrB = 6, kHdrRT = 7;
+
 struct SplitParams {
+  int* hdr;
   const void* q;
   const void* k;
   const void* v;
@@ -60,6 +71,7 @@ struct SplitParams {
   int rtiles;        // ceil(rows_per_kvh / RT)
   int sk_group;        // stream-K: KV-head units per unit group
   int sk_unit_groups;  // stream-K: number of unit groups
+  int sk_min_chunk;    // stream-K: smallest chunk (tiles)
 };
 
 template <typename QT, typename KT, int D, int RT>
@@ -84,6 +96,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int w = tid / kWave;
+  if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) p.hdr[kHdrKind] = 0;
 
   // blockIdx.x = part + max_parts * (kvh + KVH * rtile); blockIdx.z = b.
   const int part = static_cast<int>(blockIdx.x % static_cast<unsigned>(p.max_parts));

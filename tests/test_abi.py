@@ -44,11 +44,22 @@ def test_abi_version_and_status_strings():
 def test_partition_policy(B, q_len, H, KVH, D, ctx, part):
     lib = nat.lib()
     assert lib.msattn_partition_tokens(B, q_len, H, KVH, D, ctx) == part
-    # slots per row: one per partition or stream-K piece, plus the end marker
-    slots = max(-(-ctx // part) + 1, -(-ctx // 16) // 16 + 3)
-    ml = B * q_len * H * slots * 2 * 4
-    ml = -(-ml // 256) * 256
-    assert lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) == ml + B * q_len * H * slots * D * 4
+    # header: 64 ints + B + 1 prefix sums; slots: rows x (partitions + end marker),
+    # or stream-K pieces x UG x RT if larger: pieces = chunks + NUG x B, chunks at
+    # most 256 workgroups x 8 / UG waves and at most tiles / 4
+    r256 = lambda x: -(-x // 256) * 256
+    rows = B * q_len * H
+    slots = rows * (-(-ctx // part) + 1)
+    if q_len == 1:
+        G = H // KVH
+        RT = 16 if G >= 16 else 1 << (G - 1).bit_length()
+        units = KVH * -(-G // RT)
+        UG = max(u for u in (1, 2, 4, 8) if units % u == 0)
+        segments = units // UG * B
+        chunks = min(256 * 8 // UG, -(-(segments * -(-ctx // 16)) // 4))
+        slots = max(slots, (chunks + segments) * UG * RT)
+    expect = r256(4 * (64 + B + 1)) + r256(slots * 2 * 4) + slots * D * 4
+    assert lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) == expect
 
 
 def test_workspace_rejects_bad_geometry():
