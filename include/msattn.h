@@ -96,6 +96,28 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
                            float scale, int q_dtype, int kv_dtype, void* stream);
 
 /*
+ * msattn_paged_attention for decode (q_len == 1) with rotate-half RoPE applied to
+ * the query inside the attention kernels: row b's query becomes
+ * q * cos[p] + rotate_half(q) * sin[p], p = position[b] (clamped to
+ * [0, max_position)), computed in fp32 and rounded to q_dtype, then attends as
+ * msattn_paged_attention. rope_cos / rope_sin: fp32 [max_position, head_dim],
+ * 16-byte aligned; position: int32 [batch] on the device. Replaces the fused-RoPE
+ * branch of the split kernel (kernels/paged_attn_triton.py:211-220) and of
+ * flash_decode_reference (:135-139); the rotation is miniserve/attention.py:41-62.
+ * Returns MSATTN_ERR_UNSUPPORTED for q_len != 1, as the reference's decode-only path.
+ */
+int msattn_paged_attention_rope(const void* query, const void* k_cache, const void* v_cache,
+                                int64_t cache_block_stride, int64_t cache_slot_stride,
+                                int64_t cache_head_stride, const int32_t* block_table,
+                                const int32_t* context_lens, void* out, void* workspace,
+                                size_t workspace_bytes, int batch, int q_len, int num_heads,
+                                int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                                int table_width, int max_context, int causal, int window,
+                                float scale, int q_dtype, int kv_dtype, const float* rope_cos,
+                                const float* rope_sin, const int32_t* position,
+                                int max_position, void* stream);
+
+/*
  * First half of msattn_paged_attention: writes the split-K partials (running
  * max m, sum l and unnormalised accumulator per slice of context) into the
  * workspace, m in base-2 units (m = max of scale * log2(e) * q.k). The workspace

@@ -242,10 +242,10 @@ class PagedAttention:
                 raise ValueError("triton_flash does not support an FP8 KV cache")
             if query.device.type != "cuda":
                 raise RuntimeError("triton_flash requires CUDA tensors (a ROCm GPU device)")
-            if cos is not None and sin is not None and position is not None:
-                query = _rope_query(query, cos, sin, position)
+            rope = (cos, sin, position) if cos is not None and sin is not None and \
+                position is not None else None
             return paged_attention(query, k_cache, v_cache, block_table, context_lens,
-                                   causal=True, window=None, scale=scale)
+                                   causal=True, window=None, scale=scale, rope=rope)
         window = self.window if window is None else window
         return paged_attention(query, k_cache, v_cache, block_table, context_lens,
                                causal=causal, window=window, scale=scale)
@@ -253,28 +253,20 @@ class PagedAttention:
     __call__ = forward
 
 
-def _rope_query(query: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                position: torch.Tensor) -> torch.Tensor:
-    """Rotate-half RoPE of a decode query [B, 1, H, D] at per-row positions, in fp32."""
-    B = query.shape[0]
-    pos = torch.as_tensor(position, device=query.device).reshape(-1).to(torch.long)[:B]
-    cs = cos.to(query.device).index_select(0, pos).to(torch.float32)[:, None, None, :]
-    sn = sin.to(query.device).index_select(0, pos).to(torch.float32)[:, None, None, :]
-    qf = query.to(torch.float32)
-    return (qf * cs + _rotate_half(qf) * sn).to(query.dtype)
-
-
 def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                     block_table, context_lens, *, causal: bool = True, window: int | None = None,
                     scale: float | None = None, max_context: int | None = None,
-                    workspace: torch.Tensor | None = None, out: torch.Tensor | None = None
-                    ) -> torch.Tensor:
+                    workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                    rope: tuple | None = None) -> torch.Tensor:
     """Functional form of PagedAttention.forward on the HIP kernels.
 
     ``max_context`` bounds context_lens; when context_lens is a device tensor
     and it is None, the table capacity (width * block_size) is used so that no
     device->host read happens (the call is then safe to capture in a graph).
     ``workspace``/``out`` let a caller pass preallocated buffers.
+    ``rope`` = (cos, sin, position) applies rotate-half RoPE to a decode query inside
+    the attention kernels (cos/sin [max_pos, head_dim], position [batch] or a scalar;
+    kernels/paged_attn_triton.py:211-220).
     """
     _require_gpu(query, "query")
     _require_gpu(k_cache, "k_cache")
@@ -320,13 +312,30 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     if out is None:
         out = torch.empty((B, q_len, H, D), dtype=query.dtype, device=dev)
-    status = L.msattn_paged_attention(
-        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
-        k_cache.stride(1), k_cache.stride(2), table.data_ptr(), lens.data_ptr(), out.data_ptr(),
-        workspace.data_ptr(), ws_bytes, B, q_len, H, KVH, D, bs, nb, W, max_context,
-        1 if causal else 0, int(window or 0), float(scale), qcode, kvcode,
-        nat.stream_handle(dev))
-    nat.check("msattn_paged_attention", status)
+    args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+            k_cache.stride(1), k_cache.stride(2), table.data_ptr(), lens.data_ptr(),
+            out.data_ptr(), workspace.data_ptr(), ws_bytes, B, q_len, H, KVH, D, bs, nb, W,
+            max_context, 1 if causal else 0, int(window or 0), float(scale), qcode, kvcode)
+    if rope is None:
+        status = L.msattn_paged_attention(*args, nat.stream_handle(dev))
+        nat.check("msattn_paged_attention", status)
+        return out
+    if q_len != 1:
+        raise ValueError("RoPE inside the kernel is decode-only (q_len == 1)")
+    cos, sin, position = rope
+    cos = torch.as_tensor(cos, device=dev).to(torch.float32).contiguous()
+    sin = torch.as_tensor(sin, device=dev).to(torch.float32).contiguous()
+    if cos.ndim != 2 or cos.shape != sin.shape or cos.shape[1] != D:
+        raise ValueError(f"cos/sin must be [max_pos, {D}] and of one shape")
+    pos = torch.as_tensor(position, device=dev).reshape(-1).to(torch.int32)
+    if pos.numel() == 1 and B > 1:
+        pos = pos.expand(B)
+    pos = pos[:B].contiguous()
+    if pos.numel() != B:
+        raise ValueError(f"position has {pos.numel()} entries for a batch of {B}")
+    status = L.msattn_paged_attention_rope(*args, cos.data_ptr(), sin.data_ptr(), pos.data_ptr(),
+                                           cos.shape[0], nat.stream_handle(dev))
+    nat.check("msattn_paged_attention_rope", status)
     return out
 
 

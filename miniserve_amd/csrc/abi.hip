@@ -184,15 +184,25 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
   return L.total();
 }
 
-int msattn_paged_attention_partials(const void* query, const void* k_cache, const void* v_cache,
-                                    int64_t cache_block_stride, int64_t cache_slot_stride,
-                                    int64_t cache_head_stride, const int32_t* block_table,
-                                    const int32_t* context_lens, void* workspace,
-                                    size_t workspace_bytes, int batch, int q_len, int num_heads,
-                                    int num_kv_heads, int head_dim, int block_size,
-                                    int num_blocks, int table_width, int max_context, int causal,
-                                    int window, float scale, int q_dtype, int kv_dtype,
-                                    void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Optional query RoPE of the decode entry point (null cos: none).
+struct RopeArgs {
+  const float* cos;
+  const float* sin;
+  const int32_t* pos;
+  int max_pos;
+};
+
+int partials_impl(const void* query, const void* k_cache, const void* v_cache,
+                  int64_t cache_block_stride, int64_t cache_slot_stride,
+                  int64_t cache_head_stride, const int32_t* block_table,
+                  const int32_t* context_lens, void* workspace, size_t workspace_bytes, int batch,
+                  int q_len, int num_heads, int num_kv_heads, int head_dim, int block_size,
+                  int num_blocks, int table_width, int max_context, int causal, int window,
+                  float scale, int q_dtype, int kv_dtype, const RopeArgs& rope, void* stream) {
   if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
     return MSATTN_ERR_INVALID_ARG;
@@ -245,6 +255,10 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
   p.sk_group = 1;
   p.sk_unit_groups = 0;
   p.sk_min_chunk = kSkMinChunk;
+  p.rope_cos = rope.cos;
+  p.rope_sin = rope.sin;
+  p.rope_pos = rope.pos;
+  p.rope_max_pos = rope.max_pos;
   const int64_t gx = static_cast<int64_t>(p.max_parts) * num_kv_heads * p.rtiles;
   if (gx >= (int64_t(1) << 31) || batch > 65535) return MSATTN_ERR_UNSUPPORTED;
 
@@ -275,6 +289,26 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
   }
   if (!sup) return MSATTN_ERR_UNSUPPORTED;
   return hip_status(e);
+}
+
+}  // namespace
+
+extern "C" {
+
+int msattn_paged_attention_partials(const void* query, const void* k_cache, const void* v_cache,
+                                    int64_t cache_block_stride, int64_t cache_slot_stride,
+                                    int64_t cache_head_stride, const int32_t* block_table,
+                                    const int32_t* context_lens, void* workspace,
+                                    size_t workspace_bytes, int batch, int q_len, int num_heads,
+                                    int num_kv_heads, int head_dim, int block_size,
+                                    int num_blocks, int table_width, int max_context, int causal,
+                                    int window, float scale, int q_dtype, int kv_dtype,
+                                    void* stream) {
+  return partials_impl(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                       cache_head_stride, block_table, context_lens, workspace, workspace_bytes,
+                       batch, q_len, num_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                       table_width, max_context, causal, window, scale, q_dtype, kv_dtype,
+                       RopeArgs{nullptr, nullptr, nullptr, 0}, stream);
 }
 
 int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
@@ -367,11 +401,37 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
     if (!sup) return MSATTN_ERR_UNSUPPORTED;
     return hip_status(e);
   }
-  const int rc = msattn_paged_attention_partials(
+  const int rc = partials_impl(
       query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
       block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
       num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
-      scale, q_dtype, kv_dtype, stream);
+      scale, q_dtype, kv_dtype, RopeArgs{nullptr, nullptr, nullptr, 0}, stream);
+  if (rc != MSATTN_OK) return rc;
+  return msattn_merge_partials(workspace, workspace_bytes, context_lens, out, batch, q_len,
+                               num_heads, num_kv_heads, head_dim, max_context, q_dtype, stream);
+}
+
+int msattn_paged_attention_rope(const void* query, const void* k_cache, const void* v_cache,
+                                int64_t cache_block_stride, int64_t cache_slot_stride,
+                                int64_t cache_head_stride, const int32_t* block_table,
+                                const int32_t* context_lens, void* out, void* workspace,
+                                size_t workspace_bytes, int batch, int q_len, int num_heads,
+                                int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                                int table_width, int max_context, int causal, int window,
+                                float scale, int q_dtype, int kv_dtype, const float* rope_cos,
+                                const float* rope_sin, const int32_t* position,
+                                int max_position, void* stream) {
+  if (!out || !rope_cos || !rope_sin || !position || max_position <= 0)
+    return MSATTN_ERR_INVALID_ARG;
+  if (!aligned(rope_cos, 16) || !aligned(rope_sin, 16) || !aligned(position, 4))
+    return MSATTN_ERR_INVALID_ARG;
+  if (!dtype_ok(q_dtype) || !aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
+  if (q_len != 1 || head_dim % 2) return MSATTN_ERR_UNSUPPORTED;  // decode-only, as the reference
+  const int rc = partials_impl(
+      query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
+      block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
+      num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
+      scale, q_dtype, kv_dtype, RopeArgs{rope_cos, rope_sin, position, max_position}, stream);
   if (rc != MSATTN_OK) return rc;
   return msattn_merge_partials(workspace, workspace_bytes, context_lens, out, batch, q_len,
                                num_heads, num_kv_heads, head_dim, max_context, q_dtype, stream);

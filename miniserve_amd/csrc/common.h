@@ -92,6 +92,13 @@ template <> struct Elt<fp8_t> {
   __device__ static void store(fp8_t* p, float v) { p->bits = f32_to_fp8e4m3(v); }
 };
 
+// Round an fp32 value to T's precision and back (identity for float).
+template <typename T> __device__ __forceinline__ float round_to(float v) {
+  T t;
+  Elt<T>::store(&t, v);
+  return Elt<T>::load(&t);
+}
+
 // Unpack one 16-byte chunk (four dwords) of KV elements into fp32.
 template <typename T> struct Chunk;
 template <> struct Chunk<float> {
@@ -111,6 +118,15 @@ template <> struct Chunk<bf16_t> {
       o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
   }
+  // Eight fp32 values to one chunk, rounded like Elt<bf16_t>::store.
+  __device__ static uint4 pack(const float* f) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(f32_to_bf16_bits(f[2 * i])) |
+             (static_cast<uint32_t>(f32_to_bf16_bits(f[2 * i + 1])) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
 };
 template <> struct Chunk<_Float16> {
   static constexpr int kElems = 8;
@@ -123,6 +139,14 @@ template <> struct Chunk<_Float16> {
       o[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
       o[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
     }
+  }
+  __device__ static uint4 pack(const float* f) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f[2 * i]))) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f[2 * i + 1]))) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
   }
 };
 template <> struct Chunk<fp8_t> {

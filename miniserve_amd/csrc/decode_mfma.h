@@ -114,6 +114,37 @@ __host__ __device__ constexpr int tile_token(int i) {
   return TPI * (r / APR) + g * APR + (r % APR);
 }
 
+// Rotate-half RoPE on one query row held as MFMA B-operand chunks: chunk j holds
+// dims (4j + g) * 8 .. +7, and its partner (dims -/+ D/2) is chunk j +/- JD/2 of the
+// same lane. The rotated row is rounded back to T, as the unfused
+// (q * cos + rotate_half(q) * sin).to(T) of miniserve/attention.py:41-62 /
+// kernels/paged_attn_triton.py:211-220 would be.
+template <typename T, int D>
+__device__ __forceinline__ void rope_chunks(uint4 (&qb)[D / 32], const float* cs, const float* sn,
+                                            int g) {
+  constexpr int JD = D / 32;
+  float q[JD][8];
+#pragma unroll
+  for (int j = 0; j < JD; ++j) Chunk<T>::unpack(qb[j], q[j]);
+#pragma unroll
+  for (int j = 0; j < JD; ++j) {
+    const int d0 = (4 * j + g) * 8;
+    const float4 c0 = *reinterpret_cast<const float4*>(cs + d0);
+    const float4 c1 = *reinterpret_cast<const float4*>(cs + d0 + 4);
+    const float4 s0 = *reinterpret_cast<const float4*>(sn + d0);
+    const float4 s1 = *reinterpret_cast<const float4*>(sn + d0 + 4);
+    const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float r = j < JD / 2 ? -q[j + JD / 2][e] : q[j - JD / 2][e];
+      o[e] = rope_mix(q[j][e], r, c[e], sv[e]);
+    }
+    qb[j] = Chunk<T>::pack(o);
+  }
+}
+
 template <typename T, int D, int RT>
 __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitParams p) {
   static_assert(D == 64 || D == 128, "MFMA decode handles head_dim 64 and 128");
@@ -219,6 +250,10 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     for (int j = 0; j < JD; ++j) {
       qb[j] = make_uint4(0u, 0u, 0u, 0u);
       if (n < nrows) qb[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + (4 * j + g) * 8);
+    }
+    if (p.rope_cos != nullptr && n < nrows) {
+      const int64_t po = static_cast<int64_t>(rope_position(p, b)) * D;
+      rope_chunks<T, D>(qb, p.rope_cos + po, p.rope_sin + po, g);
     }
   }
 

@@ -182,6 +182,10 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
         qb[j] = make_uint4(0u, 0u, 0u, 0u);
         if (n < nrows) qb[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + (4 * j + g) * 8);
       }
+      if (p.rope_cos != nullptr && n < nrows) {
+        const int64_t po = static_cast<int64_t>(rope_position(p, b)) * D;
+        rope_chunks<T, D>(qb, p.rope_cos + po, p.rope_sin + po, g);
+      }
     }
 
     float m_run = -INFINITY;

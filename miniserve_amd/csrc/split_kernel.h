@@ -72,7 +72,30 @@ struct SplitParams {
   int sk_group;        // stream-K: KV-head units per unit group
   int sk_unit_groups;  // stream-K: number of unit groups
   int sk_min_chunk;    // stream-K: smallest chunk (tiles)
+  // Optional rotate-half RoPE of the query at position rope_pos[b] (decode):
+  // q' = q * cos[pos] + rotate_half(q) * sin[pos], fp32 tables [rope_max_pos, D].
+  const float* rope_cos;  // nullptr: no RoPE
+  const float* rope_sin;
+  const int32_t* rope_pos;
+  int rope_max_pos;
 };
+
+// Position of row b's query for RoPE, clamped into the tables.
+__device__ __forceinline__ int rope_position(const SplitParams& p, int b) {
+  int pos = p.rope_pos[b];
+  pos = pos < 0 ? 0 : (pos >= p.rope_max_pos ? p.rope_max_pos - 1 : pos);
+  return pos;
+}
+
+// q * c + r * s in fp32 with every product and sum rounded on its own (contraction
+// into a fused multiply-add is switched off here), the evaluation of (q * cos + rotate_half(q) * sin) as separate
+// elementwise tensor ops.
+__device__ __forceinline__ float rope_mix(float q, float r, float c, float s) {
+#pragma clang fp contract(off)
+  const float a = q * c;
+  const float b = r * s;
+  return a + b;
+}
 
 template <typename QT, typename KT, int D, int RT>
 __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams p) {
@@ -192,8 +215,22 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
       for (int e = 0; e < EPL; ++e) qreg[r][e] = 0.0f;
       if (r < nrows && c_ok) {
         const QT* src = qp + orow[r] * D + c * EPL;
+        float qv[EPL];
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) qreg[r][e] = Elt<QT>::load(src + e) * p.scale_log2;
+        for (int e = 0; e < EPL; ++e) qv[e] = Elt<QT>::load(src + e);
+        if (p.rope_cos != nullptr) {  // rotate-half RoPE, rounded back to QT
+          const int64_t po = static_cast<int64_t>(rope_position(p, b)) * D;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) {
+            const int d = c * EPL + e;
+            const bool lo_half = d < D / 2;
+            const float partner = Elt<QT>::load(qp + orow[r] * D + (lo_half ? d + D / 2 : d - D / 2));
+            qv[e] = round_to<QT>(rope_mix(qv[e], lo_half ? -partner : partner, p.rope_cos[po + d],
+                                          p.rope_sin[po + d]));
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) qreg[r][e] = qv[e] * p.scale_log2;
       }
     }
   }

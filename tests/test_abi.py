@@ -99,6 +99,22 @@ def test_paged_attention_argument_errors(over, status):
     assert nat.lib().msattn_paged_attention(*args) == status
 
 
+@pytest.mark.parametrize("over,rope,status", [
+    (dict(), (None, 1, 1, 8), nat.ERR_INVALID_ARG),         # no cos table
+    (dict(), (1, 1, 1, 0), nat.ERR_INVALID_ARG),            # empty tables
+    (dict(), (2, 1, 1, 8), nat.ERR_INVALID_ARG),            # cos not 16-byte aligned
+    (dict(q_len=2), (1, 1, 1, 8), nat.ERR_UNSUPPORTED),     # decode-only
+])
+def test_rope_entry_argument_errors(over, rope, status):
+    """msattn_paged_attention_rope rejects bad RoPE arguments before any HIP call."""
+    buf, args = _attn_args(**over)
+    base = (ctypes.addressof(buf) + 15) // 16 * 16
+    ptr = lambda x: None if x is None else base + (0 if x == 1 else x)
+    cos, sin, pos, max_pos = ptr(rope[0]), ptr(rope[1]), ptr(rope[2]), rope[3]
+    assert nat.lib().msattn_paged_attention_rope(*args[:-1], cos, sin, pos, max_pos,
+                                                 None) == status
+
+
 def test_check_maps_status_to_exceptions():
     with pytest.raises(ValueError, match="workspace too small"):
         nat.check("f", nat.ERR_WORKSPACE)

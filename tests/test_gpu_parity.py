@@ -188,6 +188,67 @@ def test_triton_flash_backend_and_rope(device):
     assert (got.cpu() - ref).abs().max().item() < 1e-4
 
 
+def rope_tables(max_pos, D, base=10000.0):
+    inv = 1.0 / (base ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    emb = torch.outer(torch.arange(max_pos, dtype=torch.float32), inv)
+    emb = torch.cat([emb, emb], dim=-1)
+    return torch.cos(emb), torch.sin(emb)
+
+
+def rope_unfused(q, cos, sin, pos):
+    """(q * cos + rotate_half(q) * sin).to(q.dtype) per row, every op rounded in fp32
+    (miniserve/attention.py:41-62)."""
+    D = q.shape[-1]
+    qf = q.float()
+    rot = torch.cat([-qf[..., D // 2:], qf[..., : D // 2]], dim=-1)
+    cs = cos[pos][:, None, None, :]
+    sn = sin[pos][:, None, None, :]
+    return (qf * cs + rot * sn).to(q.dtype)
+
+
+@pytest.mark.parametrize("H,KVH,D,dtype,kv_dtype,wide", [
+    (32, 8, 128, torch.bfloat16, torch.bfloat16, True),    # stream-K MFMA kernel
+    (14, 2, 64, torch.bfloat16, torch.bfloat16, False),    # partition MFMA kernel
+    (28, 4, 128, torch.float16, torch.float16, False),     # partition MFMA kernel, fp16
+    (4, 2, 64, torch.float32, torch.float32, False),       # generic kernel, fp32
+    (8, 2, 96, torch.bfloat16, torch.float8_e4m3fn, False),  # generic kernel, fp8 KV
+])
+def test_rope_in_kernel_matches_unfused(device, H, KVH, D, dtype, kv_dtype, wide):
+    """RoPE applied inside the decode kernels equals attention over the query rotated
+    beforehand (tests/test_triton_parity.py:71-81 asks 1e-4; here bit-exact), and the
+    float64 oracle over the rotated query."""
+    note(f"rope H={H} KVH={KVH} D={D} {dtype} kv={kv_dtype} wide={wide}")
+    lens = [1, 300, 77, 1234, 16, 999]
+    width = 65536 // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
+    q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=D + H)
+    if kv_dtype != dtype:
+        kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+    cos, sin = rope_tables(max(lens) + 8, D)
+    pos = torch.tensor([L - 1 for L in lens])
+    cap = width * 16
+    fused = paged_attention(q.to(device), kc.to(device), vc.to(device), table, lens,
+                            max_context=cap, rope=(cos.to(device), sin.to(device), pos.to(device)))
+    qr = rope_unfused(q, cos, sin, pos)
+    unfused = paged_attention(qr.to(device), kc.to(device), vc.to(device), table, lens,
+                              max_context=cap)
+    assert torch.equal(fused, unfused)
+    ref = dense.paged_attention_f64(qr, kc, vc, table, lens)
+    assert rel_err(fused, ref) < (1e-4 if dtype == torch.float32 else BF16_REL)
+
+
+def test_rope_contract(device):
+    """Decode-only, as the reference's fused path; malformed tables are rejected."""
+    q, kc, vc, table, _ = scenario(4, 2, 64, [40], block_size=16)
+    cos, sin = rope_tables(64, 64)
+    args = (q.to(device), kc.to(device), vc.to(device), table, [40])
+    pos = torch.tensor([39], device=device)
+    q2 = torch.zeros(1, 2, 4, 64, device=device)
+    with pytest.raises(ValueError, match="decode-only"):
+        paged_attention(q2, *args[1:], rope=(cos.to(device), sin.to(device), pos))
+    with pytest.raises(ValueError, match="max_pos"):
+        paged_attention(*args, rope=(cos[:, :32].to(device), sin[:, :32].to(device), pos))
+
+
 def test_shape_fuzz_50(device):
     """Seeds 1000+i as tests/test_triton_parity.py:110-123, HIP vs float64 oracle."""
     for i in range(50):
