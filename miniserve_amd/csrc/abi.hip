@@ -218,10 +218,13 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
 
   const int G = num_heads / num_kv_heads;
   const int rows = q_len * G;
-  // MFMA path: bf16/fp16 KV read by a same-typed query, head_dim 64 or 128, pages
-  // holding whole 16-token tiles. Everything else takes the generic kernel.
-  const bool use_mfma = q_dtype == kv_dtype && (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
-                        (head_dim == 64 || head_dim == 128) && block_size % 16 == 0;
+  // MFMA path: a bf16/fp16 query over a KV cache of its own type or of fp8 e4m3,
+  // head_dim 64 or 128, pages holding whole 16-token tiles. Everything else takes
+  // the generic kernel.
+  const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
+  const bool use_mfma = (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
+                        (kv_dtype == q_dtype || kv_fp8) && (head_dim == 64 || head_dim == 128) &&
+                        block_size % 16 == 0;
   const int RT = use_mfma ? mfma_rows_per_tile(rows) : rows_per_tile(rows);
   char* ws = static_cast<char*>(workspace);
   SplitParams p;
@@ -275,15 +278,21 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
     p.sk_group = largest_pow2_divisor_upto(units, kSkWaves);
     p.sk_unit_groups = units / p.sk_group;
     const int grid = device_cus() < kSkGrid ? device_cus() : kSkGrid;
-    if (q_dtype == MSATTN_BF16) e = launch_decode_streamk<bf16_t>(p, head_dim, RT, grid, st, &sup);
-    else e = launch_decode_streamk<_Float16>(p, head_dim, RT, grid, st, &sup);
+    if (q_dtype == MSATTN_BF16)
+      e = kv_fp8 ? launch_decode_streamk<bf16_t, fp8_t>(p, head_dim, RT, grid, st, &sup)
+                 : launch_decode_streamk<bf16_t, bf16_t>(p, head_dim, RT, grid, st, &sup);
+    else
+      e = kv_fp8 ? launch_decode_streamk<_Float16, fp8_t>(p, head_dim, RT, grid, st, &sup)
+                 : launch_decode_streamk<_Float16, _Float16>(p, head_dim, RT, grid, st, &sup);
     if (!sup) return MSATTN_ERR_UNSUPPORTED;
     return hip_status(e);
   }
   if (use_mfma && q_dtype == MSATTN_BF16) {
-    e = launch_decode_mfma<bf16_t>(p, head_dim, RT, st, &sup);
+    e = kv_fp8 ? launch_decode_mfma<bf16_t, fp8_t>(p, head_dim, RT, st, &sup)
+               : launch_decode_mfma<bf16_t, bf16_t>(p, head_dim, RT, st, &sup);
   } else if (use_mfma) {
-    e = launch_decode_mfma<_Float16>(p, head_dim, RT, st, &sup);
+    e = kv_fp8 ? launch_decode_mfma<_Float16, fp8_t>(p, head_dim, RT, st, &sup)
+               : launch_decode_mfma<_Float16, _Float16>(p, head_dim, RT, st, &sup);
   } else {
     e = dispatch_split(p, q_dtype, kv_dtype, head_dim, RT, st, &sup);
   }

@@ -100,6 +100,60 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+typedef float mf_f32x2 __attribute__((ext_vector_type(2)));
+
+// Eight consecutive K/V elements per lane. A cache of the compute type T loads 16
+// bytes; an fp8 (OCP e4m3) cache loads 8 bytes, kept raw while in flight and
+// widened once they arrive. The widening is exact (every e4m3 value is a bf16 and
+// an fp16 value), so an fp8 cache gives the result of the same kernel run on the
+// cache converted to T beforehand (miniserve/attention.py:168-170, then .to(q.dtype)).
+template <typename T, typename KT> struct Kv8;
+template <typename T> struct Kv8<T, T> {
+  typedef uint4 raw_t;
+  template <int AUX>
+  __device__ static raw_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return buffer_load16<AUX>(r, off);
+  }
+  __device__ static uint4 operand(const raw_t& x) { return x; }         // 8 x T, packed
+  __device__ static void unpack(const raw_t& x, float* o) { Chunk<T>::unpack(x, o); }
+  __device__ static raw_t keep_if(const raw_t& x, bool keep) {
+    return keep ? x : make_uint4(0u, 0u, 0u, 0u);
+  }
+};
+template <typename T> struct Kv8<T, fp8_t> {
+  typedef uint2 raw_t;
+  template <int AUX>
+  __device__ static raw_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, AUX);
+    return make_uint2(v.x, v.y);
+  }
+  // bytes 0..7 -> fp32 pairs (v_cvt_pk_f32_fp8, OCP e4m3 on gfx950)
+  __device__ static void unpack(const raw_t& x, float* o) {
+    const mf_f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(x.x), false);
+    const mf_f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(x.x), true);
+    const mf_f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(x.y), false);
+    const mf_f32x2 d = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(x.y), true);
+    o[0] = a.x; o[1] = a.y; o[2] = b.x; o[3] = b.y;
+    o[4] = c.x; o[5] = c.y; o[6] = d.x; o[7] = d.y;
+  }
+  // bytes 0..7 -> eight T values (v_cvt_scalef32_pk_{bf16,f16}_fp8 with scale 1: exact)
+  __device__ static uint4 operand(const raw_t& x) {
+    return make_uint4(widen2<false>(x.x), widen2<true>(x.x), widen2<false>(x.y),
+                      widen2<true>(x.y));
+  }
+  template <bool HI>  // bytes 2, 3 of w when HI, else bytes 0, 1
+  __device__ static uint32_t widen2(uint32_t w) {
+    if constexpr (std::is_same<T, bf16_t>::value)
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+    else
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+  }
+  __device__ static raw_t keep_if(const raw_t& x, bool keep) {
+    return keep ? x : make_uint2(0u, 0u);
+  }
+};
+
 constexpr int kMfmaWaves = MSATTN_MFMA_WAVES;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
 constexpr int kMaxTilesPerWave = kPartMax / 16 / kMfmaWaves;  // partitions are <= kPartMax tokens
@@ -145,8 +199,10 @@ __device__ __forceinline__ void rope_chunks(uint4 (&qb)[D / 32], const float* cs
   }
 }
 
-template <typename T, int D, int RT>
+template <typename T, typename KT, int D, int RT>
 __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitParams p) {
+  typedef Kv8<T, KT> KV;
+  typedef typename KV::raw_t raw_t;
   static_assert(D == 64 || D == 128, "MFMA decode handles head_dim 64 and 128");
   static_assert(RT >= 1 && RT <= 16, "at most 16 query rows per tile");
   constexpr int JD = D / 32;        // MFMAs per tile
@@ -258,17 +314,17 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   }
 
   // Per-lane byte offsets inside a tile (32-bit: a tile spans 16 slots).
-  constexpr int EB = static_cast<int>(sizeof(T));
+  constexpr int EB = static_cast<int>(sizeof(KT));
   const uint32_t k_lane_off =
-      static_cast<uint32_t>((tile_token<D>(n) * p.slot_stride + g * 8) * EB);  // + 64*j
+      static_cast<uint32_t>((tile_token<D>(n) * p.slot_stride + g * 8) * EB);  // + 32*EB*j
   uint32_t v_lane_off[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
     v_lane_off[j] = static_cast<uint32_t>(((TPI * j + va) * p.slot_stride + vc * 8) * EB);
   const int tile_bytes = static_cast<int>((15 * p.slot_stride + D) * EB);
 
-  const T* kbase = static_cast<const T*>(p.k);
-  const T* vbase = static_cast<const T*>(p.v);
+  const KT* kbase = static_cast<const KT*>(p.k);
+  const KT* vbase = static_cast<const KT*>(p.v);
 
   float m_run = -INFINITY;
   float l_run = 0.0f;
@@ -285,21 +341,21 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
     return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
   };
-  auto issue = [&](int64_t base, uint4 (&kb)[JD], uint4 (&vb)[NJ]) {
+  auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) {
     const bool ok = base >= 0;
     const int64_t b0 = ok ? base : 0;
     const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
     const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
 #pragma unroll
-    for (int j = 0; j < JD; ++j) kb[j] = buffer_load16(rk, k_lane_off + 64 * j);
+    for (int j = 0; j < JD; ++j) kb[j] = KV::template load<0>(rk, k_lane_off + 32 * EB * j);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) vb[j] = buffer_load16(rv, v_lane_off[j]);
+    for (int j = 0; j < NJ; ++j) vb[j] = KV::template load<0>(rv, v_lane_off[j]);
   };
 
-  auto consume = [&](int k, const uint4 (&kb)[JD], const uint4 (&vb)[NJ], int64_t base) {
+  auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) {
     mf_f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < JD; ++j) s = Mfma16<T>::mac(kb[j], qb[j], s);
+    for (int j = 0; j < JD; ++j) s = Mfma16<T>::mac(KV::operand(kb[j]), qb[j], s);
     const int t0 = (tw0 + k) * 16;
     const bool hole = base < 0;
     float sc[4];
@@ -341,16 +397,12 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       float vf[8];
-      uint4 vv = vb[j];
+      raw_t vv = vb[j];
       if (partial) {  // wave-uniform branch; per-lane selects inside
         const int vtok = t0 + TPI * j + va;
-        const bool keep = vtok >= a0 && vtok < a1;
-        vv.x = keep ? vv.x : 0u;
-        vv.y = keep ? vv.y : 0u;
-        vv.z = keep ? vv.z : 0u;
-        vv.w = keep ? vv.w : 0u;
+        vv = KV::keep_if(vv, vtok >= a0 && vtok < a1);
       }
-      Chunk<T>::unpack(vv, vf);
+      KV::unpack(vv, vf);
       static_for<RT>([&](auto nc) {
         constexpr int rn = decltype(nc)::value;
         float pb;
@@ -370,7 +422,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   // Two tiles in flight. The sequence is fully unrolled (a wave owns at most
   // kMaxTilesPerWave tiles) so every wait for a tile's loads is exact; a load for
   // tile nt reads nothing (its descriptor has no records).
-  uint4 k0[JD], v0[NJ], k1[JD], v1[NJ];
+  raw_t k0[JD], v0[NJ], k1[JD], v1[NJ];
   int64_t base0 = tile_base(0);
   issue(base0, k0, v0);
 #pragma unroll
@@ -453,25 +505,29 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   }
 }
 
-template <typename T, int D, int RT>
+template <typename T, typename KT, int D, int RT>
 hipError_t launch_decode_mfma_one(const SplitParams& p, hipStream_t stream) {
   const unsigned gx = static_cast<unsigned>(p.max_parts) * static_cast<unsigned>(p.KVH) *
                       static_cast<unsigned>(p.rtiles);
-  hipLaunchKernelGGL((decode_mfma_kernel<T, D, RT>), dim3(gx, 1, static_cast<unsigned>(p.batch)),
-                     dim3(kMfmaThreads), 0, stream, p);
+  hipLaunchKernelGGL((decode_mfma_kernel<T, KT, D, RT>),
+                     dim3(gx, 1, static_cast<unsigned>(p.batch)), dim3(kMfmaThreads), 0, stream, p);
   return hipGetLastError();
 }
 
-// Launch for T in {bf16_t, _Float16}; *supported = false when (D, RT) is not compiled.
-template <typename T>
+// Launch for T in {bf16_t, _Float16} and a KV cache of T or of fp8_t;
+// *supported = false when (D, RT) is not compiled.
+template <typename T, typename KT>
 hipError_t launch_decode_mfma(const SplitParams& p, int D, int RT, hipStream_t stream,
                               bool* supported);
 
-template <>
-hipError_t launch_decode_mfma<bf16_t>(const SplitParams& p, int D, int RT, hipStream_t stream,
-                                      bool* supported);
-template <>
-hipError_t launch_decode_mfma<_Float16>(const SplitParams& p, int D, int RT, hipStream_t stream,
-                                        bool* supported);
+#define MSATTN_DECLARE_MFMA_LAUNCHER(T, KT)                                                  \
+  template <>                                                                                \
+  hipError_t launch_decode_mfma<T, KT>(const SplitParams& p, int D, int RT, hipStream_t stream, \
+                                       bool* supported);
+MSATTN_DECLARE_MFMA_LAUNCHER(bf16_t, bf16_t)
+MSATTN_DECLARE_MFMA_LAUNCHER(_Float16, _Float16)
+MSATTN_DECLARE_MFMA_LAUNCHER(bf16_t, fp8_t)
+MSATTN_DECLARE_MFMA_LAUNCHER(_Float16, fp8_t)
+#undef MSATTN_DECLARE_MFMA_LAUNCHER
 
 }  // namespace msattn

@@ -1,0 +1,26 @@
+// Launcher bodies of the MFMA partition decode kernel, one per (query type, KV
+// type), expanded by the instantiation files.
+#pragma once
+
+#include "decode_mfma.h"
+
+#define MSATTN_MFMA_RT(T, KT, D)                                              \
+  switch (RT) {                                                               \
+    case 1: return launch_decode_mfma_one<T, KT, D, 1>(p, stream);            \
+    case 2: return launch_decode_mfma_one<T, KT, D, 2>(p, stream);            \
+    case 4: return launch_decode_mfma_one<T, KT, D, 4>(p, stream);            \
+    case 8: return launch_decode_mfma_one<T, KT, D, 8>(p, stream);            \
+    case 16: return launch_decode_mfma_one<T, KT, D, 16>(p, stream);          \
+    default: break;                                                           \
+  }
+
+#define MSATTN_MFMA_LAUNCHER(T, KT)                                                          \
+  template <>                                                                                \
+  hipError_t launch_decode_mfma<T, KT>(const SplitParams& p, int D, int RT, hipStream_t stream, \
+                                       bool* supported) {                                    \
+    *supported = true;                                                                       \
+    if (D == 64) { MSATTN_MFMA_RT(T, KT, 64) }                                               \
+    if (D == 128) { MSATTN_MFMA_RT(T, KT, 128) }                                             \
+    *supported = false;                                                                      \
+    return hipSuccess;                                                                       \
+  }

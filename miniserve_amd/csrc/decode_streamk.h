@@ -33,25 +33,36 @@ constexpr int kSkWaves = 8;
 constexpr int kSkThreads = kSkWaves * kWave;
 constexpr int kSkMaxBatch = 4096;   // sequences per launch on this path
 constexpr int kSkTableRun = 64;     // tile page ids fetched per table load
-#ifndef MSATTN_SK_UNROLL
-#define MSATTN_SK_UNROLL 2
+// Tiles whose loads are in flight per wave (ring depth) for 2-byte and for fp8
+// caches, and ring turns per loop iteration.
+#ifndef MSATTN_SK_DEPTH
+#define MSATTN_SK_DEPTH 2
 #endif
-constexpr int kSkUnroll = MSATTN_SK_UNROLL;  // tiles per loop iteration (even)
+#ifndef MSATTN_SK_DEPTH_FP8
+#define MSATTN_SK_DEPTH_FP8 4
+#endif
+#ifndef MSATTN_SK_ROUNDS
+#define MSATTN_SK_ROUNDS 1
+#endif
 
 // Pieces a launch can produce: one per chunk plus one per segment boundary.
 __host__ __device__ constexpr int64_t streamk_pieces(int64_t n_chunks, int64_t n_segments) {
   return n_chunks + n_segments;
 }
 
-template <typename T, int D, int RT>
+template <typename T, typename KT, int D, int RT>
 __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitParams p) {
+  typedef Kv8<T, KT> KV;
+  typedef typename KV::raw_t raw_t;
+  constexpr int DEPTH = sizeof(KT) == 1 ? MSATTN_SK_DEPTH_FP8 : MSATTN_SK_DEPTH;
+  constexpr int STEP = DEPTH * MSATTN_SK_ROUNDS;  // tiles per loop iteration
   static_assert(D == 64 || D == 128, "stream-K decode handles head_dim 64 and 128");
   constexpr int JD = D / 32;
   constexpr int LPR = D / 8;
   constexpr int TPI = 64 / LPR;
   constexpr int NJ = 16 / TPI;
   constexpr int APR = 16 / LPR;
-  constexpr int EB = static_cast<int>(sizeof(T));
+  constexpr int EB = static_cast<int>(sizeof(KT));
 
   __shared__ int s_pre[kSkMaxBatch + 1];  // exclusive prefix of T_b
   __shared__ int s_wsum[kSkWaves];
@@ -138,8 +149,8 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
   int64_t s = r * c;
   const int64_t s_end = min(s + c, total);
 
-  const T* kbase = static_cast<const T*>(p.k);
-  const T* vbase = static_cast<const T*>(p.v);
+  const KT* kbase = static_cast<const KT*>(p.k);
+  const KT* vbase = static_cast<const KT*>(p.v);
   const uint32_t k_lane_tok = static_cast<uint32_t>(tile_token<D>(n));
   const int tile_bytes = static_cast<int>((15 * p.slot_stride + D) * EB);
 
@@ -219,24 +230,25 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
         const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
         return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
       };
-      auto issue = [&](int64_t base, uint4 (&kb)[JD], uint4 (&vb)[NJ]) {
+      auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) {
         const bool ok = base >= 0;
         const int64_t b0 = ok ? base : 0;
         const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
         const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
         const uint32_t koff = (k_lane_tok * static_cast<uint32_t>(p.slot_stride) + g * 8) * EB;
 #pragma unroll
-        for (int j = 0; j < JD; ++j) kb[j] = buffer_load16<MSATTN_LOAD_AUX>(rk, koff + 64 * j);
+        for (int j = 0; j < JD; ++j)
+          kb[j] = KV::template load<MSATTN_LOAD_AUX>(rk, koff + 32 * EB * j);
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-          vb[j] = buffer_load16<MSATTN_LOAD_AUX>(
+          vb[j] = KV::template load<MSATTN_LOAD_AUX>(
               rv, ((static_cast<uint32_t>(TPI * j + va) * static_cast<uint32_t>(p.slot_stride)) +
                    vc * 8) * EB);
       };
-      auto consume = [&](int k, const uint4 (&kb)[JD], const uint4 (&vb)[NJ], int64_t base) {
+      auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) {
         mf_f32x4 sv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < JD; ++j) sv = Mfma16<T>::mac(kb[j], qb[j], sv);
+        for (int j = 0; j < JD; ++j) sv = Mfma16<T>::mac(KV::operand(kb[j]), qb[j], sv);
         const int t0 = (t_first + run0 + k) * 16;
         const bool hole = base < 0;
         float sc[4];
@@ -274,16 +286,12 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           float vf[8];
-          uint4 vv = vb[j];
+          raw_t vv = vb[j];
           if (partial) {
             const int vtok = t0 + TPI * j + va;
-            const bool keep = !hole && vtok >= a0 && vtok < a1;
-            vv.x = keep ? vv.x : 0u;
-            vv.y = keep ? vv.y : 0u;
-            vv.z = keep ? vv.z : 0u;
-            vv.w = keep ? vv.w : 0u;
+            vv = KV::keep_if(vv, !hole && vtok >= a0 && vtok < a1);
           }
-          Chunk<T>::unpack(vv, vf);
+          KV::unpack(vv, vf);
           static_for<RT>([&](auto nc) {
             constexpr int rn = decltype(nc)::value;
             float pb;
@@ -300,21 +308,26 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
         }
       };
 
-      // Tiles in groups of kSkUnroll, two in flight; a tile index >= nt reads nothing
-      // and adds nothing (its descriptor has no records, all its keys are masked).
-      uint4 k0[JD], v0[NJ], k1[JD], v1[NJ];
-      int64_t base0 = tile_base(0);
-      issue(base0, k0, v0);
-      for (int k = 0; k < nt; k += kSkUnroll) {
-#pragma unroll
-        for (int kk = 0; kk < kSkUnroll; kk += 2) {
-          const int64_t base1 = tile_base(k + kk + 1);
-          issue(base1, k1, v1);
-          consume(k + kk, k0, v0, base0);
-          base0 = tile_base(k + kk + 2);
-          issue(base0, k0, v0);
-          consume(k + kk + 1, k1, v1, base1);
-        }
+      // A ring of DEPTH tile buffers: DEPTH - 1 tiles' loads stay in flight while a
+      // tile is consumed, the next tile's loads going into the slot just freed.
+      // A tile index >= nt reads nothing and adds nothing (its descriptor has no
+      // records, all its keys are masked).
+      raw_t kq[DEPTH][JD], vq[DEPTH][NJ];
+      int64_t bq[DEPTH];
+      static_for<DEPTH - 1>([&](auto dc) {
+        constexpr int d = decltype(dc)::value;
+        bq[d] = tile_base(d);
+        issue(bq[d], kq[d], vq[d]);
+      });
+      for (int k = 0; k < nt; k += STEP) {
+        static_for<STEP>([&](auto dc) {
+          constexpr int d = decltype(dc)::value;
+          constexpr int cur = d % DEPTH;
+          constexpr int nxt = (d + DEPTH - 1) % DEPTH;
+          bq[nxt] = tile_base(k + d + DEPTH - 1);
+          issue(bq[nxt], kq[nxt], vq[nxt]);
+          consume(k + d, kq[cur], vq[cur], bq[cur]);
+        });
       }
     }
 
@@ -350,21 +363,48 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
   }
 }
 
-template <typename T, int D, int RT>
+template <typename T, typename KT, int D, int RT>
 hipError_t launch_decode_streamk_one(const SplitParams& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_streamk_kernel<T, D, RT>), dim3(static_cast<unsigned>(grid)),
+  hipLaunchKernelGGL((decode_streamk_kernel<T, KT, D, RT>), dim3(static_cast<unsigned>(grid)),
                      dim3(kSkThreads), 0, stream, p);
   return hipGetLastError();
 }
 
-template <typename T>
+// Launch for T in {bf16_t, _Float16} and a KV cache of T or of fp8_t;
+// *supported = false when (D, RT) is not compiled.
+template <typename T, typename KT>
 hipError_t launch_decode_streamk(const SplitParams& p, int D, int RT, int grid, hipStream_t stream,
                                  bool* supported);
-template <>
-hipError_t launch_decode_streamk<bf16_t>(const SplitParams& p, int D, int RT, int grid,
-                                         hipStream_t stream, bool* supported);
-template <>
-hipError_t launch_decode_streamk<_Float16>(const SplitParams& p, int D, int RT, int grid,
-                                           hipStream_t stream, bool* supported);
+
+#define MSATTN_DECLARE_SK_LAUNCHER(T, KT)                                                    \
+  template <>                                                                                \
+  hipError_t launch_decode_streamk<T, KT>(const SplitParams& p, int D, int RT, int grid,     \
+                                          hipStream_t stream, bool* supported);
+MSATTN_DECLARE_SK_LAUNCHER(bf16_t, bf16_t)
+MSATTN_DECLARE_SK_LAUNCHER(_Float16, _Float16)
+MSATTN_DECLARE_SK_LAUNCHER(bf16_t, fp8_t)
+MSATTN_DECLARE_SK_LAUNCHER(_Float16, fp8_t)
+#undef MSATTN_DECLARE_SK_LAUNCHER
+
+#define MSATTN_SK_RT(T, KT, D)                                                      \
+  switch (RT) {                                                                     \
+    case 1: return launch_decode_streamk_one<T, KT, D, 1>(p, grid, stream);         \
+    case 2: return launch_decode_streamk_one<T, KT, D, 2>(p, grid, stream);         \
+    case 4: return launch_decode_streamk_one<T, KT, D, 4>(p, grid, stream);         \
+    case 8: return launch_decode_streamk_one<T, KT, D, 8>(p, grid, stream);         \
+    case 16: return launch_decode_streamk_one<T, KT, D, 16>(p, grid, stream);       \
+    default: break;                                                                 \
+  }
+
+#define MSATTN_SK_LAUNCHER(T, KT)                                                            \
+  template <>                                                                                \
+  hipError_t launch_decode_streamk<T, KT>(const SplitParams& p, int D, int RT, int grid,     \
+                                          hipStream_t stream, bool* supported) {             \
+    *supported = true;                                                                       \
+    if (D == 64) { MSATTN_SK_RT(T, KT, 64) }                                                 \
+    if (D == 128) { MSATTN_SK_RT(T, KT, 128) }                                               \
+    *supported = false;                                                                      \
+    return hipSuccess;                                                                       \
+  }
 
 }  // namespace msattn

@@ -188,6 +188,35 @@ def test_triton_flash_backend_and_rope(device):
     assert (got.cpu() - ref).abs().max().item() < 1e-4
 
 
+@pytest.mark.parametrize("H,KVH,D,dtype,wide,window", [
+    (32, 8, 128, torch.bfloat16, True, None),    # stream-K kernel
+    (32, 8, 128, torch.bfloat16, True, 200),     # stream-K kernel, sliding window
+    (14, 2, 64, torch.bfloat16, False, None),    # partition kernel
+    (28, 4, 128, torch.float16, False, None),    # partition kernel, fp16 query
+    (28, 4, 128, torch.float16, True, None),     # stream-K kernel, fp16 query
+])
+def test_fp8_kv_mfma_equals_dequantized(device, H, KVH, D, dtype, wide, window):
+    """An fp8 (e4m3fn) cache on the MFMA kernels, widened in registers, gives exactly
+    the result of the same kernels on the cache converted to the query type first
+    (miniserve/attention.py:168-170 then .to(q.dtype)); and the float64 oracle."""
+    note(f"fp8 MFMA H={H} KVH={KVH} D={D} {dtype} wide={wide} window={window}")
+    lens = [0, 1, 17, 300, 1234, 77, 4096, 999]
+    width = 65536 // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
+    q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=D + KVH)
+    kc8, vc8 = kc.to(torch.float8_e4m3fn), vc.to(torch.float8_e4m3fn)
+    kd, vd = kc8.to(dtype), vc8.to(dtype)
+    cap = width * 16
+    qd = q.to(device)
+    got = paged_attention(qd, kc8.to(device), vc8.to(device), table, lens, window=window,
+                          max_context=cap)
+    want = paged_attention(qd, kd.to(device), vd.to(device), table, lens, window=window,
+                           max_context=cap)
+    assert torch.equal(got, want)
+    ref = dense.paged_attention_f64(q, kc8, vc8, table, lens, window=window)
+    assert rel_err(got, ref) < BF16_REL
+    assert not got[0].any()
+
+
 def rope_tables(max_pos, D, base=10000.0):
     inv = 1.0 / (base ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
     emb = torch.outer(torch.arange(max_pos, dtype=torch.float32), inv)
