@@ -1,19 +1,25 @@
 // Chunked-prefill paged attention on MFMA (gfx950): q_len > 1, bf16/fp16, head_dim 128.
 //
-// One workgroup (4 waves) owns 64 query rows of one (sequence b, KV head): rows are
-// the (query token i, GQA head g) pairs r = i * group + g, 16 per wave. It walks the
+// One workgroup (4 waves) owns 16 * RB * 4 query rows of one (sequence b, KV head): rows
+// are the (query token i, GQA head g) pairs r = i * group + g; each wave holds RB blocks of
+// 16 rows, so every K/V operand it reads from LDS feeds RB MFMAs. The workgroup walks the
 // keys its rows may see in steps of 64 tokens (four 16-token page slices):
-//   * the step's K and V rows are staged through LDS (row-major, padded), loaded
-//     one step ahead into registers;
-//   * S^T = K Q^T on v_mfma_f32_16x16x32: A = K rows read from LDS, B = the wave's
-//     query rows kept in registers, so lane (g = l/16, n = l%16) holds the scores
-//     of query row n for tokens 4g .. 4g+3 of each 16-token slice;
-//   * online softmax per row (fp32, base 2), causal / window masks per key;
-//   * O^T += V^T P^T on the same MFMA: B = P^T comes straight from the score
-//     registers (bf16), A = V^T is read transposed from the row-major V rows with
-//     ds_read_b64_tr_b16 (each lane names 4 dims of one token; lane i of a
-//     16-lane group receives dim i of four tokens). Lane (g, n) accumulates
-//     O[row n][dims 16t + 4g + r], so the softmax rescale stays in the lane.
+//   * K and V of a step are staged through LDS, double-buffered: while a step is computed
+//     from one buffer, the next step's rows (loaded into registers one step ahead) go into
+//     the other, so a step needs one barrier;
+//   * S^T = K Q^T on v_mfma_f32_16x16x32: A = K rows read from LDS, B = the wave's query
+//     rows kept in registers, so lane (g = l/16, n = l%16) holds the scores of query row n
+//     for tokens 4g .. 4g+3 of each 16-token slice;
+//   * online softmax per row (fp32, base 2), causal / window masks only on the steps that
+//     cross a row's key range;
+//   * O^T += V^T P^T on the same MFMA: B = P^T comes straight from the score registers,
+//     A = V^T is read transposed from the row-major V rows with ds_read_b64_tr_b16 (each
+//     lane names 4 dims of one token; lane i of a 16-lane group receives dim i of four
+//     tokens). Lane (g, n) accumulates O[row n][dims 16t + 4g + r], so the softmax
+//     rescale stays in the lane.
+// LDS row strides are chosen per access: K rows are 68 dwords apart (4 mod 64 banks: the
+// 16 rows of a 16-byte-per-lane read fall on disjoint banks), V rows 72 dwords (8 mod 64:
+// the 8-byte transposed reads of 8 consecutive rows tile the 64 banks).
 // The rows' outputs are normalised and written directly (no split-K partials).
 //
 // Semantics: PagedAttention.forward with q_len > 1 (miniserve/attention.py:205-250,
@@ -22,13 +28,19 @@
 
 #include "decode_mfma.h"
 
+#ifndef MSATTN_PF_RB
+#define MSATTN_PF_RB 2
+#endif
+
 namespace msattn {
 
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = kPfWaves * kWave;
-constexpr int kPfRows = 16 * kPfWaves;  // query rows per workgroup
-constexpr int kPfStep = 64;             // key tokens per step
-constexpr int kPfPageChunk = 512;       // page ids cached in LDS at a time
+constexpr int kPfRB = MSATTN_PF_RB;             // 16-row blocks per wave
+constexpr int kPfRows = 16 * kPfRB * kPfWaves;  // query rows per workgroup
+constexpr int kPfStep = 64;                     // key tokens per step
+constexpr int kPfPageChunk = 512;               // page ids cached in LDS at a time
+constexpr float kPfRescaleSlack = 8.0f;         // base-2 headroom before the max moves
 
 typedef short pf_s4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) pf_s4 lds_s4;  // an LDS pointer target
@@ -69,18 +81,21 @@ template <> struct Pack2<_Float16> {
   }
 };
 
-template <typename T, int D>
+template <typename T, int D, int RB>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillParams p) {
   static_assert(D == 128, "prefill MFMA kernel handles head_dim 128");
   constexpr int JD = D / 32;              // k-steps of S^T
   constexpr int ND = D / 16;              // 16-dim tiles of O^T
-  constexpr int RS = D + 8;               // LDS row stride (elements): 16 B of padding
+  constexpr int RSK = D + 8;              // K LDS row stride (elements): 68 dwords
+  constexpr int RSV = D + 16;             // V LDS row stride (elements): 72 dwords
   constexpr int CPR = D * 2 / 16;         // 16-byte chunks per K/V row
   constexpr int LPT = kPfStep * CPR / kPfThreads;  // chunks per thread per tensor per step
   static_assert(LPT * kPfThreads == kPfStep * CPR, "staging split");
+  constexpr int WROWS = 16 * RB;          // query rows per wave
+  constexpr int BROWS = WROWS * kPfWaves; // query rows per workgroup
 
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[kPfStep * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[kPfStep * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kPfStep * RSK];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kPfStep * RSV];
   __shared__ int s_pg[kPfPageChunk];
 
   const int tid = threadIdx.x;
@@ -97,8 +112,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 
   int ctx = p.lens[b];
   ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
-  const int row0 = rblock * kPfRows;
-  const int rows_here = min(kPfRows, p.rows_per_kvh - row0);
+  const int row0 = rblock * BROWS;
+  const int rows_here = min(BROWS, p.rows_per_kvh - row0);
 
   // Key range of the block (query index grows with the row).
   const int i_first = row0 / p.G;
@@ -106,24 +121,31 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int lo_all = p.window > 0 ? max(0, ctx - p.q_len + i_first - p.window + 1) : 0;
   const int hi_all = p.causal ? min(ctx, ctx - p.q_len + i_last + 1) : ctx;
 
-  // This lane's query row (MFMA column n of the wave's 16 rows).
-  const int row = row0 + w * 16 + n;
-  const bool row_ok = row < p.rows_per_kvh;
-  int lo_n = 0, hi_n = 0;
-  int64_t orow = 0;
-  if (row_ok) {
-    const int i = row / p.G;
-    const int qpos = ctx - p.q_len + i;
-    hi_n = p.causal ? min(ctx, qpos + 1) : ctx;
-    lo_n = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
-    if (hi_n < lo_n) hi_n = lo_n;
-    orow = (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
+  // This lane's query rows (MFMA column n of each of the wave's row blocks).
+  bool row_ok[RB];
+  int lo_n[RB], hi_n[RB];
+  int64_t orow[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int row = row0 + w * WROWS + rb * 16 + n;
+    row_ok[rb] = row < p.rows_per_kvh;
+    lo_n[rb] = 0;
+    hi_n[rb] = 0;
+    orow[rb] = 0;
+    if (row_ok[rb]) {
+      const int i = row / p.G;
+      const int qpos = ctx - p.q_len + i;
+      hi_n[rb] = p.causal ? min(ctx, qpos + 1) : ctx;
+      lo_n[rb] = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
+      if (hi_n[rb] < lo_n[rb]) hi_n[rb] = lo_n[rb];
+      orow[rb] = (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
+    }
   }
   // Keys every row of this wave sees: [wave_lo, wave_hi) (rows grow with the query).
   int wave_lo = 0, wave_hi = 0;
   {
-    const int wr0 = row0 + w * 16;
-    const int wr1 = min(wr0 + 16, p.rows_per_kvh) - 1;
+    const int wr0 = row0 + w * WROWS;
+    const int wr1 = min(wr0 + WROWS, p.rows_per_kvh) - 1;
     if (wr1 >= wr0) {
       const int qa = ctx - p.q_len + wr0 / p.G;  // first row's query position
       const int qb_ = ctx - p.q_len + wr1 / p.G; // last row's
@@ -131,28 +153,34 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       wave_lo = p.window > 0 ? max(0, qb_ - p.window + 1) : 0;
     }
   }
-  uint4 qb[JD];
+  uint4 qb[RB][JD];
   {
     const T* qp = static_cast<const T*>(p.q);
 #pragma unroll
-    for (int j = 0; j < JD; ++j) {
-      qb[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (row_ok) qb[j] = *reinterpret_cast<const uint4*>(qp + orow * D + 32 * j + 8 * g);
-    }
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int j = 0; j < JD; ++j) {
+        qb[rb][j] = make_uint4(0u, 0u, 0u, 0u);
+        if (row_ok[rb]) qb[rb][j] = *reinterpret_cast<const uint4*>(qp + orow[rb] * D + 32 * j + 8 * g);
+      }
   }
 
-  mf_f32x4 acc[ND];
+  mf_f32x4 acc[RB][ND];
+  float m_run[RB], l_run[RB];
 #pragma unroll
-  for (int t = 0; t < ND; ++t) acc[t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;
-  float l_run = 0.0f;
+  for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+    for (int t = 0; t < ND; ++t) acc[rb][t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run[rb] = -INFINITY;
+    l_run[rb] = 0.0f;
+  }
 
   const T* kbase = static_cast<const T*>(p.k);
   const T* vbase = static_cast<const T*>(p.v);
   const int step_first = hi_all > lo_all ? lo_all / kPfStep : 0;
   const int step_end = hi_all > lo_all ? ceil_div(hi_all, kPfStep) : 0;
 
-  // Staging: thread tid loads chunk c of token rows tr + (kPfThreads / CPR) * j.
+  // Staging: thread tid loads chunk st_c of token rows st_r + ROWS_PER_PASS * j.
   const int st_c = tid % CPR;
   const int st_r = tid / CPR;
   constexpr int ROWS_PER_PASS = kPfThreads / CPR;
@@ -170,23 +198,6 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       s_pg[j] = phys;
     }
   };
-  auto issue = [&](int step) {
-#pragma unroll
-    for (int j = 0; j < LPT; ++j) {
-      const int tok = step * kPfStep + st_r + ROWS_PER_PASS * j;
-      const int pg = tok / p.bs;
-      const int phys = (tok < hi_all && tok >= lo_all) ? s_pg[pg - pg_chunk * kPfPageChunk] : -1;
-      kst[j] = make_uint4(0u, 0u, 0u, 0u);
-      vst[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (phys >= 0) {
-        const int64_t off = static_cast<int64_t>(phys) * p.blk_stride +
-                            static_cast<int64_t>(tok - pg * p.bs) * p.slot_stride +
-                            static_cast<int64_t>(kvh) * p.head_stride + st_c * 8;
-        kst[j] = *reinterpret_cast<const uint4*>(kbase + off);
-        vst[j] = *reinterpret_cast<const uint4*>(vbase + off);
-      }
-    }
-  };
   // The page ids a step needs lie in one chunk when kPfStep divides the chunk's tokens.
   auto ensure_pages = [&](int step) {
     const int chunk = (step * kPfStep) / p.bs / kPfPageChunk;
@@ -197,133 +208,221 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       __syncthreads();
     }
   };
-
-  if (step_first < step_end) {
-    ensure_pages(step_first);
-    issue(step_first);
-  }
-  for (int step = step_first; step < step_end; ++step) {
-    __syncthreads();  // the previous step's LDS reads are done
+  // A step's row j * 16 + r is row r of its 16-token tile j; block_size % 16 == 0 puts a
+  // tile in one page, so the page lookup and the tile's base offset are the same for
+  // every lane (scalar), and a lane only adds its constant in-tile offset. Each tile is
+  // read through a buffer descriptor whose size ends at the last row below hi_all (rows
+  // past it, and tiles that are holes, read as zeros).
+  const uint32_t st_off = static_cast<uint32_t>((st_r * p.slot_stride + st_c * 8) * 2);
+  const int64_t row_bytes = p.slot_stride * 2;
+  auto issue = [&](int step) {
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int t0 = step * kPfStep + ROWS_PER_PASS * j;  // first token of tile j
+      const int pg = t0 / p.bs;
+      const int phys = __builtin_amdgcn_readfirstlane(s_pg[pg - pg_chunk * kPfPageChunk]);
+      const int rows_valid = min(16, hi_all - t0);
+      const bool tile_in = phys >= 0 && rows_valid > 0 && t0 + 16 > lo_all;
+      const int64_t tbase = tile_in ? static_cast<int64_t>(phys) * p.blk_stride +
+                                          static_cast<int64_t>(t0 - pg * p.bs) * p.slot_stride +
+                                          static_cast<int64_t>(kvh) * p.head_stride
+                                    : 0;
+      const int nbytes = tile_in ? static_cast<int>((rows_valid - 1) * row_bytes + D * 2) : 0;
+      kst[j] = buffer_load16(tile_rsrc(kbase + tbase, nbytes), st_off);
+      vst[j] = buffer_load16(tile_rsrc(vbase + tbase, nbytes), st_off);
+      if (t0 < lo_all) {  // a window's first tile: rows below it are zeros too
+        const bool keep = t0 + st_r >= lo_all;
+        kst[j] = keep ? kst[j] : make_uint4(0u, 0u, 0u, 0u);
+        vst[j] = keep ? vst[j] : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  auto stage = [&](int buf) {  // the registers loaded by issue() into LDS buffer `buf`
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int r = st_r + ROWS_PER_PASS * j;
-      *reinterpret_cast<uint4*>(&s_k[r * RS + st_c * 8]) = kst[j];
-      *reinterpret_cast<uint4*>(&s_v[r * RS + st_c * 8]) = vst[j];
+      *reinterpret_cast<uint4*>(&s_k[buf][r * RSK + st_c * 8]) = kst[j];
+      *reinterpret_cast<uint4*>(&s_v[buf][r * RSV + st_c * 8]) = vst[j];
     }
-    if (step + 1 < step_end) {
-      ensure_pages(step + 1);
-      issue(step + 1);
-    }
-    __syncthreads();  // this step's K/V rows are in LDS
+  };
 
+  // Transposed-read coordinates: lane s of a 16-lane group names 4 dims (4 * (s & 3) ..)
+  // of token (s >> 2) + base; lane i then receives dim i of those four tokens.
+  const int tr_tok = lane >> 2 & 3;
+  const int tr_dim = 4 * (lane & 3);
+
+  auto compute = [&](int step, int buf) {
     const int t_base = step * kPfStep;
     // Keys of this step all visible to every row of the wave: no per-key mask.
     const bool full = t_base >= wave_lo && t_base + kPfStep <= wave_hi;
-    // ---- S^T for the wave's 16 rows: 4 slices of 16 tokens ----
-    float sc[4][4];
-    float mt = -INFINITY;
-    mf_f32x4 sv[4];
+    // ---- S^T for the wave's row blocks: 4 slices of 16 tokens each ----
+    mf_f32x4 sv[RB][4];
 #pragma unroll
-    for (int sl = 0; sl < 4; ++sl) sv[sl] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-    // k-step outer, slices inner: four independent LDS reads, then four MFMAs
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) sv[rb][sl] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < JD; ++j) {
       uint4 ka[4];
 #pragma unroll
       for (int sl = 0; sl < 4; ++sl)
-        ka[sl] = *reinterpret_cast<const uint4*>(&s_k[(16 * sl + n) * RS + 32 * j + 8 * g]);
+        ka[sl] = *reinterpret_cast<const uint4*>(&s_k[buf][(16 * sl + n) * RSK + 32 * j + 8 * g]);
 #pragma unroll
-      for (int sl = 0; sl < 4; ++sl) sv[sl] = Mfma16<T>::mac(ka[sl], qb[j], sv[sl]);
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) sv[rb][sl] = Mfma16<T>::mac(ka[sl], qb[rb][j], sv[rb][sl]);
     }
+    // ---- online softmax per row block; P^T packed as the B operand ----
+    // The row max is taken on raw scores (scale_log2 > 0 keeps the order), the weights
+    // are exp2(s * scale_log2 - m). The running max m only moves when a row's max
+    // exceeds it by more than kPfRescaleSlack (base-2 units): the weights then stay
+    // below 2^kPfRescaleSlack, which fp32 sums and the bf16/fp16 P operand hold, and the
+    // accumulator rescale is skipped on most steps. The normalisation by l is exact
+    // whatever reference max the sums share.
+    uint4 pb[RB][2];
+    float alpha[RB];
 #pragma unroll
-    for (int sl = 0; sl < 4; ++sl) {
+    for (int rb = 0; rb < RB; ++rb) {
+      float sc[4][4];
+      float mt = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[sl][r] = sv[sl][r] * p.scale_log2;
-      if (!full) {
+      for (int sl = 0; sl < 4; ++sl) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tok = t_base + 16 * sl + 4 * g + r;
-          sc[sl][r] = (tok >= lo_n && tok < hi_n) ? sc[sl][r] : -INFINITY;
+        for (int r = 0; r < 4; ++r) sc[sl][r] = sv[rb][sl][r];
+        if (!full) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = t_base + 16 * sl + 4 * g + r;
+            sc[sl][r] = (tok >= lo_n[rb] && tok < hi_n[rb]) ? sc[sl][r] : -INFINITY;
+          }
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sc[sl][r]);
       }
+      mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+      mt *= p.scale_log2;  // the step's row max, base-2 units
+      const float m_new = mt > m_run[rb] + kPfRescaleSlack ? mt : m_run[rb];
+      const bool live = m_new != -INFINITY;
+      alpha[rb] = live ? __builtin_amdgcn_exp2f(m_run[rb] - m_new) : 1.0f;
+      // A row with no key yet has only -inf scores: any finite reference gives zeros.
+      const float m_use = live ? m_new : 0.0f;
+      float psum = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sc[sl][r]);
+      for (int ks = 0; ks < 2; ++ks) {
+        float pr[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = __builtin_amdgcn_exp2f(fmaf(sc[2 * ks + h][r], p.scale_log2, -m_use));
+            pr[4 * h + r] = x;
+            psum += x;
+          }
+        pb[rb][ks] = make_uint4(Pack2<T>::pack(pr[0], pr[1]), Pack2<T>::pack(pr[2], pr[3]),
+                                Pack2<T>::pack(pr[4], pr[5]), Pack2<T>::pack(pr[6], pr[7]));
+      }
+      l_run[rb] = fmaf(l_run[rb], alpha[rb], psum);
+      m_run[rb] = m_new;
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float m_new = fmaxf(m_run, mt);
-    const bool live = m_new != -INFINITY;
-    const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-    float psum = 0.0f;
-    uint4 pb[2];  // P^T as the B operand of the two 32-token k-steps
+    // alpha is exactly 1 for rows whose reference max did not move: most steps skip this
+    bool moved = false;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      float pr[8];
+    for (int rb = 0; rb < RB; ++rb) moved = moved || alpha[rb] != 1.0f;
+    if (__builtin_expect(__any(moved), 0)) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float x = live ? __builtin_amdgcn_exp2f(sc[2 * ks + h][r] - m_new) : 0.0f;
-          pr[4 * h + r] = x;
-          psum += x;
-        }
-      pb[ks] = make_uint4(Pack2<T>::pack(pr[0], pr[1]), Pack2<T>::pack(pr[2], pr[3]),
-                          Pack2<T>::pack(pr[4], pr[5]), Pack2<T>::pack(pr[6], pr[7]));
+        for (int t = 0; t < ND; ++t) acc[rb][t] *= alpha[rb];
     }
-    l_run = fmaf(l_run, alpha, psum);
-    m_run = m_new;
-    if (__any(alpha != 1.0f)) {  // alpha is exactly 1 for rows whose max did not move
-#pragma unroll
-      for (int t = 0; t < ND; ++t) acc[t] *= alpha;
-    }
-
-    // ---- O^T += V^T P^T: A = V^T via transposed LDS reads ----
-    // Lane s of a 16-lane group names 4 dims (4 * (s & 3) ..) of token (s >> 2) + base;
-    // lane i then receives dim i of those four tokens.
-    const int tr_tok = lane >> 2 & 3;   // (s >> 2) within the group
-    const int tr_dim = 4 * (lane & 3);  // 4 * (s & 3)
+    // ---- O^T += V^T P^T: A = V^T via transposed LDS reads, shared by the row blocks ----
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int tok0 = 32 * ks + 4 * g + tr_tok;        // e = 0..3: slice 2ks
       const int tok1 = 32 * ks + 16 + 4 * g + tr_tok;   // e = 4..7: slice 2ks + 1
-      uint4 va[ND];  // all eight dim tiles' operands first, then the MFMAs
+      uint4 va[ND];
 #pragma unroll
       for (int t = 0; t < ND; ++t) {
         const pf_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s4*)(&s_v[tok0 * RS + 16 * t + tr_dim]));
+            (lds_s4*)(&s_v[buf][tok0 * RSV + 16 * t + tr_dim]));
         const pf_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s4*)(&s_v[tok1 * RS + 16 * t + tr_dim]));
+            (lds_s4*)(&s_v[buf][tok1 * RSV + 16 * t + tr_dim]));
         const uint2 lo2 = __builtin_bit_cast(uint2, lo);
         const uint2 hi2 = __builtin_bit_cast(uint2, hi);
         va[t] = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
       }
 #pragma unroll
-      for (int t = 0; t < ND; ++t) acc[t] = Mfma16<T>::mac(va[t], pb[ks], acc[t]);
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int t = 0; t < ND; ++t) acc[rb][t] = Mfma16<T>::mac(va[t], pb[rb][ks], acc[rb][t]);
     }
+  };
+
+  // Prologue: step_first into buffer 0, step_first + 1 loaded into registers.
+  if (step_first < step_end) {
+    ensure_pages(step_first);
+    issue(step_first);
+    stage(0);
+    if (step_first + 1 < step_end) {
+      ensure_pages(step_first + 1);
+      issue(step_first + 1);
+    }
+  }
+  // Everything loaded before the loop (query rows, the first steps) has landed: the
+  // loop then only waits for its own staging loads, not for every load in flight.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int step = step_first; step < step_end; ++step) {
+    const int buf = (step - step_first) & 1;
+    compute(step, buf);
+    if (step + 1 < step_end) {
+      stage(buf ^ 1);  // the other buffer's readers finished before the last barrier
+      if (step + 2 < step_end) {
+        ensure_pages(step + 2);
+        issue(step + 2);
+      }
+    }
+    __syncthreads();  // buf ^ 1 is written; buf's reads are done
   }
 
   // ---- normalise and store: lane (g, n) holds O[row n][dims 16t + 4g + r] ----
-  l_run += __shfl_xor(l_run, 16, kWave);
-  l_run += __shfl_xor(l_run, 32, kWave);
-  if (row_ok) {
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    T* op = static_cast<T*>(p.out) + orow * D;
 #pragma unroll
-    for (int t = 0; t < ND; ++t) {
-      const uint2 pk = make_uint2(Pack2<T>::pack(acc[t][0] * inv, acc[t][1] * inv),
-                                  Pack2<T>::pack(acc[t][2] * inv, acc[t][3] * inv));
-      *reinterpret_cast<uint2*>(op + 16 * t + 4 * g) = pk;
+  for (int rb = 0; rb < RB; ++rb) {
+    float l = l_run[rb];
+    l += __shfl_xor(l, 16, kWave);
+    l += __shfl_xor(l, 32, kWave);
+    if (row_ok[rb]) {
+      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+      T* op = static_cast<T*>(p.out) + orow[rb] * D;
+#pragma unroll
+      for (int t = 0; t < ND; ++t) {
+        const uint2 pk = make_uint2(Pack2<T>::pack(acc[rb][t][0] * inv, acc[rb][t][1] * inv),
+                                    Pack2<T>::pack(acc[rb][t][2] * inv, acc[rb][t][3] * inv));
+        *reinterpret_cast<uint2*>(op + 16 * t + 4 * g) = pk;
+      }
     }
   }
 }
 
 template <typename T>
-hipError_t launch_prefill_mfma(const PrefillParams& p, int D, hipStream_t stream, bool* supported) {
+hipError_t launch_prefill_mfma_impl(const PrefillParams& p, int D, hipStream_t stream,
+                                    bool* supported) {
   *supported = D == 128;
   if (!*supported) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(p.rblocks * p.KVH), 1, static_cast<unsigned>(p.batch));
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, 128>), grid, dim3(kPfThreads), 0, stream, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, kPfRB>), grid, dim3(kPfThreads), 0, stream, p);
   return hipGetLastError();
 }
+
+// Launch for T in {bf16_t, _Float16} (defined in prefill_mfma.hip, the translation unit
+// compiled with the MFMA-in-VGPR option); *supported = false unless head_dim is 128.
+template <typename T>
+hipError_t launch_prefill_mfma(const PrefillParams& p, int D, hipStream_t stream, bool* supported);
+template <>
+hipError_t launch_prefill_mfma<bf16_t>(const PrefillParams& p, int D, hipStream_t stream,
+                                       bool* supported);
+template <>
+hipError_t launch_prefill_mfma<_Float16>(const PrefillParams& p, int D, hipStream_t stream,
+                                         bool* supported);
 
 }  // namespace msattn
