@@ -402,6 +402,7 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
     pp.scale_log2 = scale * kLog2e;
     pp.rows_per_kvh = q_len * pp.G;
     pp.rblocks = ceil_div(pp.rows_per_kvh, kPfRows);
+    pp.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(block_size)) : -1;
     if (static_cast<int64_t>(pp.rblocks) * num_kv_heads >= (int64_t(1) << 31)) return MSATTN_ERR_UNSUPPORTED;
     bool sup = false;
     const hipStream_t st = static_cast<hipStream_t>(stream);

@@ -1,12 +1,15 @@
 // Chunked-prefill paged attention on MFMA (gfx950): q_len > 1, bf16/fp16, head_dim 128.
 //
-// One workgroup (4 waves) owns 16 * RB * 4 query rows of one (sequence b, KV head): rows
-// are the (query token i, GQA head g) pairs r = i * group + g; each wave holds RB blocks of
-// 16 rows, so every K/V operand it reads from LDS feeds RB MFMAs. The workgroup walks the
-// keys its rows may see in steps of 64 tokens (four 16-token page slices):
-//   * K and V of a step are staged through LDS, double-buffered: while a step is computed
-//     from one buffer, the next step's rows (loaded into registers one step ahead) go into
-//     the other, so a step needs one barrier;
+// One workgroup owns 16 * RB * 4 query rows of one (sequence b, KV head): rows are the
+// (query token i, GQA head g) pairs r = i * group + g. It has two groups of 4 waves, one
+// wave of each group per SIMD: both groups hold the same rows (each wave RB blocks of 16
+// rows, so every K/V operand it reads from LDS feeds RB MFMAs) and split the keys, group 0
+// taking the even 64-token steps and group 1 the odd ones; the two running (m, l, O) are
+// merged through LDS at the end. With two waves per SIMD, one wave's softmax and LDS
+// traffic overlap the other's MFMAs. Per group and step:
+//   * K and V of the step are staged through the group's LDS buffers, double-buffered:
+//     while a step is computed from one buffer, the group's next step (loaded into
+//     registers one pair of steps ahead) goes into the other; one barrier per step pair;
 //   * S^T = K Q^T on v_mfma_f32_16x16x32: A = K rows read from LDS, B = the wave's query
 //     rows kept in registers, so lane (g = l/16, n = l%16) holds the scores of query row n
 //     for tokens 4g .. 4g+3 of each 16-token slice;
@@ -31,11 +34,18 @@
 #ifndef MSATTN_PF_RB
 #define MSATTN_PF_RB 2
 #endif
+// P.V ordering: 1 = row block by row block (softmax of the next block overlaps the
+// MFMAs of the previous one), 0 = all softmax first, V operands shared.
+#ifndef MSATTN_PF_INTERLEAVE
+#define MSATTN_PF_INTERLEAVE 1
+#endif
 
 namespace msattn {
 
-constexpr int kPfWaves = 4;
-constexpr int kPfThreads = kPfWaves * kWave;
+constexpr int kPfWaves = 4;                     // waves per key group (one per SIMD)
+constexpr int kPfGroups = 2;                    // key groups: even / odd steps
+constexpr int kPfGroupThreads = kPfWaves * kWave;
+constexpr int kPfThreads = kPfGroups * kPfGroupThreads;
 constexpr int kPfRB = MSATTN_PF_RB;             // 16-row blocks per wave
 constexpr int kPfRows = 16 * kPfRB * kPfWaves;  // query rows per workgroup
 constexpr int kPfStep = 64;                     // key tokens per step
@@ -59,6 +69,7 @@ struct PrefillParams {
   float scale_log2;
   int rows_per_kvh;  // q_len * G
   int rblocks;       // ceil(rows_per_kvh / kPfRows)
+  int bs_shift;      // log2(bs) when bs is a power of two, else -1
 };
 
 typedef float pf_f2 __attribute__((ext_vector_type(2)));
@@ -89,18 +100,22 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   constexpr int RSK = D + 8;              // K LDS row stride (elements): 68 dwords
   constexpr int RSV = D + 16;             // V LDS row stride (elements): 72 dwords
   constexpr int CPR = D * 2 / 16;         // 16-byte chunks per K/V row
-  constexpr int LPT = kPfStep * CPR / kPfThreads;  // chunks per thread per tensor per step
-  static_assert(LPT * kPfThreads == kPfStep * CPR, "staging split");
+  constexpr int LPT = kPfStep * CPR / kPfGroupThreads;  // chunks per thread per tensor per step
+  static_assert(LPT * kPfGroupThreads == kPfStep * CPR, "staging split");
   constexpr int WROWS = 16 * RB;          // query rows per wave
   constexpr int BROWS = WROWS * kPfWaves; // query rows per workgroup
 
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kPfStep * RSK];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kPfStep * RSV];
+  // [key group][buffer][token row]
+  __shared__ __attribute__((aligned(16))) uint16_t s_k[kPfGroups][2][kPfStep * RSK];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[kPfGroups][2][kPfStep * RSV];
   __shared__ int s_pg[kPfPageChunk];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wg = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int grp = wg / kPfWaves;  // key group: steps step_first + grp, + 2, ...
+  const int w = wg - grp * kPfWaves;  // wave within the group: its query rows
+  const int gtid = tid - grp * kPfGroupThreads;
   const int g = lane >> 4;
   const int n = lane & 15;
 
@@ -180,31 +195,34 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int step_first = hi_all > lo_all ? lo_all / kPfStep : 0;
   const int step_end = hi_all > lo_all ? ceil_div(hi_all, kPfStep) : 0;
 
-  // Staging: thread tid loads chunk st_c of token rows st_r + ROWS_PER_PASS * j.
-  const int st_c = tid % CPR;
-  const int st_r = tid / CPR;
-  constexpr int ROWS_PER_PASS = kPfThreads / CPR;
+  // Staging: a group's thread gtid loads chunk st_c of token rows st_r + ROWS_PER_PASS * j
+  // of the group's steps.
+  const int st_c = gtid % CPR;
+  const int st_r = gtid / CPR;
+  constexpr int ROWS_PER_PASS = kPfGroupThreads / CPR;
   uint4 kst[LPT], vst[LPT];
-  int pg_chunk = -1;
+#pragma unroll
+  for (int j = 0; j < LPT; ++j) kst[j] = vst[j] = make_uint4(0u, 0u, 0u, 0u);
+  int pg_base = -(1 << 30);  // s_pg[i] = physical page of logical page pg_base + i
 
-  auto load_pages = [&](int chunk) {  // all threads; caller brackets with barriers
-    for (int j = tid; j < kPfPageChunk; j += kPfThreads) {
-      const int pg = chunk * kPfPageChunk + j;
-      int phys = -1;
-      if (pg < p.W) {
-        phys = p.table[static_cast<int64_t>(b) * p.W + pg];
-        if (phys < 0 || phys >= p.num_blocks) phys = -1;
-      }
-      s_pg[j] = phys;
-    }
-  };
-  // The page ids a step needs lie in one chunk when kPfStep divides the chunk's tokens.
-  auto ensure_pages = [&](int step) {
-    const int chunk = (step * kPfStep) / p.bs / kPfPageChunk;
-    if (chunk != pg_chunk) {
+  auto page_of = [&](int tok) { return p.bs_shift >= 0 ? tok >> p.bs_shift : tok / p.bs; };
+  // Make s_pg cover the pages of steps [s_lo, s_hi]: called by every thread (it may
+  // hold barriers); reloads the window from the first page of s_lo when needed.
+  auto ensure_pages = [&](int s_lo, int s_hi) {
+    const int p_lo = page_of(s_lo * kPfStep);
+    const int p_hi = page_of(s_hi * kPfStep + kPfStep - 1);
+    if (p_lo < pg_base || p_hi >= pg_base + kPfPageChunk) {
       __syncthreads();
-      load_pages(chunk);
-      pg_chunk = chunk;
+      for (int j = tid; j < kPfPageChunk; j += kPfThreads) {
+        const int pg = p_lo + j;
+        int phys = -1;
+        if (pg < p.W) {
+          phys = p.table[static_cast<int64_t>(b) * p.W + pg];
+          if (phys < 0 || phys >= p.num_blocks) phys = -1;
+        }
+        s_pg[j] = phys;
+      }
+      pg_base = p_lo;
       __syncthreads();
     }
   };
@@ -219,8 +237,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int t0 = step * kPfStep + ROWS_PER_PASS * j;  // first token of tile j
-      const int pg = t0 / p.bs;
-      const int phys = __builtin_amdgcn_readfirstlane(s_pg[pg - pg_chunk * kPfPageChunk]);
+      const int pg = page_of(t0);
+      const int phys = __builtin_amdgcn_readfirstlane(s_pg[pg - pg_base]);
       const int rows_valid = min(16, hi_all - t0);
       const bool tile_in = phys >= 0 && rows_valid > 0 && t0 + 16 > lo_all;
       const int64_t tbase = tile_in ? static_cast<int64_t>(phys) * p.blk_stride +
@@ -241,8 +259,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int r = st_r + ROWS_PER_PASS * j;
-      *reinterpret_cast<uint4*>(&s_k[buf][r * RSK + st_c * 8]) = kst[j];
-      *reinterpret_cast<uint4*>(&s_v[buf][r * RSV + st_c * 8]) = vst[j];
+      *reinterpret_cast<uint4*>(&s_k[grp][buf][r * RSK + st_c * 8]) = kst[j];
+      *reinterpret_cast<uint4*>(&s_v[grp][buf][r * RSV + st_c * 8]) = vst[j];
     }
   };
 
@@ -266,13 +284,14 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       uint4 ka[4];
 #pragma unroll
       for (int sl = 0; sl < 4; ++sl)
-        ka[sl] = *reinterpret_cast<const uint4*>(&s_k[buf][(16 * sl + n) * RSK + 32 * j + 8 * g]);
+        ka[sl] = *reinterpret_cast<const uint4*>(&s_k[grp][buf][(16 * sl + n) * RSK + 32 * j + 8 * g]);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int sl = 0; sl < 4; ++sl) sv[rb][sl] = Mfma16<T>::mac(ka[sl], qb[rb][j], sv[rb][sl]);
     }
-    // ---- online softmax per row block; P^T packed as the B operand ----
+
+    // ---- online softmax of one row block; P^T packed as the B operand ----
     // The row max is taken on raw scores (scale_log2 > 0 keeps the order), the weights
     // are exp2(s * scale_log2 - m). The running max m only moves when a row's max
     // exceeds it by more than kPfRescaleSlack (base-2 units): the weights then stay
@@ -281,8 +300,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     // whatever reference max the sums share.
     uint4 pb[RB][2];
     float alpha[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
+    auto softmax = [&](int rb) {
       float sc[4][4];
       float mt = -INFINITY;
 #pragma unroll
@@ -324,81 +342,130 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       }
       l_run[rb] = fmaf(l_run[rb], alpha[rb], psum);
       m_run[rb] = m_new;
-    }
+    };
     // alpha is exactly 1 for rows whose reference max did not move: most steps skip this
-    bool moved = false;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) moved = moved || alpha[rb] != 1.0f;
-    if (__builtin_expect(__any(moved), 0)) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+    auto rescale = [&](int rb) {
+      if (__builtin_expect(__any(alpha[rb] != 1.0f), 0)) {
 #pragma unroll
         for (int t = 0; t < ND; ++t) acc[rb][t] *= alpha[rb];
-    }
-    // ---- O^T += V^T P^T: A = V^T via transposed LDS reads, shared by the row blocks ----
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+      }
+    };
+    // ---- O^T += V^T P^T: A = V^T via transposed LDS reads ----
+    auto v_operands = [&](int ks, uint4 (&va)[ND]) {
       const int tok0 = 32 * ks + 4 * g + tr_tok;        // e = 0..3: slice 2ks
       const int tok1 = 32 * ks + 16 + 4 * g + tr_tok;   // e = 4..7: slice 2ks + 1
-      uint4 va[ND];
 #pragma unroll
       for (int t = 0; t < ND; ++t) {
         const pf_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s4*)(&s_v[buf][tok0 * RSV + 16 * t + tr_dim]));
+            (lds_s4*)(&s_v[grp][buf][tok0 * RSV + 16 * t + tr_dim]));
         const pf_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s4*)(&s_v[buf][tok1 * RSV + 16 * t + tr_dim]));
+            (lds_s4*)(&s_v[grp][buf][tok1 * RSV + 16 * t + tr_dim]));
         const uint2 lo2 = __builtin_bit_cast(uint2, lo);
         const uint2 hi2 = __builtin_bit_cast(uint2, hi);
         va[t] = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
       }
+    };
+#if MSATTN_PF_INTERLEAVE
+    // Row block by row block: block rb's P.V MFMAs run while block rb + 1's softmax
+    // is computed; each block reads the V operands itself.
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      softmax(rb);
+      rescale(rb);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        uint4 va[ND];
+        v_operands(ks, va);
+#pragma unroll
+        for (int t = 0; t < ND; ++t) acc[rb][t] = Mfma16<T>::mac(va[t], pb[rb][ks], acc[rb][t]);
+      }
+    }
+#else
+    // All row blocks' softmax first, then P.V with each V operand read once.
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) softmax(rb);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) rescale(rb);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      uint4 va[ND];
+      v_operands(ks, va);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int t = 0; t < ND; ++t) acc[rb][t] = Mfma16<T>::mac(va[t], pb[rb][ks], acc[rb][t]);
     }
+#endif
   };
 
-  // Prologue: step_first into buffer 0, step_first + 1 loaded into registers.
+  // Group grp takes steps step_first + grp + 2i (i = 0, 1, ...) from its own pair of
+  // buffers; both groups meet at one barrier per pair of steps.
+  const int s_first = step_first + grp;
   if (step_first < step_end) {
-    ensure_pages(step_first);
-    issue(step_first);
+    ensure_pages(step_first, min(step_first + 3, step_end - 1));
+    if (s_first < step_end) issue(s_first);
     stage(0);
-    if (step_first + 1 < step_end) {
-      ensure_pages(step_first + 1);
-      issue(step_first + 1);
-    }
+    if (s_first + 2 < step_end) issue(s_first + 2);
   }
   // Everything loaded before the loop (query rows, the first steps) has landed: the
   // loop then only waits for its own staging loads, not for every load in flight.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int step = step_first; step < step_end; ++step) {
-    const int buf = (step - step_first) & 1;
-    compute(step, buf);
-    if (step + 1 < step_end) {
-      stage(buf ^ 1);  // the other buffer's readers finished before the last barrier
-      if (step + 2 < step_end) {
-        ensure_pages(step + 2);
-        issue(step + 2);
-      }
+  const int npairs = ceil_div(step_end - step_first, 2);
+  for (int i = 0; i < npairs; ++i) {
+    const int step = s_first + 2 * i;
+    const int buf = i & 1;
+    if (step < step_end) compute(step, buf);
+    if (step + 2 < step_end) stage(buf ^ 1);  // its readers finished before the last barrier
+    const int pair_next = step_first + 2 * i + 4;  // the next prefetch, uniform over groups
+    if (pair_next < step_end) {
+      ensure_pages(pair_next, min(pair_next + 1, step_end - 1));
+      if (step + 4 < step_end) issue(step + 4);
     }
     __syncthreads();  // buf ^ 1 is written; buf's reads are done
   }
 
-  // ---- normalise and store: lane (g, n) holds O[row n][dims 16t + 4g + r] ----
+  // ---- combine the two key groups (same rows, same lane layout), normalise, store ----
+  // Group 1 hands its (acc, m, l) through LDS (the V buffers, free after the loop);
+  // lane (g, n) of group 0's wave w reads exactly what lane (g, n) of group 1's wave w
+  // wrote: O[row n][dims 16t + 4g + r] and the row's running m and partial l.
+  static_assert(sizeof(s_v) >= kPfWaves * RB * (ND * kWave * 16 + kWave * 8), "combine space");
+  float4* s_acc = reinterpret_cast<float4*>(&s_v[0][0][0]);
+  float2* s_ml = reinterpret_cast<float2*>(s_acc + kPfWaves * RB * ND * kWave);
+  if (grp == 1) {
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    float l = l_run[rb];
-    l += __shfl_xor(l, 16, kWave);
-    l += __shfl_xor(l, 32, kWave);
-    if (row_ok[rb]) {
-      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-      T* op = static_cast<T*>(p.out) + orow[rb] * D;
+    for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-      for (int t = 0; t < ND; ++t) {
-        const uint2 pk = make_uint2(Pack2<T>::pack(acc[rb][t][0] * inv, acc[rb][t][1] * inv),
-                                    Pack2<T>::pack(acc[rb][t][2] * inv, acc[rb][t][3] * inv));
-        *reinterpret_cast<uint2*>(op + 16 * t + 4 * g) = pk;
+      for (int t = 0; t < ND; ++t)
+        s_acc[((w * RB + rb) * ND + t) * kWave + lane] =
+            make_float4(acc[rb][t][0], acc[rb][t][1], acc[rb][t][2], acc[rb][t][3]);
+      s_ml[(w * RB + rb) * kWave + lane] = make_float2(m_run[rb], l_run[rb]);
+    }
+  }
+  __syncthreads();
+  if (grp == 0) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const float2 ml1 = s_ml[(w * RB + rb) * kWave + lane];
+      const float M = fmaxf(m_run[rb], ml1.x);
+      const float a0 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[rb] - M);
+      const float a1 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml1.x - M);
+      float l = l_run[rb] * a0 + ml1.y * a1;
+      l += __shfl_xor(l, 16, kWave);
+      l += __shfl_xor(l, 32, kWave);
+      if (row_ok[rb]) {
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        T* op = static_cast<T*>(p.out) + orow[rb] * D;
+#pragma unroll
+        for (int t = 0; t < ND; ++t) {
+          const float4 o1 = s_acc[((w * RB + rb) * ND + t) * kWave + lane];
+          const float o0 = (acc[rb][t][0] * a0 + o1.x * a1) * inv;
+          const float o1_ = (acc[rb][t][1] * a0 + o1.y * a1) * inv;
+          const float o2 = (acc[rb][t][2] * a0 + o1.z * a1) * inv;
+          const float o3 = (acc[rb][t][3] * a0 + o1.w * a1) * inv;
+          const uint2 pk = make_uint2(Pack2<T>::pack(o0, o1_), Pack2<T>::pack(o2, o3));
+          *reinterpret_cast<uint2*>(op + 16 * t + 4 * g) = pk;
+        }
       }
     }
   }
