@@ -34,10 +34,10 @@
 #ifndef MSATTN_PF_RB
 #define MSATTN_PF_RB 2
 #endif
-// P.V ordering: 1 = row block by row block (softmax of the next block overlaps the
-// MFMAs of the previous one), 0 = all softmax first, V operands shared.
+// P.V ordering: 0 = all softmax first, V operands shared (measured faster); 1 = row
+// block by row block, the next block's softmax overlapping the previous one's MFMAs.
 #ifndef MSATTN_PF_INTERLEAVE
-#define MSATTN_PF_INTERLEAVE 1
+#define MSATTN_PF_INTERLEAVE 0
 #endif
 
 namespace msattn {
