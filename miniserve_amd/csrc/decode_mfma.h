@@ -232,6 +232,16 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   const int rtile = static_cast<int>(rest / static_cast<unsigned>(p.max_parts));
   const int b = blockIdx.z;
 
+  // Wave w owns a fixed run of the partition's tiles, so their page ids can be
+  // requested together with the context length instead of after it.
+  const int per_wave = p.part / (16 * kMfmaWaves);
+  const int tw0 = part * (p.part / 16) + w * per_wave;
+  int phys_pre = -1;
+  if (lane < per_wave) {
+    const int pg = ((tw0 + lane) * 16) / p.bs;
+    if (pg < p.W) phys_pre = p.table[static_cast<int64_t>(b) * p.W + pg];
+  }
+
   int ctx = p.lens[b];
   ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
   const int nparts = ctx > 0 ? ceil_div(ctx, p.part) : 1;
@@ -275,27 +285,22 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     return;
   }
 
-  // Tiles [t_begin, t_end) of 16 absolute positions; wave w owns a contiguous run.
+  // Tiles [t_begin, t_end) of 16 absolute positions hold the keys; the wave's run is
+  // tiles tw0 .. tw0 + nt - 1 of it (earlier ones, below a window, read nothing).
   const int t_begin = a0 / 16;
   const int t_end = ceil_div(a1, 16);
-  const int per_wave = ceil_div(t_end - t_begin, kMfmaWaves);
-  const int tw0 = t_begin + w * per_wave;
   const int nt = max(0, min(per_wave, t_end - tw0));
 
-  // Page ids of the wave's tiles: lane k holds tile tw0 + k's element offset, or -1
-  // for a hole (a table entry outside [0, num_blocks) or a page past the table).
+  // Lane k holds tile tw0 + k's element offset, or -1 for a hole (a table entry outside
+  // [0, num_blocks), a page past the table, a tile outside the key range).
   int64_t my_base = -1;
-  if (lane < nt) {
+  if (lane < nt && tw0 + lane >= t_begin && phys_pre >= 0 && phys_pre < p.num_blocks) {
     const int t = tw0 + lane;
     const int pg = (t * 16) / p.bs;
     const int slot0 = t * 16 - pg * p.bs;
-    if (pg < p.W) {
-      const int phys = p.table[static_cast<int64_t>(b) * p.W + pg];
-      if (phys >= 0 && phys < p.num_blocks)
-        my_base = static_cast<int64_t>(phys) * p.blk_stride +
-                  static_cast<int64_t>(slot0) * p.slot_stride +
-                  static_cast<int64_t>(kvh) * p.head_stride;
-    }
+    my_base = static_cast<int64_t>(phys_pre) * p.blk_stride +
+              static_cast<int64_t>(slot0) * p.slot_stride +
+              static_cast<int64_t>(kvh) * p.head_stride;
   }
 
   // Query rows as the MFMA B operand: lane (g, n) holds Q[row n][dims 8*(4j+g) .. +8].

@@ -73,18 +73,34 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
   for (int k = 0; k < kMergeMaxDims; ++k) acc[k] = 0.0f;
   float M = -INFINITY;
   float L = 0.0f;
-  // 64 partials at a time: lane j loads (m, l) of partial j0 + j, the wave takes
-  // their max and weights, then folds the acc rows kMergeBatch at a time with all
-  // of a batch's loads in flight together.
+  // 64 partials at a time: lane j loads (m, l) of partial j0 + j, the wave takes their
+  // max and weights, then folds the acc rows kMergeBatch at a time with all of a batch's
+  // loads in flight together. The first batch's acc rows do not depend on (m, l) and are
+  // loaded together with them.
   for (int64_t j0 = 0; j0 < n; j0 += kWave) {
     const int64_t j = j0 + lane;
+    const int cmax = static_cast<int>(n - j0 < kWave ? n - j0 : kWave);
     float m = -INFINITY, l = 0.0f;
     if (j < n) {
       const float2 v = *reinterpret_cast<const float2*>(p.ml + (base + j * stride) * 2);
       m = v.x;
       l = v.y;
     }
-    int cnt = static_cast<int>(n - j0 < kWave ? n - j0 : kWave);
+    auto load_batch = [&](int i0, float (&x)[kMergeBatch][kMergeMaxDims]) {
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const int i = i0 + u < cmax ? i0 + u : cmax - 1;  // stays on a real slot
+        const float* arow = p.acc + (base + (j0 + i) * stride) * D;
+#pragma unroll
+        for (int k = 0; k < kMergeMaxDims; ++k) {
+          const int d = lane + kWave * k;
+          x[u][k] = d < D ? arow[d] : 0.0f;
+        }
+      }
+    };
+    float x0[kMergeBatch][kMergeMaxDims];
+    load_batch(0, x0);
+    int cnt = cmax;
     bool end = false;
     if (markers) {  // the first end marker (l = -1) closes the row
       const uint64_t mk = __ballot(j < n && l == -1.0f);
@@ -102,28 +118,23 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
       L = L * a + group_sum<kWave>(wj * l);
 #pragma unroll
       for (int k = 0; k < kMergeMaxDims; ++k) acc[k] *= a;
-      for (int i0 = 0; i0 < cnt; i0 += kMergeBatch) {
-        float x[kMergeBatch][kMergeMaxDims];
-        float wv[kMergeBatch];
+      auto fold = [&](int i0, const float (&x)[kMergeBatch][kMergeMaxDims]) {
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u) {
-          const int i = i0 + u < cnt ? i0 + u : cnt - 1;  // stays on a real partial
-          wv[u] = i0 + u < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                                __builtin_bit_cast(int, wj), i))
-                               : 0.0f;
-          const float* arow = p.acc + (base + (j0 + i) * stride) * D;
-#pragma unroll
-          for (int k = 0; k < kMergeMaxDims; ++k) {
-            const int d = lane + kWave * k;
-            x[u][k] = d < D ? arow[d] : 0.0f;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u) {
+          const int i = i0 + u < cnt ? i0 + u : cnt - 1;
+          const float wv = i0 + u < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                                    __builtin_bit_cast(int, wj), i))
+                                        : 0.0f;
 #pragma unroll
           for (int k = 0; k < kMergeMaxDims; ++k)  // weight 0: partial without keys
-            acc[k] += wv[u] != 0.0f ? wv[u] * x[u][k] : 0.0f;
+            acc[k] += wv != 0.0f ? wv * x[u][k] : 0.0f;
         }
+      };
+      fold(0, x0);
+      for (int i0 = kMergeBatch; i0 < cnt; i0 += kMergeBatch) {
+        float x[kMergeBatch][kMergeMaxDims];
+        load_batch(i0, x);
+        fold(i0, x);
       }
       M = Mn;
     }
