@@ -472,6 +472,47 @@ def test_prefill_mfma(device, H, KVH, q_len, lens, dtype, causal, window):
             assert not out[b, : q_len - L].any()
 
 
+def paged_case(H, KVH, D, lens, dtype, bs, width_pages, seed, q_len=1):
+    """Scattered pages of `bs` tokens for `lens` in a table `width_pages` wide."""
+    g = torch.Generator().manual_seed(seed)
+    need = sum((L + bs - 1) // bs for L in lens)
+    pool = max(need, 1) + 5
+    q = torch.randn(len(lens), q_len, H, D, generator=g).to(dtype)
+    kc = torch.randn(pool, bs, KVH, D, generator=g).to(dtype)
+    vc = torch.randn(pool, bs, KVH, D, generator=g).to(dtype)
+    perm = torch.randperm(pool, generator=g)
+    table = torch.zeros(len(lens), width_pages, dtype=torch.long)
+    cur = 0
+    for b, L in enumerate(lens):
+        n = (L + bs - 1) // bs
+        table[b, :n] = perm[cur:cur + n]
+        cur += n
+    return q, kc, vc, table
+
+
+@pytest.mark.parametrize("bs", [32, 48, 64])
+def test_mfma_paths_other_page_sizes(device, bs):
+    """Pages of 32, 48 (not a power of two) and 64 tokens on the MFMA kernels: chunked
+    prefill, partition decode, stream-K decode (wide table) and an fp8 cache, each
+    against the float64 oracle."""
+    lens = [5, 100, 1000, 333]
+    cases = [  # (H, KVH, D, q_len, table width in pages, kv dtype)
+        (28, 4, 128, 64, (max(lens) + bs - 1) // bs + 2, torch.bfloat16),   # prefill
+        (14, 2, 64, 1, (max(lens) + bs - 1) // bs + 2, torch.bfloat16),     # partition decode
+        (32, 8, 128, 1, 65536 * 16 // (bs * len(lens) * 8) + 1, torch.bfloat16),  # stream-K
+        (32, 8, 128, 1, (max(lens) + bs - 1) // bs + 2, torch.float8_e4m3fn),     # fp8
+    ]
+    for H, KVH, D, q_len, width, kv_dtype in cases:
+        note(f"page size {bs}: H={H} KVH={KVH} D={D} q_len={q_len} width={width} kv={kv_dtype}")
+        q, kc, vc, table = paged_case(H, KVH, D, [max(L, q_len) for L in lens], torch.bfloat16,
+                                      bs, width, seed=bs + D + q_len)
+        kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+        ctx = [max(L, q_len) for L in lens]
+        out = run_hip(device, q, kc, vc, table, ctx, max_context=width * bs)
+        ref = dense.paged_attention_f64(q, kc, vc, table, ctx)
+        assert rel_err(out, ref) < BF16_REL
+
+
 # ------------------------------------------------------------------ benchmark configs
 
 @pytest.fixture(scope="module")
