@@ -150,6 +150,38 @@ int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
                           int q_dtype, void* stream);
 
 /*
+ * Workspace bytes of msattn_paged_attention_prefix (at least msattn_workspace_bytes
+ * of the same decode geometry); 0 for an invalid geometry. No reference counterpart.
+ */
+size_t msattn_prefix_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                     int block_size, int max_context, int prefix_pages);
+
+/*
+ * Cascade decode (q_len == 1, causal, no window) over block tables whose first
+ * prefix_pages entries are the same physical pages in every row, as
+ * RadixPrefixCache.match hands them out (miniserve/prefix_cache.py:66-96) and the
+ * scheduler forks them into each request's table (miniserve/scheduler.py:146-151).
+ * Same result as msattn_paged_attention(q_len = 1, causal = 1, window = 0) within
+ * float rounding. The shared pages are read once per KV head for the whole batch
+ * (table row 0 names them) by one pass that takes every sequence's query as a row;
+ * a second pass reads each sequence's own keys from prefix_pages * block_size on;
+ * the merge folds both. A row whose context ends inside the prefix sees only its
+ * own length. Types or head sizes without the cascade kernels (anything but bf16 or
+ * fp16 query and cache of one type, head_dim 128, block_size a multiple of 16), and
+ * prefix_pages == 0, run msattn_paged_attention. The reference has no cascade
+ * kernel: its decode re-reads the shared pages per sequence
+ * (miniserve/attention.py:155-171).
+ */
+int msattn_paged_attention_prefix(const void* query, const void* k_cache, const void* v_cache,
+                                  int64_t cache_block_stride, int64_t cache_slot_stride,
+                                  int64_t cache_head_stride, const int32_t* block_table,
+                                  const int32_t* context_lens, void* out, void* workspace,
+                                  size_t workspace_bytes, int batch, int num_heads,
+                                  int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                                  int table_width, int max_context, int prefix_pages, float scale,
+                                  int q_dtype, int kv_dtype, void* stream);
+
+/*
  * Scatter new keys/values into the paged cache: for row b, token t,
  * pos = starts[b] + t, cache[table[b, pos / block_size], pos % block_size] = kv[b, t]
  * converted to kv_dtype (round to nearest even). Replaces PagedAttention.write_kv

@@ -40,6 +40,11 @@ SIGNATURES = {
         c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_size,
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
         c_float, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp]),
+    "msattn_prefix_workspace_bytes": (c_size, [c_int] * 7),
+    "msattn_paged_attention_prefix": (c_int, [
+        c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_size,
+        c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+        c_float, c_int, c_int, c_vp]),
     "msattn_paged_attention_partials": (c_int, [
         c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_size,
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,

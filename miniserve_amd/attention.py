@@ -221,6 +221,7 @@ class PagedAttention:
         sin: torch.Tensor | None = None,
         position: torch.Tensor | None = None,
         scale: float | None = None,
+        shared_prefix_pages: int | None = None,
     ) -> torch.Tensor:
         """Paged attention; ``window`` overrides the constructor value.
 
@@ -228,6 +229,8 @@ class PagedAttention:
         the same HIP kernels; "triton_flash" keeps the reference's decode-only
         contract (attention.py:187-194) and its optional RoPE on the query
         (cos/sin/position, kernels/paged_attn_triton.py:135-139).
+        ``shared_prefix_pages``: the leading block-table entries every row shares (a
+        radix-cache hit, prefix_cache.py:66-96); a decode reads them once per KV head.
         """
         if backend not in _BACKENDS:
             raise ValueError(f"unknown attention backend: {backend!r}")
@@ -245,10 +248,13 @@ class PagedAttention:
             rope = (cos, sin, position) if cos is not None and sin is not None and \
                 position is not None else None
             return paged_attention(query, k_cache, v_cache, block_table, context_lens,
-                                   causal=True, window=None, scale=scale, rope=rope)
+                                   causal=True, window=None, scale=scale, rope=rope,
+                                   prefix_pages=shared_prefix_pages if rope is None else None)
         window = self.window if window is None else window
+        cascade = shared_prefix_pages if (query.shape[1] == 1 and causal and window is None) \
+            else None
         return paged_attention(query, k_cache, v_cache, block_table, context_lens,
-                               causal=causal, window=window, scale=scale)
+                               causal=causal, window=window, scale=scale, prefix_pages=cascade)
 
     __call__ = forward
 
@@ -257,7 +263,7 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
                     block_table, context_lens, *, causal: bool = True, window: int | None = None,
                     scale: float | None = None, max_context: int | None = None,
                     workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                    rope: tuple | None = None) -> torch.Tensor:
+                    rope: tuple | None = None, prefix_pages: int | None = None) -> torch.Tensor:
     """Functional form of PagedAttention.forward on the HIP kernels.
 
     ``max_context`` bounds context_lens; when context_lens is a device tensor
@@ -267,6 +273,9 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     ``rope`` = (cos, sin, position) applies rotate-half RoPE to a decode query inside
     the attention kernels (cos/sin [max_pos, head_dim], position [batch] or a scalar;
     kernels/paged_attn_triton.py:211-220).
+    ``prefix_pages`` > 0 declares that the first prefix_pages entries of every block-table
+    row are the same physical pages (a shared prefix): a causal decode then reads them
+    once per KV head for the whole batch (cascade decode).
     """
     _require_gpu(query, "query")
     _require_gpu(k_cache, "k_cache")
@@ -305,7 +314,16 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     qcode = nat.dtype_code(query.dtype)
     kvcode = nat.dtype_code(k_cache.dtype)
     L = nat.lib()
-    ws_bytes = L.msattn_workspace_bytes(B, q_len, H, KVH, D, max_context)
+    if prefix_pages:
+        if q_len != 1 or not causal or window is not None or rope is not None:
+            raise ValueError("prefix_pages applies to causal decode (q_len == 1) without "
+                             "a window or RoPE")
+        if not 0 <= int(prefix_pages) <= W:
+            raise ValueError(f"prefix_pages {prefix_pages} outside [0, {W}]")
+        ws_bytes = L.msattn_prefix_workspace_bytes(B, H, KVH, D, bs, max_context,
+                                                   int(prefix_pages))
+    else:
+        ws_bytes = L.msattn_workspace_bytes(B, q_len, H, KVH, D, max_context)
     if ws_bytes == 0:
         raise ValueError("unsupported attention geometry")
     if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
@@ -316,6 +334,14 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
             k_cache.stride(1), k_cache.stride(2), table.data_ptr(), lens.data_ptr(),
             out.data_ptr(), workspace.data_ptr(), ws_bytes, B, q_len, H, KVH, D, bs, nb, W,
             max_context, 1 if causal else 0, int(window or 0), float(scale), qcode, kvcode)
+    if prefix_pages:
+        status = L.msattn_paged_attention_prefix(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+            k_cache.stride(1), k_cache.stride(2), table.data_ptr(), lens.data_ptr(),
+            out.data_ptr(), workspace.data_ptr(), ws_bytes, B, H, KVH, D, bs, nb, W,
+            max_context, int(prefix_pages), float(scale), qcode, kvcode, nat.stream_handle(dev))
+        nat.check("msattn_paged_attention_prefix", status)
+        return out
     if rope is None:
         status = L.msattn_paged_attention(*args, nat.stream_handle(dev))
         nat.check("msattn_paged_attention", status)

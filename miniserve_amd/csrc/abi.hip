@@ -113,6 +113,39 @@ Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, i
   return L;
 }
 
+// Cascade decode: the shared-prefix pass splits the prefix into npart key partitions
+// so that (row blocks x KV heads x npart) workgroups about fill the chip (kSkGrid), each
+// at least kPxMinPart tokens; its partials follow the regular workspace layout.
+constexpr int kPxMinPart = 2 * kPfStep;
+struct PrefixLayout {
+  Layout base;
+  int prefix;     // shared tokens
+  int key_part;   // tokens per partition (a multiple of kPfStep)
+  int npart;
+  size_t pml_off, pacc_off;
+  size_t total;
+};
+
+PrefixLayout prefix_layout(int batch, int num_heads, int num_kv_heads, int head_dim,
+                           int block_size, int max_context, int prefix_pages) {
+  PrefixLayout X;
+  X.base = workspace_layout(batch, 1, num_heads, num_kv_heads, head_dim, max_context);
+  const int64_t pt = static_cast<int64_t>(prefix_pages) * block_size;
+  X.prefix = static_cast<int>(pt < max_context ? pt : max_context);
+  const int rblocks = ceil_div(batch * (num_heads / num_kv_heads), kPfRows);
+  const int64_t per_part = static_cast<int64_t>(rblocks) * num_kv_heads;
+  int want = static_cast<int>(ceil_div(static_cast<int64_t>(kSkGrid), per_part));
+  const int most = X.prefix > 0 ? ceil_div(X.prefix, kPxMinPart) : 1;
+  want = want < 1 ? 1 : (want > most ? most : want);
+  X.key_part = X.prefix > 0 ? ceil_div(ceil_div(X.prefix, want), kPfStep) * kPfStep : kPfStep;
+  X.npart = X.prefix > 0 ? ceil_div(X.prefix, X.key_part) : 1;
+  const int64_t slots = static_cast<int64_t>(batch) * num_heads * X.npart;
+  X.pml_off = round256(X.base.total());
+  X.pacc_off = X.pml_off + round256(static_cast<size_t>(slots) * 2 * sizeof(float));
+  X.total = X.pacc_off + static_cast<size_t>(slots) * head_dim * sizeof(float);
+  return X;
+}
+
 int hip_status(hipError_t e) { return e == hipSuccess ? MSATTN_OK : MSATTN_ERR_HIP; }
 
 // Compute units of the current device (cached per device).
@@ -202,7 +235,8 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
                   const int32_t* context_lens, void* workspace, size_t workspace_bytes, int batch,
                   int q_len, int num_heads, int num_kv_heads, int head_dim, int block_size,
                   int num_blocks, int table_width, int max_context, int causal, int window,
-                  float scale, int q_dtype, int kv_dtype, const RopeArgs& rope, void* stream) {
+                  float scale, int q_dtype, int kv_dtype, const RopeArgs& rope, int key_lo,
+                  void* stream) {
   if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
     return MSATTN_ERR_INVALID_ARG;
@@ -258,6 +292,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   p.sk_group = 1;
   p.sk_unit_groups = 0;
   p.sk_min_chunk = kSkMinChunk;
+  p.key_lo = key_lo;
   p.rope_cos = rope.cos;
   p.rope_sin = rope.sin;
   p.rope_pos = rope.pos;
@@ -317,13 +352,17 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
                        cache_head_stride, block_table, context_lens, workspace, workspace_bytes,
                        batch, q_len, num_heads, num_kv_heads, head_dim, block_size, num_blocks,
                        table_width, max_context, causal, window, scale, q_dtype, kv_dtype,
-                       RopeArgs{nullptr, nullptr, nullptr, 0}, stream);
+                       RopeArgs{nullptr, nullptr, nullptr, 0}, 0, stream);
 }
 
-int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
-                          const int32_t* context_lens, void* out, int batch, int q_len,
-                          int num_heads, int num_kv_heads, int head_dim, int max_context,
-                          int q_dtype, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int merge_impl(const void* workspace, size_t workspace_bytes, const int32_t* context_lens,
+               void* out, int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+               int max_context, int q_dtype, const float* pml, const float* pacc, int npp,
+               void* stream) {
   if (!workspace || !context_lens || !out) return MSATTN_ERR_INVALID_ARG;
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
     return MSATTN_ERR_INVALID_ARG;
@@ -345,10 +384,25 @@ int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
   p.G = num_heads / num_kv_heads;
   p.D = head_dim;
   p.max_parts = L.max_parts;
+  p.pml = pml;
+  p.pacc = pacc;
+  p.npp = npp;
   bool sup = false;
   const hipError_t e = launch_merge(p, q_dtype, static_cast<hipStream_t>(stream), &sup);
   if (!sup) return MSATTN_ERR_UNSUPPORTED;
   return hip_status(e);
+}
+
+}  // namespace
+
+extern "C" {
+
+int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
+                          const int32_t* context_lens, void* out, int batch, int q_len,
+                          int num_heads, int num_kv_heads, int head_dim, int max_context,
+                          int q_dtype, void* stream) {
+  return merge_impl(workspace, workspace_bytes, context_lens, out, batch, q_len, num_heads,
+                    num_kv_heads, head_dim, max_context, q_dtype, nullptr, nullptr, 0, stream);
 }
 
 int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
@@ -378,7 +432,7 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
     if (!aligned(query, 16)) return MSATTN_ERR_INVALID_ARG;
     const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
     if (workspace_bytes < L.total()) return MSATTN_ERR_WORKSPACE;
-    PrefillParams pp;
+    PrefillParams pp{};
     pp.q = query;
     pp.k = k_cache;
     pp.v = v_cache;
@@ -415,7 +469,7 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
       query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
       block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
       num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
-      scale, q_dtype, kv_dtype, RopeArgs{nullptr, nullptr, nullptr, 0}, stream);
+      scale, q_dtype, kv_dtype, RopeArgs{nullptr, nullptr, nullptr, 0}, 0, stream);
   if (rc != MSATTN_OK) return rc;
   return msattn_merge_partials(workspace, workspace_bytes, context_lens, out, batch, q_len,
                                num_heads, num_kv_heads, head_dim, max_context, q_dtype, stream);
@@ -441,10 +495,110 @@ int msattn_paged_attention_rope(const void* query, const void* k_cache, const vo
       query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
       block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
       num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
-      scale, q_dtype, kv_dtype, RopeArgs{rope_cos, rope_sin, position, max_position}, stream);
+      scale, q_dtype, kv_dtype, RopeArgs{rope_cos, rope_sin, position, max_position}, 0, stream);
   if (rc != MSATTN_OK) return rc;
   return msattn_merge_partials(workspace, workspace_bytes, context_lens, out, batch, q_len,
                                num_heads, num_kv_heads, head_dim, max_context, q_dtype, stream);
+}
+
+size_t msattn_prefix_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                     int block_size, int max_context, int prefix_pages) {
+  if (!geometry_ok(batch, 1, num_heads, num_kv_heads, head_dim, max_context) ||
+      block_size <= 0 || prefix_pages < 0)
+    return 0;
+  return prefix_layout(batch, num_heads, num_kv_heads, head_dim, block_size, max_context,
+                       prefix_pages).total;
+}
+
+int msattn_paged_attention_prefix(const void* query, const void* k_cache, const void* v_cache,
+                                  int64_t cache_block_stride, int64_t cache_slot_stride,
+                                  int64_t cache_head_stride, const int32_t* block_table,
+                                  const int32_t* context_lens, void* out, void* workspace,
+                                  size_t workspace_bytes, int batch, int num_heads,
+                                  int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                                  int table_width, int max_context, int prefix_pages, float scale,
+                                  int q_dtype, int kv_dtype, void* stream) {
+  if (!query || !block_table || !context_lens || !out || !workspace) return MSATTN_ERR_INVALID_ARG;
+  if (!geometry_ok(batch, 1, num_heads, num_kv_heads, head_dim, max_context))
+    return MSATTN_ERR_INVALID_ARG;
+  if (!dtype_ok(q_dtype) || q_dtype == MSATTN_FP8_E4M3 || !dtype_ok(kv_dtype))
+    return MSATTN_ERR_INVALID_ARG;
+  if (!std::isfinite(scale) || prefix_pages < 0 || prefix_pages > table_width)
+    return MSATTN_ERR_INVALID_ARG;
+  const int rc = check_cache_args(k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                                  cache_head_stride, kv_dtype, block_size, num_blocks, table_width);
+  if (rc != MSATTN_OK) return rc;
+  if (!aligned(query, 16) || !aligned(out, dtype_bytes(q_dtype)) || !aligned(workspace, 16))
+    return MSATTN_ERR_INVALID_ARG;
+  const PrefixLayout X = prefix_layout(batch, num_heads, num_kv_heads, head_dim, block_size,
+                                       max_context, prefix_pages);
+  if (workspace_bytes < X.total) return MSATTN_ERR_WORKSPACE;
+  // The shared-prefix pass runs the MFMA prefill kernel; other types and head sizes,
+  // and calls without a shared prefix, attend in one pass over the whole context.
+  const bool cascade = X.prefix > 0 && q_dtype == kv_dtype &&
+                       (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) && head_dim == 128 &&
+                       block_size % 16 == 0;
+  if (!cascade)
+    return msattn_paged_attention(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                                  cache_head_stride, block_table, context_lens, out, workspace,
+                                  workspace_bytes, batch, 1, num_heads, num_kv_heads, head_dim,
+                                  block_size, num_blocks, table_width, max_context, 1, 0, scale,
+                                  q_dtype, kv_dtype, stream);
+  char* ws = static_cast<char*>(workspace);
+  float* pml = reinterpret_cast<float*>(ws + X.pml_off);
+  float* pacc = reinterpret_cast<float*>(ws + X.pacc_off);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+
+  // Pass 1: every sequence's query against the shared pages (table row 0), once per
+  // KV head, as one virtual sequence of `batch` query positions.
+  PrefillParams pp{};
+  pp.q = query;
+  pp.k = k_cache;
+  pp.v = v_cache;
+  pp.table = block_table;
+  pp.lens = context_lens;
+  pp.out = nullptr;
+  pp.blk_stride = cache_block_stride;
+  pp.slot_stride = cache_slot_stride;
+  pp.head_stride = cache_head_stride;
+  pp.batch = 1;
+  pp.q_len = batch;
+  pp.H = num_heads;
+  pp.KVH = num_kv_heads;
+  pp.G = num_heads / num_kv_heads;
+  pp.bs = block_size;
+  pp.num_blocks = num_blocks;
+  pp.W = table_width;
+  pp.max_ctx = X.prefix;
+  pp.causal = 0;
+  pp.window = 0;
+  pp.scale_log2 = scale * kLog2e;
+  pp.rows_per_kvh = batch * pp.G;
+  pp.rblocks = ceil_div(pp.rows_per_kvh, kPfRows);
+  pp.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(block_size)) : -1;
+  pp.row_lens = context_lens;
+  pp.pml = pml;
+  pp.pacc = pacc;
+  pp.key_part = X.key_part;
+  pp.npart = X.npart;
+  if (static_cast<int64_t>(pp.rblocks) * num_kv_heads >= (int64_t(1) << 31) || X.npart > 65535)
+    return MSATTN_ERR_UNSUPPORTED;
+  bool sup = false;
+  hipError_t e = q_dtype == MSATTN_BF16 ? launch_prefix_partials<bf16_t>(pp, head_dim, st, &sup)
+                                        : launch_prefix_partials<_Float16>(pp, head_dim, st, &sup);
+  if (!sup) return MSATTN_ERR_UNSUPPORTED;
+  if (e != hipSuccess) return MSATTN_ERR_HIP;
+
+  // Pass 2: each sequence's own pages, keys from the end of the prefix on.
+  const int rc2 = partials_impl(
+      query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
+      block_table, context_lens, workspace, workspace_bytes, batch, 1, num_heads, num_kv_heads,
+      head_dim, block_size, num_blocks, table_width, max_context, 1, 0, scale, q_dtype, kv_dtype,
+      RopeArgs{nullptr, nullptr, nullptr, 0}, X.prefix, stream);
+  if (rc2 != MSATTN_OK) return rc2;
+  // Merge: both passes' partials of every row.
+  return merge_impl(workspace, workspace_bytes, context_lens, out, batch, 1, num_heads,
+                    num_kv_heads, head_dim, max_context, q_dtype, pml, pacc, X.npart, stream);
 }
 
 int msattn_write_kv(void* k_cache, void* v_cache, int64_t cache_block_stride,

@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   // Key range of the tile's first and last rows (ranges grow with the query index).
   const int i_first = row0 / p.G;
   const int i_last = (row0 + nrows - 1) / p.G;
-  const int lo_all = p.window > 0 ? max(0, ctx - p.q_len + i_first - p.window + 1) : 0;
+  const int lo_all = max(p.key_lo, p.window > 0 ? max(0, ctx - p.q_len + i_first - p.window + 1) : 0);
   const int hi_all = p.causal ? min(ctx, ctx - p.q_len + i_last + 1) : ctx;
   const int tok0 = part * p.part;
   const int a0 = max(tok0, lo_all);
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     const int i = gr / p.G;
     const int qpos = ctx - p.q_len + i;
     hi_n = p.causal ? min(ctx, qpos + 1) : ctx;
-    lo_n = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
+    lo_n = max(p.key_lo, p.window > 0 ? max(0, qpos - p.window + 1) : 0);
     if (hi_n < lo_n) hi_n = lo_n;
     orow_n = (static_cast<int64_t>(b) * p.q_len + i) * p.H + (kvh * p.G + (gr - i * p.G));
   }

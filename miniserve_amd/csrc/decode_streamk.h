@@ -87,7 +87,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
     if (b < B) {
       int ctx = p.lens[b];
       ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
-      const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
+      const int lo = max(p.key_lo, p.window > 0 ? max(0, ctx - p.window) : 0);
       t = ctx > lo ? ceil_div(ctx, 16) - lo / 16 : 0;
     }
     tb[k] = t;
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
     const int rtile = unit / p.KVH;
     int ctx = p.lens[b];
     ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
-    const int lo_key = p.window > 0 ? max(0, ctx - p.window) : 0;
+    const int lo_key = max(p.key_lo, p.window > 0 ? max(0, ctx - p.window) : 0);
     const int t_first = lo_key / 16 + static_cast<int>(s - seg_start);
     const int ntiles = static_cast<int>(pe - s);
     const int a0 = max(lo_key, t_first * 16);

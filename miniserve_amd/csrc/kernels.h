@@ -14,6 +14,11 @@ struct MergeParams {
   int64_t rows;       // batch * q_len * H
   int batch, H, KVH, G, D;
   int max_parts;      // slots per row of the partition layout
+  // Shared-prefix partials folded in as well (npp per row at slots row * npp ..; npp = 0:
+  // none), as the prefix pass of a cascade decode writes them.
+  const float* pml;
+  const float* pacc;
+  int npp;
 };
 
 hipError_t launch_merge(const MergeParams& p, int q_dtype, hipStream_t stream, bool* supported);

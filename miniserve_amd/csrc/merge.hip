@@ -13,7 +13,8 @@
 // which is the merge of kernels/paged_attn_triton.py:_merge_kernel (:250-284) and
 // of flash_decode_reference's running update (:155-170), in base 2. Partials with
 // m = -inf carry no weight; rows with no key at all get zeros (the value
-// flash_decode_reference returns for L <= 0, :143-144).
+// flash_decode_reference returns for L <= 0, :143-144). A cascade decode adds a second
+// source: the npp partials per row of its shared-prefix pass, all slots written.
 #include "kernels.h"
 
 namespace msattn {
@@ -77,69 +78,74 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
   // max and weights, then folds the acc rows kMergeBatch at a time with all of a batch's
   // loads in flight together. The first batch's acc rows do not depend on (m, l) and are
   // loaded together with them.
-  for (int64_t j0 = 0; j0 < n; j0 += kWave) {
-    const int64_t j = j0 + lane;
-    const int cmax = static_cast<int>(n - j0 < kWave ? n - j0 : kWave);
-    float m = -INFINITY, l = 0.0f;
-    if (j < n) {
-      const float2 v = *reinterpret_cast<const float2*>(p.ml + (base + j * stride) * 2);
-      m = v.x;
-      l = v.y;
-    }
-    auto load_batch = [&](int i0, float (&x)[kMergeBatch][kMergeMaxDims]) {
-#pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        const int i = i0 + u < cmax ? i0 + u : cmax - 1;  // stays on a real slot
-        const float* arow = p.acc + (base + (j0 + i) * stride) * D;
-#pragma unroll
-        for (int k = 0; k < kMergeMaxDims; ++k) {
-          const int d = lane + kWave * k;
-          x[u][k] = d < D ? arow[d] : 0.0f;
-        }
+  auto fold_source = [&](const float* src_ml, const float* src_acc, int64_t base,
+                         int64_t stride, int64_t n, bool markers) {
+    for (int64_t j0 = 0; j0 < n; j0 += kWave) {
+      const int64_t j = j0 + lane;
+      const int cmax = static_cast<int>(n - j0 < kWave ? n - j0 : kWave);
+      float m = -INFINITY, l = 0.0f;
+      if (j < n) {
+        const float2 v = *reinterpret_cast<const float2*>(src_ml + (base + j * stride) * 2);
+        m = v.x;
+        l = v.y;
       }
-    };
-    float x0[kMergeBatch][kMergeMaxDims];
-    load_batch(0, x0);
-    int cnt = cmax;
-    bool end = false;
-    if (markers) {  // the first end marker (l = -1) closes the row
-      const uint64_t mk = __ballot(j < n && l == -1.0f);
-      if (mk) {
-        cnt = __builtin_ctzll(mk);
-        end = true;
-      }
-    }
-    if (lane >= cnt) m = -INFINITY;
-    const float mb = group_max<kWave>(m);
-    if (mb != -INFINITY) {
-      const float Mn = fmaxf(M, mb);
-      const float a = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M = -inf
-      const float wj = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - Mn);
-      L = L * a + group_sum<kWave>(wj * l);
-#pragma unroll
-      for (int k = 0; k < kMergeMaxDims; ++k) acc[k] *= a;
-      auto fold = [&](int i0, const float (&x)[kMergeBatch][kMergeMaxDims]) {
+      auto load_batch = [&](int i0, float (&x)[kMergeBatch][kMergeMaxDims]) {
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u) {
-          const int i = i0 + u < cnt ? i0 + u : cnt - 1;
-          const float wv = i0 + u < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                                    __builtin_bit_cast(int, wj), i))
-                                        : 0.0f;
+          const int i = i0 + u < cmax ? i0 + u : cmax - 1;  // stays on a real slot
+          const float* arow = src_acc + (base + (j0 + i) * stride) * D;
 #pragma unroll
-          for (int k = 0; k < kMergeMaxDims; ++k)  // weight 0: partial without keys
-            acc[k] += wv != 0.0f ? wv * x[u][k] : 0.0f;
+          for (int k = 0; k < kMergeMaxDims; ++k) {
+            const int d = lane + kWave * k;
+            x[u][k] = d < D ? arow[d] : 0.0f;
+          }
         }
       };
-      fold(0, x0);
-      for (int i0 = kMergeBatch; i0 < cnt; i0 += kMergeBatch) {
-        float x[kMergeBatch][kMergeMaxDims];
-        load_batch(i0, x);
-        fold(i0, x);
+      float x0[kMergeBatch][kMergeMaxDims];
+      load_batch(0, x0);
+      int cnt = cmax;
+      bool end = false;
+      if (markers) {  // the first end marker (l = -1) closes the row
+        const uint64_t mk = __ballot(j < n && l == -1.0f);
+        if (mk) {
+          cnt = __builtin_ctzll(mk);
+          end = true;
+        }
       }
-      M = Mn;
+      if (lane >= cnt) m = -INFINITY;
+      const float mb = group_max<kWave>(m);
+      if (mb != -INFINITY) {
+        const float Mn = fmaxf(M, mb);
+        const float a = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M = -inf
+        const float wj = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - Mn);
+        L = L * a + group_sum<kWave>(wj * l);
+#pragma unroll
+        for (int k = 0; k < kMergeMaxDims; ++k) acc[k] *= a;
+        auto fold = [&](int i0, const float (&x)[kMergeBatch][kMergeMaxDims]) {
+#pragma unroll
+          for (int u = 0; u < kMergeBatch; ++u) {
+            const int i = i0 + u < cnt ? i0 + u : cnt - 1;
+            const float wv = i0 + u < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                                      __builtin_bit_cast(int, wj), i))
+                                          : 0.0f;
+#pragma unroll
+            for (int k = 0; k < kMergeMaxDims; ++k)  // weight 0: partial without keys
+              acc[k] += wv != 0.0f ? wv * x[u][k] : 0.0f;
+          }
+        };
+        fold(0, x0);
+        for (int i0 = kMergeBatch; i0 < cnt; i0 += kMergeBatch) {
+          float x[kMergeBatch][kMergeMaxDims];
+          load_batch(i0, x);
+          fold(i0, x);
+        }
+        M = Mn;
+      }
+      if (end) break;
     }
-    if (end) break;
-  }
+  };
+  fold_source(p.ml, p.acc, base, stride, n, markers);
+  if (p.npp > 0) fold_source(p.pml, p.pacc, row * p.npp, 1, p.npp, false);
 
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   QT* out = static_cast<QT*>(p.out) + row * D;

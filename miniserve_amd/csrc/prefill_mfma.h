@@ -70,6 +70,15 @@ struct PrefillParams {
   int rows_per_kvh;  // q_len * G
   int rblocks;       // ceil(rows_per_kvh / kPfRows)
   int bs_shift;      // log2(bs) when bs is a power of two, else -1
+  // Shared-prefix partials mode (the PX kernels): the rows are the decode queries of
+  // every sequence (query index i = sequence), the keys are the first max_ctx positions
+  // of table row 0 (the pages every sequence shares), split into partitions of key_part
+  // tokens (blockIdx.y); row i sees keys below min(max_ctx, row_lens[i]); each
+  // (row, partition) writes an unnormalised partial (m, l, acc) at slot row * npart + part.
+  const int32_t* row_lens;
+  float* pml;
+  float* pacc;
+  int key_part, npart;
 };
 
 typedef float pf_f2 __attribute__((ext_vector_type(2)));
@@ -92,7 +101,7 @@ template <> struct Pack2<_Float16> {
   }
 };
 
-template <typename T, int D, int RB>
+template <typename T, int D, int RB, bool PX>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillParams p) {
   static_assert(D == 128, "prefill MFMA kernel handles head_dim 128");
   constexpr int JD = D / 32;              // k-steps of S^T
@@ -123,9 +132,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const unsigned bx = blockIdx.x;
   const int rblock = p.rblocks - 1 - static_cast<int>(bx % static_cast<unsigned>(p.rblocks));
   const int kvh = static_cast<int>(bx / static_cast<unsigned>(p.rblocks));
-  const int b = blockIdx.z;
+  const int b = PX ? 0 : static_cast<int>(blockIdx.z);
 
-  int ctx = p.lens[b];
+  int ctx = PX ? p.max_ctx : p.lens[b];
   ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
   const int row0 = rblock * BROWS;
   const int rows_here = min(BROWS, p.rows_per_kvh - row0);
@@ -133,8 +142,15 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   // Key range of the block (query index grows with the row).
   const int i_first = row0 / p.G;
   const int i_last = (row0 + rows_here - 1) / p.G;
-  const int lo_all = p.window > 0 ? max(0, ctx - p.q_len + i_first - p.window + 1) : 0;
-  const int hi_all = p.causal ? min(ctx, ctx - p.q_len + i_last + 1) : ctx;
+  int lo_all, hi_all;
+  if constexpr (PX) {  // the block's key partition of the shared prefix
+    const int part = blockIdx.y;
+    lo_all = part * p.key_part;
+    hi_all = min(ctx, lo_all + p.key_part);
+  } else {
+    lo_all = p.window > 0 ? max(0, ctx - p.q_len + i_first - p.window + 1) : 0;
+    hi_all = p.causal ? min(ctx, ctx - p.q_len + i_last + 1) : ctx;
+  }
 
   // This lane's query rows (MFMA column n of each of the wave's row blocks).
   bool row_ok[RB];
@@ -150,8 +166,13 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     if (row_ok[rb]) {
       const int i = row / p.G;
       const int qpos = ctx - p.q_len + i;
-      hi_n[rb] = p.causal ? min(ctx, qpos + 1) : ctx;
-      lo_n[rb] = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
+      if constexpr (PX) {
+        lo_n[rb] = lo_all;
+        hi_n[rb] = min(hi_all, max(0, p.row_lens[i]));
+      } else {
+        hi_n[rb] = p.causal ? min(ctx, qpos + 1) : ctx;
+        lo_n[rb] = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
+      }
       if (hi_n[rb] < lo_n[rb]) hi_n[rb] = lo_n[rb];
       orow[rb] = (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
     }
@@ -166,6 +187,15 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       const int qb_ = ctx - p.q_len + wr1 / p.G; // last row's
       wave_hi = p.causal ? min(ctx, qa + 1) : ctx;
       wave_lo = p.window > 0 ? max(0, qb_ - p.window + 1) : 0;
+    }
+    if constexpr (PX) {  // the smallest per-row limit of the wave's valid rows
+      int h = INT_MAX;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) h = row_ok[rb] ? min(h, hi_n[rb]) : h;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) h = min(h, __shfl_xor(h, o, kWave));
+      wave_lo = lo_all;
+      wave_hi = h == INT_MAX ? 0 : h;
     }
   }
   uint4 qb[RB][JD];
@@ -453,6 +483,20 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       float l = l_run[rb] * a0 + ml1.y * a1;
       l += __shfl_xor(l, 16, kWave);
       l += __shfl_xor(l, 32, kWave);
+      if constexpr (PX) {  // unnormalised partial of this (row, key partition)
+        if (row_ok[rb]) {
+          const int64_t slot = orow[rb] * p.npart + blockIdx.y;
+          if (g == 0) *reinterpret_cast<float2*>(p.pml + slot * 2) = make_float2(M, l);
+#pragma unroll
+          for (int t = 0; t < ND; ++t) {
+            const float4 o1 = s_acc[((w * RB + rb) * ND + t) * kWave + lane];
+            *reinterpret_cast<float4*>(p.pacc + slot * D + 16 * t + 4 * g) =
+                make_float4(acc[rb][t][0] * a0 + o1.x * a1, acc[rb][t][1] * a0 + o1.y * a1,
+                            acc[rb][t][2] * a0 + o1.z * a1, acc[rb][t][3] * a0 + o1.w * a1);
+          }
+        }
+        continue;
+      }
       if (row_ok[rb]) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         T* op = static_cast<T*>(p.out) + orow[rb] * D;
@@ -477,7 +521,17 @@ hipError_t launch_prefill_mfma_impl(const PrefillParams& p, int D, hipStream_t s
   *supported = D == 128;
   if (!*supported) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(p.rblocks * p.KVH), 1, static_cast<unsigned>(p.batch));
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, kPfRB>), grid, dim3(kPfThreads), 0, stream, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, kPfRB, false>), grid, dim3(kPfThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_prefix_partials_impl(const PrefillParams& p, int D, hipStream_t stream,
+                                       bool* supported) {
+  *supported = D == 128;
+  if (!*supported) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(p.rblocks * p.KVH), static_cast<unsigned>(p.npart), 1);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, kPfRB, true>), grid, dim3(kPfThreads), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -491,5 +545,16 @@ hipError_t launch_prefill_mfma<bf16_t>(const PrefillParams& p, int D, hipStream_
 template <>
 hipError_t launch_prefill_mfma<_Float16>(const PrefillParams& p, int D, hipStream_t stream,
                                          bool* supported);
+
+// The shared-prefix partials pass (PX kernels), same types.
+template <typename T>
+hipError_t launch_prefix_partials(const PrefillParams& p, int D, hipStream_t stream,
+                                  bool* supported);
+template <>
+hipError_t launch_prefix_partials<bf16_t>(const PrefillParams& p, int D, hipStream_t stream,
+                                          bool* supported);
+template <>
+hipError_t launch_prefix_partials<_Float16>(const PrefillParams& p, int D, hipStream_t stream,
+                                            bool* supported);
 
 }  // namespace msattn

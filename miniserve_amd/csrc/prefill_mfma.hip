@@ -18,4 +18,16 @@ hipError_t launch_prefill_mfma<_Float16>(const PrefillParams& p, int D, hipStrea
   return launch_prefill_mfma_impl<_Float16>(p, D, stream, supported);
 }
 
+template <>
+hipError_t launch_prefix_partials<bf16_t>(const PrefillParams& p, int D, hipStream_t stream,
+                                          bool* supported) {
+  return launch_prefix_partials_impl<bf16_t>(p, D, stream, supported);
+}
+
+template <>
+hipError_t launch_prefix_partials<_Float16>(const PrefillParams& p, int D, hipStream_t stream,
+                                            bool* supported) {
+  return launch_prefix_partials_impl<_Float16>(p, D, stream, supported);
+}
+
 }  // namespace msattn

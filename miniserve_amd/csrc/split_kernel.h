@@ -74,6 +74,8 @@ struct SplitParams {
   int sk_min_chunk;    // stream-K: smallest chunk (tiles)
   // Optional rotate-half RoPE of the query at position rope_pos[b] (decode):
   // q' = q * cos[pos] + rotate_half(q) * sin[pos], fp32 tables [rope_max_pos, D].
+  int key_lo;             // keys below this position are excluded (a shared prefix
+                          // handled by another pass); 0 for none
   const float* rope_cos;  // nullptr: no RoPE
   const float* rope_sin;
   const int32_t* rope_pos;
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
       const int g = gr - i * p.G;
       const int qpos = ctx - p.q_len + i;
       int hi = p.causal ? min(ctx, qpos + 1) : ctx;
-      int lo = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
+      int lo = max(p.key_lo, p.window > 0 ? max(0, qpos - p.window + 1) : 0);
       if (hi < lo) hi = lo;
       lo_r[r] = lo;
       hi_r[r] = hi;

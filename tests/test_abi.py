@@ -115,6 +115,58 @@ def test_rope_entry_argument_errors(over, rope, status):
                                                  None) == status
 
 
+@pytest.mark.parametrize("B,H,KVH,D,bs,ctx,pages", [
+    (8, 32, 8, 128, 16, 131072, 512),   # C4: 8192 shared tokens
+    (4, 14, 2, 64, 16, 512, 3),
+    (64, 32, 8, 128, 32, 8192, 1),
+    (3, 32, 8, 128, 16, 100, 40),       # prefix longer than max_context
+])
+def test_prefix_workspace_layout(B, H, KVH, D, bs, ctx, pages):
+    """Cascade workspace = the decode workspace, then (m, l) and acc slots for
+    rows x prefix partitions; partitions of >= 128 tokens (whole 64-token steps)
+    sized so (row blocks x KV heads x partitions) about reaches 256 workgroups."""
+    lib = nat.lib()
+    r256 = lambda x: -(-x // 256) * 256
+    base = lib.msattn_workspace_bytes(B, 1, H, KVH, D, ctx)
+    prefix = min(pages * bs, ctx)
+    per = -(-(B * (H // KVH)) // 128) * KVH
+    want = max(1, min(-(-256 // per), -(-prefix // 128)))
+    key_part = -(-(-(-prefix // want)) // 64) * 64
+    npart = -(-prefix // key_part)
+    slots = B * H * npart
+    expect = r256(base) + r256(slots * 8) + slots * D * 4
+    assert lib.msattn_prefix_workspace_bytes(B, H, KVH, D, bs, ctx, pages) == expect
+    assert lib.msattn_prefix_workspace_bytes(B, H, KVH, D, bs, ctx, -1) == 0
+
+
+def _prefix_args(pages=1, query_offset=0, **over):
+    buf, args = _attn_args(**over)
+    names = ["query", "k", "v", "bstride", "sstride", "hstride", "table", "lens", "out", "ws",
+             "ws_bytes", "batch", "q_len", "H", "KVH", "D", "bs", "nb", "W", "max_ctx",
+             "causal", "window", "scale", "qd", "kvd", "stream"]
+    a = dict(zip(names, args))
+    if a["query"] is not None:
+        a["query"] += query_offset
+    keep = names[:12] + ["H", "KVH", "D", "bs", "nb", "W", "max_ctx"]
+    return buf, [a[n] for n in keep] + [pages, a["scale"], a["qd"], a["kvd"], None]
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(query=None), nat.ERR_INVALID_ARG),
+    (dict(out=None), nat.ERR_INVALID_ARG),
+    (dict(pages=-1), nat.ERR_INVALID_ARG),
+    (dict(pages=2), nat.ERR_INVALID_ARG),                 # more pages than the table holds
+    (dict(qd=nat.FP8_E4M3), nat.ERR_INVALID_ARG),
+    (dict(scale=float("inf")), nat.ERR_INVALID_ARG),
+    (dict(ws_bytes=16), nat.ERR_WORKSPACE),
+    (dict(query_offset=2), nat.ERR_INVALID_ARG),          # query not 16-byte aligned
+])
+def test_prefix_entry_argument_errors(over, status):
+    """msattn_paged_attention_prefix returns before any HIP call on a bad argument."""
+    buf, args = _prefix_args(**over)
+    assert nat.lib().msattn_paged_attention_prefix(*args) == status
+
+
 def test_check_maps_status_to_exceptions():
     with pytest.raises(ValueError, match="workspace too small"):
         nat.check("f", nat.ERR_WORKSPACE)

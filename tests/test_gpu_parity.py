@@ -513,6 +513,108 @@ def test_mfma_paths_other_page_sizes(device, bs):
         assert rel_err(out, ref) < BF16_REL
 
 
+# ------------------------------------------------------------------ cascade decode
+
+def shared_prefix_case(H, KVH, D, lens, dtype, bs, prefix_pages, width, seed):
+    """Block tables whose first `prefix_pages` entries are the same physical pages in
+    every row (a radix-cache hit); each row's later pages are its own, scattered."""
+    g = torch.Generator().manual_seed(seed)
+    own = [max(0, (L + bs - 1) // bs - prefix_pages) for L in lens]
+    pool = prefix_pages + sum(own) + 3
+    q = torch.randn(len(lens), 1, H, D, generator=g).to(dtype)
+    kc = torch.randn(pool, bs, KVH, D, generator=g).to(dtype)
+    vc = torch.randn(pool, bs, KVH, D, generator=g).to(dtype)
+    perm = torch.randperm(pool, generator=g)
+    table = torch.zeros(len(lens), width, dtype=torch.long)
+    table[:, :prefix_pages] = perm[:prefix_pages]
+    cur = prefix_pages
+    for b, n in enumerate(own):
+        table[b, prefix_pages:prefix_pages + n] = perm[cur:cur + n]
+        cur += n
+    return q, kc, vc, table
+
+
+_g = torch.Generator().manual_seed(77)
+CASCADE_CASES = [  # (H, KVH, D, dtype, bs, lens, prefix pages, table width in pages)
+    # partition decode for the suffix; rows ending before, at and just after the prefix
+    (32, 8, 128, torch.bfloat16, 16, [5, 100, 1000, 333, 2000, 160, 161, 0], 10, 130),
+    # 20 x 7 = 140 query rows per KV head: two row blocks in the prefix pass
+    (28, 4, 128, torch.float16, 16,
+     [int(x) for x in torch.randint(1, 3000, (20,), generator=_g)], 37, 190),
+    (32, 8, 128, torch.bfloat16, 32, [700, 64, 4000], 20, 126),     # 32-token pages
+    (32, 8, 128, torch.bfloat16, 48, [700, 64, 4000], 9, 90),       # 48-token pages
+    # stream-K decode for the suffix (batch x KV heads x table tiles >= 65536)
+    (32, 8, 128, torch.bfloat16, 16, [30000, 9000, 20000, 1000], 256, 2048),
+    # every key in the prefix: the suffix pass has no work
+    (32, 8, 128, torch.bfloat16, 16, [480, 480, 480], 30, 30),
+    # without cascade kernels (head_dim 64, fp32): one pass over the whole context
+    (14, 2, 64, torch.bfloat16, 16, [300, 50, 900], 8, 60),
+    (4, 2, 64, torch.float32, 16, [300, 50, 900], 8, 60),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASCADE_CASES)))
+def test_cascade_decode(device, case):
+    """Cascade decode (shared prefix read once per KV head, then each row's own pages,
+    then one merge) against the float64 oracle and against the one-pass decode."""
+    H, KVH, D, dtype, bs, lens, pages, width = CASCADE_CASES[case]
+    note(f"cascade case {case}: H={H} KVH={KVH} D={D} {dtype} bs={bs} B={len(lens)} "
+         f"prefix={pages} pages width={width}")
+    q, kc, vc, table = shared_prefix_case(H, KVH, D, lens, dtype, bs, pages, width, seed=case)
+    cap = width * bs
+    out = run_hip(device, q, kc, vc, table, lens, max_context=cap, prefix_pages=pages)
+    one = run_hip(device, q, kc, vc, table, lens, max_context=cap)
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens)
+    if dtype == torch.float32:
+        assert abs_err(out, ref) < FP32_ATOL
+        assert torch.equal(out, one)  # no cascade kernels: the same one-pass launch
+    else:
+        assert rel_err(out, ref) < BF16_REL
+        assert rel_err(out, one.double().cpu().numpy()) < BF16_REL
+    zero = [b for b, L in enumerate(lens) if L == 0]
+    if zero:
+        assert not out[zero].abs().any().item()
+
+
+def test_cascade_graph_replays(device):
+    """Cascade decode captured in a graph: replays with new lengths match eager bit-exactly."""
+    note("cascade graph")
+    H, KVH, D, bs, pages, width = 32, 8, 128, 16, 40, 200
+    lens = [3000, 17, 640, 0, 800, 3200]
+    q, kc, vc, table = shared_prefix_case(H, KVH, D, [width * bs] * len(lens), torch.bfloat16,
+                                          bs, pages, width, seed=9)
+    kc, vc = kc.to(device), vc.to(device)
+    sq = q.to(device)
+    stable = table.to(device=device, dtype=torch.int32)
+    slens = torch.tensor(lens, dtype=torch.int32, device=device)
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+    out = torch.empty_like(sq)
+    cap = width * bs
+
+    def step():
+        paged_attention(sq, kc, vc, stable, slens, max_context=cap, workspace=ws, out=out,
+                        prefix_pages=pages)
+
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream(device).wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    g = torch.Generator().manual_seed(10)
+    for rep in range(4):
+        new = [int(x) for x in torch.randint(0, cap + 1, (len(lens),), generator=g)]
+        slens.copy_(torch.tensor(new, dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = paged_attention(sq, kc, vc, stable, new, max_context=cap, prefix_pages=pages)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay {rep}"
+
+
 # ------------------------------------------------------------------ benchmark configs
 
 @pytest.fixture(scope="module")
