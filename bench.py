@@ -41,6 +41,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cascade", action="store_true",
+                    help="decode a shared-prefix workload (config 4) in one pass per sequence "
+                         "instead of the cascade entry point")
     ap.add_argument("--prefill", action="store_true",
                     help="C5's chunked-prefill part (2 x 512 query tokens onto 4096 cached): "
                          "MFMA-bound, reported in TFLOP/s")
@@ -119,6 +122,11 @@ def main():
     max_ctx = W * bs  # capture-safe bound: the table capacity
     q = w.query.to(dev).contiguous()
     ws_bytes = lib.msattn_workspace_bytes(B, 1, H, KVH, D, max_ctx)
+    # Shared-prefix workloads decode through the cascade entry point (shared pages read
+    # once per KV head for the batch) unless --no-cascade.
+    cascade = w.shared_prefix_pages if not args.no_cascade else 0
+    if cascade:
+        ws_bytes = lib.msattn_prefix_workspace_bytes(B, H, KVH, D, bs, max_ctx, cascade)
     part_tokens = lib.msattn_partition_tokens(B, 1, H, KVH, D, max_ctx)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     outs = [torch.empty_like(q) for _ in range(w.layers)]
@@ -127,7 +135,8 @@ def main():
     def step():
         for layer in range(w.layers):
             paged_attention(q, w.k_caches[layer], w.v_caches[layer], table, lens,
-                            max_context=max_ctx, workspace=ws, out=outs[layer])
+                            max_context=max_ctx, workspace=ws, out=outs[layer],
+                            prefix_pages=cascade or None)
 
     # eager warm-up on a side stream, then capture the step into a hipGraph
     side = torch.cuda.Stream(dev)
@@ -218,6 +227,7 @@ def main():
             "block_size": bs, "layers": w.layers, "context_tokens": sum(w.lens),
             "pool_pages": w.num_blocks, "partition_tokens": part_tokens,
             "algorithmic_bytes_per_layer": per_layer_bytes,
+            "shared_prefix_pages": w.shared_prefix_pages, "cascade": bool(cascade),
         },
         "roofline": {
             "kernel": "msattn::decode_streamk_kernel (split-K partials)",
