@@ -457,7 +457,9 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
     pp.rows_per_kvh = q_len * pp.G;
     pp.rblocks = ceil_div(pp.rows_per_kvh, kPfRows);
     pp.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(block_size)) : -1;
-    if (static_cast<int64_t>(pp.rblocks) * num_kv_heads >= (int64_t(1) << 31)) return MSATTN_ERR_UNSUPPORTED;
+    const int64_t tasks = static_cast<int64_t>(pp.rblocks) * num_kv_heads * batch;
+    if (tasks >= (int64_t(1) << 31) - kXcds) return MSATTN_ERR_UNSUPPORTED;
+    pp.xcd_per = static_cast<int>((tasks + kXcds - 1) / kXcds);
     bool sup = false;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const hipError_t e = q_dtype == MSATTN_BF16 ? launch_prefill_mfma<bf16_t>(pp, head_dim, st, &sup)

@@ -178,6 +178,39 @@ __device__ __forceinline__ float group_max(float x) {
   return x;
 }
 
+// Max over the four 16-lane rows of the wave (lanes n, n + 16, n + 32, n + 48, for
+// each n), every lane receiving it. gfx950's row swaps exchange rows 2k <-> 2k + 1
+// (v_permlane16_swap) and the halves (v_permlane32_swap) of a register pair in the
+// VALU, without the LDS round trip of a lane shuffle. Called with the same value twice,
+// the pair returned holds each lane's own row value and its partner row's value.
+#ifndef MSATTN_ROW_SWAPS
+#define MSATTN_ROW_SWAPS 1
+#endif
+__device__ __forceinline__ float rows4_max(float v) {
+#if MSATTN_ROW_SWAPS
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+#else
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  return fmaxf(v, __shfl_xor(v, 32, kWave));
+#endif
+}
+
+// Sum over the four 16-lane rows, as rows4_max; every lane adds in the same order.
+__device__ __forceinline__ float rows4_sum(float v) {
+#if MSATTN_ROW_SWAPS
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+#else
+  v += __shfl_xor(v, 16, kWave);
+  return v + __shfl_xor(v, 32, kWave);
+#endif
+}
+
 __host__ __device__ constexpr int next_pow2(int x) {
   int p = 1;
   while (p < x) p <<= 1;

@@ -372,8 +372,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
       sc[r] = ok ? s[r] * p.scale_log2 : -INFINITY;
       mt = fmaxf(mt, sc[r]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    mt = rows4_max(mt);
     const float m_new = fmaxf(m_run, mt);
     const bool live = m_new != -INFINITY;
     const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
@@ -445,8 +444,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   }
 
   // Wave totals: l over the 4 lane groups, acc over the V token groups.
-  l_run += __shfl_xor(l_run, 16, kWave);
-  l_run += __shfl_xor(l_run, 32, kWave);
+  l_run = rows4_sum(l_run);
 #pragma unroll
   for (int r = 0; r < RT; ++r)
 #pragma unroll

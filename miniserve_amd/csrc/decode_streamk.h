@@ -260,8 +260,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
           sc[q] = ok ? sv[q] * p.scale_log2 : -INFINITY;
           mt = fmaxf(mt, sc[q]);
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+        mt = rows4_max(mt);
         const float m_new = fmaxf(m_run, mt);
         const bool live = m_new != -INFINITY;
         const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
@@ -332,8 +331,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
     }
 
     // ---- wave totals and the piece's partial ----
-    l_run += __shfl_xor(l_run, 16, kWave);
-    l_run += __shfl_xor(l_run, 32, kWave);
+    l_run = rows4_sum(l_run);
 #pragma unroll
     for (int rr = 0; rr < RT; ++rr)
 #pragma unroll

@@ -50,6 +50,14 @@ constexpr int kPfRB = MSATTN_PF_RB;             // 16-row blocks per wave
 constexpr int kPfRows = 16 * kPfRB * kPfWaves;  // query rows per workgroup
 constexpr int kPfStep = 64;                     // key tokens per step
 constexpr int kPfPageChunk = 512;               // page ids cached in LDS at a time
+// Workgroups are dispatched to the 8 XCDs round-robin (workgroup i runs on XCD i % 8),
+// and each XCD has its own L2. The (sequence, KV head, row block) tasks are dealt so
+// that XCD x takes a contiguous run of them: the row blocks of one (sequence, KV
+// head) then share one L2, where their common K/V stream stays.
+#ifndef MSATTN_PF_XCD
+#define MSATTN_PF_XCD 1
+#endif
+constexpr int kXcds = 8;
 constexpr float kPfRescaleSlack = 8.0f;         // base-2 headroom before the max moves
 
 typedef short pf_s4 __attribute__((ext_vector_type(4)));
@@ -70,6 +78,7 @@ struct PrefillParams {
   int rows_per_kvh;  // q_len * G
   int rblocks;       // ceil(rows_per_kvh / kPfRows)
   int bs_shift;      // log2(bs) when bs is a power of two, else -1
+  int xcd_per;       // tasks per XCD (the grid is kXcds * xcd_per workgroups)
   // Shared-prefix partials mode (the PX kernels): the rows are the decode queries of
   // every sequence (query index i = sequence), the keys are the first max_ctx positions
   // of table row 0 (the pages every sequence shares), split into partitions of key_part
@@ -128,11 +137,20 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int g = lane >> 4;
   const int n = lane & 15;
 
-  // Larger (later) row blocks first: they see the most keys under a causal mask.
-  const unsigned bx = blockIdx.x;
+  // Task = (sequence, KV head) pair-major, then row block; larger (later) row blocks
+  // first: they see the most keys under a causal mask.
+  unsigned bx = blockIdx.x;
+  int b = 0;
+  if constexpr (!PX) {
+    const unsigned i = blockIdx.x;
+    const unsigned task = MSATTN_PF_XCD ? (i % kXcds) * static_cast<unsigned>(p.xcd_per) + i / kXcds : i;
+    const unsigned per_b = static_cast<unsigned>(p.rblocks) * static_cast<unsigned>(p.KVH);
+    if (task >= per_b * static_cast<unsigned>(p.batch)) return;  // the grid's tail
+    b = static_cast<int>(task / per_b);
+    bx = task - static_cast<unsigned>(b) * per_b;
+  }
   const int rblock = p.rblocks - 1 - static_cast<int>(bx % static_cast<unsigned>(p.rblocks));
   const int kvh = static_cast<int>(bx / static_cast<unsigned>(p.rblocks));
-  const int b = PX ? 0 : static_cast<int>(blockIdx.z);
 
   int ctx = PX ? p.max_ctx : p.lens[b];
   ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
@@ -347,8 +365,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 #pragma unroll
         for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sc[sl][r]);
       }
-      mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+      mt = rows4_max(mt);
       mt *= p.scale_log2;  // the step's row max, base-2 units
       const float m_new = mt > m_run[rb] + kPfRescaleSlack ? mt : m_run[rb];
       const bool live = m_new != -INFINITY;
@@ -481,8 +498,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       const float a0 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[rb] - M);
       const float a1 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml1.x - M);
       float l = l_run[rb] * a0 + ml1.y * a1;
-      l += __shfl_xor(l, 16, kWave);
-      l += __shfl_xor(l, 32, kWave);
+      l = rows4_sum(l);
       if constexpr (PX) {  // unnormalised partial of this (row, key partition)
         if (row_ok[rb]) {
           const int64_t slot = orow[rb] * p.npart + blockIdx.y;
@@ -520,7 +536,7 @@ hipError_t launch_prefill_mfma_impl(const PrefillParams& p, int D, hipStream_t s
                                     bool* supported) {
   *supported = D == 128;
   if (!*supported) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>(p.rblocks * p.KVH), 1, static_cast<unsigned>(p.batch));
+  const dim3 grid(static_cast<unsigned>(kXcds * p.xcd_per));
   hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, kPfRB, false>), grid, dim3(kPfThreads), 0, stream, p);
   return hipGetLastError();
 }
