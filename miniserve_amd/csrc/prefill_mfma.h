@@ -58,6 +58,11 @@ constexpr int kPfPageChunk = 512;               // page ids cached in LDS at a t
 #define MSATTN_PF_XCD 1
 #endif
 constexpr int kXcds = 8;
+// Wave priority (s_setprio) raised for the two MFMA blocks of a step: when both waves of
+// a SIMD are ready, the one feeding the matrix core issues first.
+#ifndef MSATTN_PF_PRIO
+#define MSATTN_PF_PRIO 1
+#endif
 constexpr float kPfRescaleSlack = 8.0f;         // base-2 headroom before the max moves
 
 typedef short pf_s4 __attribute__((ext_vector_type(4)));
@@ -327,6 +332,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int sl = 0; sl < 4; ++sl) sv[rb][sl] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int j = 0; j < JD; ++j) {
       uint4 ka[4];
@@ -338,6 +344,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 #pragma unroll
         for (int sl = 0; sl < 4; ++sl) sv[rb][sl] = Mfma16<T>::mac(ka[sl], qb[rb][j], sv[rb][sl]);
     }
+    if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(0);
 
     // ---- online softmax of one row block; P^T packed as the B operand ----
     // The row max is taken on raw scores (scale_log2 > 0 keeps the order), the weights
@@ -433,6 +440,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     for (int rb = 0; rb < RB; ++rb) softmax(rb);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) rescale(rb);
+    if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       uint4 va[ND];
@@ -442,6 +450,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 #pragma unroll
         for (int t = 0; t < ND; ++t) acc[rb][t] = Mfma16<T>::mac(va[t], pb[rb][ks], acc[rb][t]);
     }
+    if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(0);
 #endif
   };
 
