@@ -74,6 +74,45 @@ __device__ __forceinline__ float row_bcast(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x150 + N, 0xF, 0xF, false));
 }
 
+template <int N>
+__device__ __forceinline__ uint32_t row_bcast_u(uint32_t v) {
+  static_assert(N >= 0 && N < 16, "row_newbcast source lane");
+  const int x = static_cast<int>(v);
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(x, x, 0x150 + N, 0xF, 0xF, false));
+}
+
+// Two fp32 values rounded to T (nearest even) and packed, a in the low half.
+typedef float mf_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 mf_bf2 __attribute__((ext_vector_type(2)));
+typedef _Float16 mf_h2 __attribute__((ext_vector_type(2)));
+template <typename T> struct Pack2;
+template <> struct Pack2<bf16_t> {
+  __device__ static uint32_t pack(float a, float b) {
+    const mf_f2 x = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, mf_bf2));
+  }
+};
+template <> struct Pack2<_Float16> {
+  __device__ static uint32_t pack(float a, float b) {
+    const mf_f2 x = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, mf_h2));
+  }
+};
+
+// c + a.lo * b.lo + a.hi * b.hi for packed T pairs, accumulated in fp32 (v_dot2_f32_*).
+template <typename T> struct Dot2;
+template <> struct Dot2<bf16_t> {
+  __device__ static float dot(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(mf_bf2, a), __builtin_bit_cast(mf_bf2, b),
+                                           c, false);
+  }
+};
+template <> struct Dot2<_Float16> {
+  __device__ static float dot(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(mf_h2, a), __builtin_bit_cast(mf_h2, b), c, false);
+  }
+};
+
 template <typename F, int... I>
 __device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
   (f(std::integral_constant<int, I>{}), ...);
@@ -115,6 +154,16 @@ template <typename T> struct Kv8<T, T> {
     return buffer_load16<AUX>(r, off);
   }
   __device__ static uint4 operand(const raw_t& x) { return x; }         // 8 x T, packed
+  // Dim e of two tokens' chunks as one packed T pair (token a low): o[e] = (a[e], b[e]).
+  __device__ static void pairs(const raw_t& a, const raw_t& b, uint32_t (&o)[8]) {
+    const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
+    const uint32_t wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[2 * k] = __builtin_amdgcn_perm(wb[k], wa[k], 0x05040100u);
+      o[2 * k + 1] = __builtin_amdgcn_perm(wb[k], wa[k], 0x07060302u);
+    }
+  }
   __device__ static void unpack(const raw_t& x, float* o) { Chunk<T>::unpack(x, o); }
   __device__ static raw_t keep_if(const raw_t& x, bool keep) {
     return keep ? x : make_uint4(0u, 0u, 0u, 0u);
@@ -142,6 +191,21 @@ template <typename T> struct Kv8<T, fp8_t> {
     return make_uint4(widen2<false>(x.x), widen2<true>(x.x), widen2<false>(x.y),
                       widen2<true>(x.y));
   }
+  // Dim e of two tokens' chunks widened to T and packed (token a low): the bytes of dims
+  // 2m, 2m + 1 of both tokens are interleaved first, then each half is widened.
+  __device__ static void pairs(const raw_t& a, const raw_t& b, uint32_t (&o)[8]) {
+    const uint32_t wa[2] = {a.x, a.y};
+    const uint32_t wb[2] = {b.x, b.y};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t lo = __builtin_amdgcn_perm(wb[k], wa[k], 0x05010400u);  // a0 b0 a1 b1
+      const uint32_t hi = __builtin_amdgcn_perm(wb[k], wa[k], 0x07030602u);  // a2 b2 a3 b3
+      o[4 * k] = widen2<false>(lo);
+      o[4 * k + 1] = widen2<true>(lo);
+      o[4 * k + 2] = widen2<false>(hi);
+      o[4 * k + 3] = widen2<true>(hi);
+    }
+  }
   template <bool HI>  // bytes 2, 3 of w when HI, else bytes 0, 1
   __device__ static uint32_t widen2(uint32_t w) {
     if constexpr (std::is_same<T, bf16_t>::value)
@@ -153,6 +217,73 @@ template <typename T> struct Kv8<T, fp8_t> {
     return keep ? x : make_uint2(0u, 0u);
   }
 };
+
+#ifndef MSATTN_PV_DOT2
+#define MSATTN_PV_DOT2 1
+#endif
+
+// P.V of one 16-token tile on the VALU, for the decode kernels. Lane (g, n) holds the
+// weights pr[r] of query row n for tokens tile_token(4g + r); V lane (va, vc) holds, for
+// load j, dims 8 vc .. 8 vc + 7 of token TPI * j + va, whose weight for row rn sits in
+// lane rn of the lane's own 16-lane row (DPP row_newbcast; with two token groups per row,
+// APR = 2, the group va & 1 picks between two broadcasts). With MSATTN_PV_DOT2 the tokens
+// of loads 2i and 2i + 1 are paired: their weights are rounded to T and packed, V is
+// widened to T (exact for fp8), and one v_dot2_f32 adds both products to the fp32
+// accumulator, which halves the multiply-adds and the broadcasts.
+template <typename T, typename KT, int D, int RT>
+__device__ __forceinline__ void pv_tile(float (&acc)[RT][8], const float (&pr)[4],
+                                        const typename Kv8<T, KT>::raw_t (&vb)[D / 32], int va) {
+  typedef Kv8<T, KT> KV;
+  constexpr int LPR = D / 8;
+  constexpr int TPI = 64 / LPR;
+  constexpr int NJ = 16 / TPI;
+  constexpr int APR = 16 / LPR;
+  static_assert(NJ == D / 32, "V loads per tile");
+#if MSATTN_PV_DOT2
+  static_assert(NJ % 2 == 0, "V loads pair up");
+#pragma unroll
+  for (int i = 0; i < NJ / 2; ++i) {
+    uint32_t vp[8];
+    KV::pairs(vb[2 * i], vb[2 * i + 1], vp);
+    uint32_t pp[APR];
+#pragma unroll
+    for (int a = 0; a < APR; ++a)
+      pp[a] = Pack2<T>::pack(pr[APR * (2 * i) + a], pr[APR * (2 * i + 1) + a]);
+    static_for<RT>([&](auto nc) {
+      constexpr int rn = decltype(nc)::value;
+      uint32_t pb;
+      if constexpr (APR == 1) {
+        pb = row_bcast_u<rn>(pp[0]);
+      } else {
+        const uint32_t b0 = row_bcast_u<rn>(pp[0]);
+        const uint32_t b1 = row_bcast_u<rn>(pp[1]);
+        pb = (va & 1) ? b1 : b0;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[rn][e] = Dot2<T>::dot(pb, vp[e], acc[rn][e]);
+    });
+  }
+#else
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    float vf[8];
+    KV::unpack(vb[j], vf);
+    static_for<RT>([&](auto nc) {
+      constexpr int rn = decltype(nc)::value;
+      float pb;
+      if constexpr (APR == 1) {
+        pb = row_bcast<rn>(pr[j]);
+      } else {
+        const float b0 = row_bcast<rn>(pr[APR * j]);
+        const float b1 = row_bcast<rn>(pr[APR * j + 1]);
+        pb = (va & 1) ? b1 : b0;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[rn][e] = fmaf(pb, vf[e], acc[rn][e]);
+    });
+  }
+#endif
+}
 
 constexpr int kMfmaWaves = MSATTN_MFMA_WAVES;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
@@ -398,29 +529,16 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     // Rows outside the tile's key range (partial tiles) may hold anything, even
     // NaN: their values are replaced by zeros before the weights meet them.
     const bool partial = t0 < a0 || t0 + 16 > a1;
+    raw_t vm[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      float vf[8];
-      raw_t vv = vb[j];
+      vm[j] = vb[j];
       if (partial) {  // wave-uniform branch; per-lane selects inside
         const int vtok = t0 + TPI * j + va;
-        vv = KV::keep_if(vv, vtok >= a0 && vtok < a1);
+        vm[j] = KV::keep_if(vm[j], vtok >= a0 && vtok < a1);
       }
-      KV::unpack(vv, vf);
-      static_for<RT>([&](auto nc) {
-        constexpr int rn = decltype(nc)::value;
-        float pb;
-        if constexpr (APR == 1) {
-          pb = row_bcast<rn>(pr[j]);
-        } else {
-          const float b0 = row_bcast<rn>(pr[APR * j]);
-          const float b1 = row_bcast<rn>(pr[APR * j + 1]);
-          pb = (va & 1) ? b1 : b0;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[rn][e] = fmaf(pb, vf[e], acc[rn][e]);
-      });
     }
+    pv_tile<T, KT, D, RT>(acc, pr, vm, va);
   };
 
   // Two tiles in flight. The sequence is fully unrolled (a wave owns at most

@@ -282,29 +282,16 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
           });
         }
         const bool partial = hole || t0 < a0 || t0 + 16 > a1;
+        raw_t vm[NJ];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          float vf[8];
-          raw_t vv = vb[j];
+          vm[j] = vb[j];
           if (partial) {
             const int vtok = t0 + TPI * j + va;
-            vv = KV::keep_if(vv, !hole && vtok >= a0 && vtok < a1);
+            vm[j] = KV::keep_if(vm[j], !hole && vtok >= a0 && vtok < a1);
           }
-          KV::unpack(vv, vf);
-          static_for<RT>([&](auto nc) {
-            constexpr int rn = decltype(nc)::value;
-            float pb;
-            if constexpr (APR == 1) {
-              pb = row_bcast<rn>(pr[j]);
-            } else {
-              const float b0 = row_bcast<rn>(pr[APR * j]);
-              const float b1 = row_bcast<rn>(pr[APR * j + 1]);
-              pb = (va & 1) ? b1 : b0;
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[rn][e] = fmaf(pb, vf[e], acc[rn][e]);
-          });
         }
+        pv_tile<T, KT, D, RT>(acc, pr, vm, va);
       };
 
       // A ring of DEPTH tile buffers: DEPTH - 1 tiles' loads stay in flight while a

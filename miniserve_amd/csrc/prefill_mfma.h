@@ -95,26 +95,6 @@ struct PrefillParams {
   int key_part, npart;
 };
 
-typedef float pf_f2 __attribute__((ext_vector_type(2)));
-typedef __bf16 pf_bf2 __attribute__((ext_vector_type(2)));
-typedef _Float16 pf_h2 __attribute__((ext_vector_type(2)));
-
-// Two fp32 values -> one packed 16-bit pair (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32,
-// round to nearest even).
-template <typename T> struct Pack2;
-template <> struct Pack2<bf16_t> {
-  __device__ static uint32_t pack(float a, float b) {
-    const pf_f2 x = {a, b};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, pf_bf2));
-  }
-};
-template <> struct Pack2<_Float16> {
-  __device__ static uint32_t pack(float a, float b) {
-    const pf_f2 x = {a, b};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, pf_h2));
-  }
-};
-
 template <typename T, int D, int RB, bool PX>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillParams p) {
   static_assert(D == 128, "prefill MFMA kernel handles head_dim 128");
