@@ -65,6 +65,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
   constexpr int EB = static_cast<int>(sizeof(KT));
 
   __shared__ int s_pre[kSkMaxBatch + 1];  // exclusive prefix of T_b
+  __shared__ int s_ctx[kSkMaxBatch];      // context length of b, clamped to max_ctx
   __shared__ int s_wsum[kSkWaves];
 
   const int tid = threadIdx.x;
@@ -87,6 +88,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
     if (b < B) {
       int ctx = p.lens[b];
       ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
+      s_ctx[b] = ctx;
       const int lo = max(p.key_lo, p.window > 0 ? max(0, ctx - p.window) : 0);
       t = ctx > lo ? ceil_div(ctx, 16) - lo / 16 : 0;
     }
@@ -172,8 +174,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
     const int unit = ug * UG + ul;          // unit = rtile * KVH + kvh
     const int kvh = unit % p.KVH;
     const int rtile = unit / p.KVH;
-    int ctx = p.lens[b];
-    ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
+    const int ctx = s_ctx[b];  // stored before the scan's barriers
     const int lo_key = max(p.key_lo, p.window > 0 ? max(0, ctx - p.window) : 0);
     const int t_first = lo_key / 16 + static_cast<int>(s - seg_start);
     const int ntiles = static_cast<int>(pe - s);
