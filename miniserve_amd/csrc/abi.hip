@@ -236,7 +236,8 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
                   int q_len, int num_heads, int num_kv_heads, int head_dim, int block_size,
                   int num_blocks, int table_width, int max_context, int causal, int window,
                   float scale, int q_dtype, int kv_dtype, const RopeArgs& rope, int key_lo,
-                  void* stream) {
+                  int* kind, void* stream) {
+  *kind = -1;
   if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
     return MSATTN_ERR_INVALID_ARG;
@@ -309,6 +310,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   const int64_t tile_capacity =
       static_cast<int64_t>(batch) * num_kv_heads * ceil_div(max_context, 16);
   if (use_mfma && q_len == 1 && batch <= kSkMaxBatch && tile_capacity >= kStreamKMinTiles) {
+    *kind = 1;
     const int units = num_kv_heads * p.rtiles;
     p.sk_group = largest_pow2_divisor_upto(units, kSkWaves);
     p.sk_unit_groups = units / p.sk_group;
@@ -322,6 +324,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
     if (!sup) return MSATTN_ERR_UNSUPPORTED;
     return hip_status(e);
   }
+  *kind = 0;  // the partition kernels below
   if (use_mfma && q_dtype == MSATTN_BF16) {
     e = kv_fp8 ? launch_decode_mfma<bf16_t, fp8_t>(p, head_dim, RT, st, &sup)
                : launch_decode_mfma<bf16_t, bf16_t>(p, head_dim, RT, st, &sup);
@@ -348,11 +351,12 @@ int msattn_paged_attention_partials(const void* query, const void* k_cache, cons
                                     int num_blocks, int table_width, int max_context, int causal,
                                     int window, float scale, int q_dtype, int kv_dtype,
                                     void* stream) {
+  int kind = -1;
   return partials_impl(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
                        cache_head_stride, block_table, context_lens, workspace, workspace_bytes,
                        batch, q_len, num_heads, num_kv_heads, head_dim, block_size, num_blocks,
                        table_width, max_context, causal, window, scale, q_dtype, kv_dtype,
-                       RopeArgs{nullptr, nullptr, nullptr, 0}, 0, stream);
+                       RopeArgs{nullptr, nullptr, nullptr, 0}, 0, &kind, stream);
 }
 
 }  // extern "C"
@@ -362,7 +366,7 @@ namespace {
 int merge_impl(const void* workspace, size_t workspace_bytes, const int32_t* context_lens,
                void* out, int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
                int max_context, int q_dtype, const float* pml, const float* pacc, int npp,
-               void* stream) {
+               int kind_hint, void* stream) {
   if (!workspace || !context_lens || !out) return MSATTN_ERR_INVALID_ARG;
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
     return MSATTN_ERR_INVALID_ARG;
@@ -387,6 +391,7 @@ int merge_impl(const void* workspace, size_t workspace_bytes, const int32_t* con
   p.pml = pml;
   p.pacc = pacc;
   p.npp = npp;
+  p.kind_hint = kind_hint;
   bool sup = false;
   const hipError_t e = launch_merge(p, q_dtype, static_cast<hipStream_t>(stream), &sup);
   if (!sup) return MSATTN_ERR_UNSUPPORTED;
@@ -402,7 +407,7 @@ int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
                           int num_heads, int num_kv_heads, int head_dim, int max_context,
                           int q_dtype, void* stream) {
   return merge_impl(workspace, workspace_bytes, context_lens, out, batch, q_len, num_heads,
-                    num_kv_heads, head_dim, max_context, q_dtype, nullptr, nullptr, 0, stream);
+                    num_kv_heads, head_dim, max_context, q_dtype, nullptr, nullptr, 0, -1, stream);
 }
 
 int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
@@ -467,14 +472,15 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
     if (!sup) return MSATTN_ERR_UNSUPPORTED;
     return hip_status(e);
   }
+  int kind = -1;
   const int rc = partials_impl(
       query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
       block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
       num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
-      scale, q_dtype, kv_dtype, RopeArgs{nullptr, nullptr, nullptr, 0}, 0, stream);
+      scale, q_dtype, kv_dtype, RopeArgs{nullptr, nullptr, nullptr, 0}, 0, &kind, stream);
   if (rc != MSATTN_OK) return rc;
-  return msattn_merge_partials(workspace, workspace_bytes, context_lens, out, batch, q_len,
-                               num_heads, num_kv_heads, head_dim, max_context, q_dtype, stream);
+  return merge_impl(workspace, workspace_bytes, context_lens, out, batch, q_len, num_heads,
+                    num_kv_heads, head_dim, max_context, q_dtype, nullptr, nullptr, 0, kind, stream);
 }
 
 int msattn_paged_attention_rope(const void* query, const void* k_cache, const void* v_cache,
@@ -493,14 +499,16 @@ int msattn_paged_attention_rope(const void* query, const void* k_cache, const vo
     return MSATTN_ERR_INVALID_ARG;
   if (!dtype_ok(q_dtype) || !aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
   if (q_len != 1 || head_dim % 2) return MSATTN_ERR_UNSUPPORTED;  // decode-only, as the reference
+  int kind = -1;
   const int rc = partials_impl(
       query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
       block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
       num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
-      scale, q_dtype, kv_dtype, RopeArgs{rope_cos, rope_sin, position, max_position}, 0, stream);
+      scale, q_dtype, kv_dtype, RopeArgs{rope_cos, rope_sin, position, max_position}, 0, &kind,
+      stream);
   if (rc != MSATTN_OK) return rc;
-  return msattn_merge_partials(workspace, workspace_bytes, context_lens, out, batch, q_len,
-                               num_heads, num_kv_heads, head_dim, max_context, q_dtype, stream);
+  return merge_impl(workspace, workspace_bytes, context_lens, out, batch, q_len, num_heads,
+                    num_kv_heads, head_dim, max_context, q_dtype, nullptr, nullptr, 0, kind, stream);
 }
 
 size_t msattn_prefix_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
@@ -592,15 +600,17 @@ int msattn_paged_attention_prefix(const void* query, const void* k_cache, const 
   if (e != hipSuccess) return MSATTN_ERR_HIP;
 
   // Pass 2: each sequence's own pages, keys from the end of the prefix on.
+  int kind = -1;
   const int rc2 = partials_impl(
       query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
       block_table, context_lens, workspace, workspace_bytes, batch, 1, num_heads, num_kv_heads,
       head_dim, block_size, num_blocks, table_width, max_context, 1, 0, scale, q_dtype, kv_dtype,
-      RopeArgs{nullptr, nullptr, nullptr, 0}, X.prefix, stream);
+      RopeArgs{nullptr, nullptr, nullptr, 0}, X.prefix, &kind, stream);
   if (rc2 != MSATTN_OK) return rc2;
   // Merge: both passes' partials of every row.
   return merge_impl(workspace, workspace_bytes, context_lens, out, batch, 1, num_heads,
-                    num_kv_heads, head_dim, max_context, q_dtype, pml, pacc, X.npart, stream);
+                    num_kv_heads, head_dim, max_context, q_dtype, pml, pacc, X.npart, kind,
+                    stream);
 }
 
 int msattn_write_kv(void* k_cache, void* v_cache, int64_t cache_block_stride,

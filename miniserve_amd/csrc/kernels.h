@@ -19,6 +19,8 @@ struct MergeParams {
   const float* pml;
   const float* pacc;
   int npp;
+  int kind_hint;      // layout the caller knows the partials kernel used (0: partition
+                      // slots), or -1: read it from the header
 };
 
 hipError_t launch_merge(const MergeParams& p, int q_dtype, hipStream_t stream, bool* supported);

@@ -32,19 +32,24 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
   if (row >= p.rows) return;
   const int D = p.D;
 
-  // Header and this row's prefix entries are read up front, in one round trip.
-  int hv[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) hv[i] = p.hdr[i];
+  // Header and this row's prefix entries are read up front, in one round trip (skipped
+  // when the caller knows the partition layout was used: its slots need no header).
+  const bool known0 = p.kind_hint == 0;
+  int hv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const int b = static_cast<int>(row / p.H);  // the sequence when q_len == 1
   const int bh = b < p.batch ? b : p.batch - 1;  // header holds batch + 1 prefixes
-  const int pb = p.hdr[kHdrPrefix + bh];
-  const int pe = p.hdr[kHdrPrefix + bh + 1];
+  int pb = 0, pe = 0;
+  if (!known0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hv[i] = p.hdr[i];
+    pb = p.hdr[kHdrPrefix + bh];
+    pe = p.hdr[kHdrPrefix + bh + 1];
+  }
 
   // Partial j of this row sits at slot base + j * stride; n bounds the count.
   int64_t base = 0, stride = 1;
   int64_t n = 0;
-  const bool markers = hv[kHdrKind] == 0;
+  const bool markers = known0 || hv[kHdrKind] == 0;
   if (markers) {
     base = row * p.max_parts;
     n = p.max_parts;
