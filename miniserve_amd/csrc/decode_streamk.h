@@ -156,149 +156,179 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
   const uint32_t k_lane_tok = static_cast<uint32_t>(tile_token<D>(n));
   const int tile_bytes = static_cast<int>((15 * p.slot_stride + D) * EB);
 
-  while (s < s_end) {
-    // Locate the piece: unit group ug, sequence b (largest b with s_pre[b] <= o).
-    const int ug = static_cast<int>(s / sumT);
-    const int o = static_cast<int>(s - static_cast<int64_t>(ug) * sumT);
-    int lo_b = 0, hi_b = B;  // s_pre[lo_b] <= o < s_pre[hi_b]
+  // A piece: the part of this chunk's tiles inside one segment (unit group ug, sequence b).
+  struct Piece {
+    int b, kvh, row0, nrows, t_first, ntiles, a0, a1;
+    int64_t pid, pe;
+  };
+  auto locate = [&](int64_t s0) {
+    Piece pc;
+    const int ug = static_cast<int>(s0 / sumT);
+    const int o = static_cast<int>(s0 - static_cast<int64_t>(ug) * sumT);
+    int lo_b = 0, hi_b = B;  // largest b with s_pre[b] <= o: s_pre[lo_b] <= o < s_pre[hi_b]
     while (hi_b - lo_b > 1) {
       const int mid = (lo_b + hi_b) >> 1;
       if (s_pre[mid] <= o) lo_b = mid; else hi_b = mid;
     }
-    const int b = lo_b;
-    const int64_t seg_start = static_cast<int64_t>(ug) * sumT + s_pre[b];
-    const int64_t seg_end = static_cast<int64_t>(ug) * sumT + s_pre[b + 1];
-    const int64_t pe = min(s_end, seg_end);
-    const int64_t pid = r + static_cast<int64_t>(ug) * B + b;  // piece id
-
-    const int unit = ug * UG + ul;          // unit = rtile * KVH + kvh
-    const int kvh = unit % p.KVH;
-    const int rtile = unit / p.KVH;
-    const int ctx = s_ctx[b];  // stored before the scan's barriers
+    pc.b = lo_b;
+    const int64_t seg_start = static_cast<int64_t>(ug) * sumT + s_pre[pc.b];
+    const int64_t seg_end = static_cast<int64_t>(ug) * sumT + s_pre[pc.b + 1];
+    pc.pe = min(s_end, seg_end);
+    pc.pid = r + static_cast<int64_t>(ug) * B + pc.b;  // piece id
+    const int unit = ug * UG + ul;  // unit = rtile * KVH + kvh
+    pc.kvh = unit % p.KVH;
+    pc.row0 = (unit / p.KVH) * RT;  // query row n of the tile is head kvh * G + row0 + n
+    pc.nrows = min(RT, p.G - pc.row0);
+    const int ctx = s_ctx[pc.b];  // stored before the scan's barriers
     const int lo_key = max(p.key_lo, p.window > 0 ? max(0, ctx - p.window) : 0);
-    const int t_first = lo_key / 16 + static_cast<int>(s - seg_start);
-    const int ntiles = static_cast<int>(pe - s);
-    const int a0 = max(lo_key, t_first * 16);
-    const int a1 = min(ctx, (t_first + ntiles) * 16);
-
-    // Rows of this unit: query row n of the tile is head kvh * G + rtile * RT + n.
-    const int row0 = rtile * RT;
-    const int nrows = min(RT, p.G - row0);
-    int64_t orow_n = 0;
-    if (n < nrows) orow_n = static_cast<int64_t>(b) * p.H + kvh * p.G + row0 + n;
-    uint4 qb[JD];
-    {
-      const T* qp = static_cast<const T*>(p.q);
-#pragma unroll
-      for (int j = 0; j < JD; ++j) {
-        qb[j] = make_uint4(0u, 0u, 0u, 0u);
-        if (n < nrows) qb[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + (4 * j + g) * 8);
-      }
-      if (p.rope_cos != nullptr && n < nrows) {
-        const int64_t po = static_cast<int64_t>(rope_position(p, b)) * D;
-        rope_chunks<T, D>(qb, p.rope_cos + po, p.rope_sin + po, g);
+    pc.t_first = lo_key / 16 + static_cast<int>(s0 - seg_start);
+    pc.ntiles = static_cast<int>(pc.pe - s0);
+    pc.a0 = max(lo_key, pc.t_first * 16);
+    pc.a1 = min(ctx, (pc.t_first + pc.ntiles) * 16);
+    return pc;
+  };
+  // Lane k: element offset of tile t_first + run0 + k of the piece, or -1 for a hole or
+  // a lane past the run.
+  auto table_run = [&](const Piece& pc, int run0) -> int64_t {
+    const int nt = min(kSkTableRun, pc.ntiles - run0);
+    int64_t mb = -1;
+    if (lane < nt) {
+      const int t = pc.t_first + run0 + lane;
+      const int pg = (t * 16) / p.bs;
+      const int slot0 = t * 16 - pg * p.bs;
+      if (pg < p.W) {
+        const int phys = p.table[static_cast<int64_t>(pc.b) * p.W + pg];
+        if (phys >= 0 && phys < p.num_blocks)
+          mb = static_cast<int64_t>(phys) * p.blk_stride +
+               static_cast<int64_t>(slot0) * p.slot_stride +
+               static_cast<int64_t>(pc.kvh) * p.head_stride;
       }
     }
-
-    float m_run = -INFINITY;
-    float l_run = 0.0f;
-    float acc[RT][8];
+    return mb;
+  };
+  // The piece's query rows as the MFMA B operand (lane (g, n): row n, dims 8 (4j + g) ..).
+  auto load_q = [&](const Piece& pc, uint4 (&q)[JD]) {
+    const T* qp = static_cast<const T*>(p.q);
+    const int64_t orow_n = static_cast<int64_t>(pc.b) * p.H + pc.kvh * p.G + pc.row0 + n;
 #pragma unroll
-    for (int rr = 0; rr < RT; ++rr)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[rr][e] = 0.0f;
+    for (int j = 0; j < JD; ++j) {
+      q[j] = make_uint4(0u, 0u, 0u, 0u);
+      if (n < pc.nrows) q[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + (4 * j + g) * 8);
+    }
+    if (p.rope_cos != nullptr && n < pc.nrows) {
+      const int64_t po = static_cast<int64_t>(rope_position(p, pc.b)) * D;
+      rope_chunks<T, D>(q, p.rope_cos + po, p.rope_sin + po, g);
+    }
+  };
 
-    for (int run0 = 0; run0 < ntiles; run0 += kSkTableRun) {
-      const int nt = min(kSkTableRun, ntiles - run0);
-      // lane k: element offset of tile t_first + run0 + k, or -1 for a hole / k >= nt
-      int64_t my_base = -1;
-      if (lane < nt) {
-        const int t = t_first + run0 + lane;
-        const int pg = (t * 16) / p.bs;
-        const int slot0 = t * 16 - pg * p.bs;
-        if (pg < p.W) {
-          const int phys = p.table[static_cast<int64_t>(b) * p.W + pg];
-          if (phys >= 0 && phys < p.num_blocks)
-            my_base = static_cast<int64_t>(phys) * p.blk_stride +
-                      static_cast<int64_t>(slot0) * p.slot_stride +
-                      static_cast<int64_t>(kvh) * p.head_stride;
+  if (s >= s_end) return;
+  Piece cur = locate(s);
+  int run0 = 0;
+  int64_t my_base = table_run(cur, 0);
+  uint4 qb[JD];
+  load_q(cur, qb);
+
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+  float acc[RT][8];
+#pragma unroll
+  for (int rr = 0; rr < RT; ++rr)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[rr][e] = 0.0f;
+
+  // Runs of up to kSkTableRun tiles, piece after piece. The next run's page ids (and a
+  // new piece's query rows) are requested before this run streams, so they have landed
+  // when it starts: a piece boundary costs no page-table round trip.
+  while (true) {
+    const bool more_here = run0 + kSkTableRun < cur.ntiles;
+    const bool next_piece = !more_here && cur.pe < s_end;
+    Piece nxt = cur;
+    int run_n = run0 + kSkTableRun;
+    uint4 qn[JD];
+    if (next_piece) {
+      nxt = locate(cur.pe);
+      run_n = 0;
+      load_q(nxt, qn);
+    }
+    const int64_t base_n = (more_here || next_piece) ? table_run(nxt, run_n) : -1;
+
+    const int nt = min(kSkTableRun, cur.ntiles - run0);
+    auto tile_base = [&](int k) -> int64_t {
+      if (k >= nt) return -1;
+      const uint32_t lo = static_cast<uint32_t>(
+          __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(my_base)), k));
+      const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
+      return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
+    };
+    auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) {
+      const bool ok = base >= 0;
+      const int64_t b0 = ok ? base : 0;
+      const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
+      const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
+      const uint32_t koff = (k_lane_tok * static_cast<uint32_t>(p.slot_stride) + g * 8) * EB;
+#pragma unroll
+      for (int j = 0; j < JD; ++j)
+        kb[j] = KV::template load<MSATTN_LOAD_AUX>(rk, koff + 32 * EB * j);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        vb[j] = KV::template load<MSATTN_LOAD_AUX>(
+            rv, ((static_cast<uint32_t>(TPI * j + va) * static_cast<uint32_t>(p.slot_stride)) +
+                 vc * 8) * EB);
+    };
+    auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) {
+      mf_f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < JD; ++j) sv = Mfma16<T>::mac(KV::operand(kb[j]), qb[j], sv);
+      const int t0 = (cur.t_first + run0 + k) * 16;
+      const bool hole = base < 0;
+      float sc[4];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int tok = t0 + tile_token<D>(4 * g + q);
+        const bool ok = !hole && n < cur.nrows && tok >= cur.a0 && tok < cur.a1;
+        sc[q] = ok ? sv[q] * p.scale_log2 : -INFINITY;
+        mt = fmaxf(mt, sc[q]);
+      }
+      mt = rows4_max(mt);
+      const float m_new = fmaxf(m_run, mt);
+      const bool live = m_new != -INFINITY;
+      const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+      float pr[4];
+      float psum = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        pr[q] = live ? __builtin_amdgcn_exp2f(sc[q] - m_new) : 0.0f;
+        psum += pr[q];
+      }
+      l_run = fmaf(l_run, alpha, psum);
+      m_run = m_new;
+      if (!MSATTN_LAZY_RESCALE || __any(alpha != 1.0f)) {
+        static_for<RT>([&](auto nc) {
+          constexpr int rn = decltype(nc)::value;
+          const float al = row_bcast<rn>(alpha);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[rn][e] *= al;
+        });
+      }
+      const bool partial = hole || t0 < cur.a0 || t0 + 16 > cur.a1;
+      raw_t vm[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        vm[j] = vb[j];
+        if (partial) {
+          const int vtok = t0 + TPI * j + va;
+          vm[j] = KV::keep_if(vm[j], !hole && vtok >= cur.a0 && vtok < cur.a1);
         }
       }
-      auto tile_base = [&](int k) -> int64_t {
-        if (k >= nt) return -1;
-        const uint32_t lo = static_cast<uint32_t>(
-            __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(my_base)), k));
-        const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
-        return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
-      };
-      auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) {
-        const bool ok = base >= 0;
-        const int64_t b0 = ok ? base : 0;
-        const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
-        const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
-        const uint32_t koff = (k_lane_tok * static_cast<uint32_t>(p.slot_stride) + g * 8) * EB;
-#pragma unroll
-        for (int j = 0; j < JD; ++j)
-          kb[j] = KV::template load<MSATTN_LOAD_AUX>(rk, koff + 32 * EB * j);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          vb[j] = KV::template load<MSATTN_LOAD_AUX>(
-              rv, ((static_cast<uint32_t>(TPI * j + va) * static_cast<uint32_t>(p.slot_stride)) +
-                   vc * 8) * EB);
-      };
-      auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) {
-        mf_f32x4 sv = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < JD; ++j) sv = Mfma16<T>::mac(KV::operand(kb[j]), qb[j], sv);
-        const int t0 = (t_first + run0 + k) * 16;
-        const bool hole = base < 0;
-        float sc[4];
-        float mt = -INFINITY;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int tok = t0 + tile_token<D>(4 * g + q);
-          const bool ok = !hole && n < nrows && tok >= a0 && tok < a1;
-          sc[q] = ok ? sv[q] * p.scale_log2 : -INFINITY;
-          mt = fmaxf(mt, sc[q]);
-        }
-        mt = rows4_max(mt);
-        const float m_new = fmaxf(m_run, mt);
-        const bool live = m_new != -INFINITY;
-        const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-        float pr[4];
-        float psum = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          pr[q] = live ? __builtin_amdgcn_exp2f(sc[q] - m_new) : 0.0f;
-          psum += pr[q];
-        }
-        l_run = fmaf(l_run, alpha, psum);
-        m_run = m_new;
-        if (!MSATTN_LAZY_RESCALE || __any(alpha != 1.0f)) {
-          static_for<RT>([&](auto nc) {
-            constexpr int rn = decltype(nc)::value;
-            const float al = row_bcast<rn>(alpha);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[rn][e] *= al;
-          });
-        }
-        const bool partial = hole || t0 < a0 || t0 + 16 > a1;
-        raw_t vm[NJ];
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          vm[j] = vb[j];
-          if (partial) {
-            const int vtok = t0 + TPI * j + va;
-            vm[j] = KV::keep_if(vm[j], !hole && vtok >= a0 && vtok < a1);
-          }
-        }
-        pv_tile<T, KT, D, RT>(acc, pr, vm, va);
-      };
+      pv_tile<T, KT, D, RT>(acc, pr, vm, va);
+    };
 
-      // A ring of DEPTH tile buffers: DEPTH - 1 tiles' loads stay in flight while a
-      // tile is consumed, the next tile's loads going into the slot just freed.
-      // A tile index >= nt reads nothing and adds nothing (its descriptor has no
-      // records, all its keys are masked).
+    // A ring of DEPTH tile buffers: DEPTH - 1 tiles' loads stay in flight while a
+    // tile is consumed, the next tile's loads going into the slot just freed.
+    // A tile index >= nt reads nothing and adds nothing (its descriptor has no
+    // records, all its keys are masked).
+    {
       raw_t kq[DEPTH][JD], vq[DEPTH][NJ];
       int64_t bq[DEPTH];
       static_for<DEPTH - 1>([&](auto dc) {
@@ -309,43 +339,56 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
       for (int k = 0; k < nt; k += STEP) {
         static_for<STEP>([&](auto dc) {
           constexpr int d = decltype(dc)::value;
-          constexpr int cur = d % DEPTH;
-          constexpr int nxt = (d + DEPTH - 1) % DEPTH;
-          bq[nxt] = tile_base(k + d + DEPTH - 1);
-          issue(bq[nxt], kq[nxt], vq[nxt]);
-          consume(k + d, kq[cur], vq[cur], bq[cur]);
+          constexpr int cu = d % DEPTH;
+          constexpr int nx = (d + DEPTH - 1) % DEPTH;
+          bq[nx] = tile_base(k + d + DEPTH - 1);
+          issue(bq[nx], kq[nx], vq[nx]);
+          consume(k + d, kq[cu], vq[cu], bq[cu]);
         });
       }
     }
 
-    // ---- wave totals and the piece's partial ----
-    l_run = rows4_sum(l_run);
+    if (!more_here) {
+      // ---- wave totals and the piece's partial ----
+      l_run = rows4_sum(l_run);
 #pragma unroll
-    for (int rr = 0; rr < RT; ++rr)
+      for (int rr = 0; rr < RT; ++rr)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float a = acc[rr][e];
+        for (int e = 0; e < 8; ++e) {
+          float a = acc[rr][e];
 #pragma unroll
-        for (int oo = LPR; oo < kWave; oo <<= 1) a += __shfl_xor(a, oo, kWave);
-        acc[rr][e] = a;
-      }
-    const int64_t slot0 = (pid * UG + ul) * RT;  // this unit's rows in the piece
-    if (va == 0) {
+          for (int oo = LPR; oo < kWave; oo <<= 1) a += __shfl_xor(a, oo, kWave);
+          acc[rr][e] = a;
+        }
+      const int64_t slot0 = (cur.pid * UG + ul) * RT;  // this unit's rows in the piece
+      if (va == 0) {
 #pragma unroll
-      for (int rr = 0; rr < RT; ++rr) {
-        if (rr < nrows) {
-          float* dst = p.acc + (slot0 + rr) * D + vc * 8;
-          *reinterpret_cast<float4*>(dst) = make_float4(acc[rr][0], acc[rr][1], acc[rr][2], acc[rr][3]);
-          *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[rr][4], acc[rr][5], acc[rr][6], acc[rr][7]);
+        for (int rr = 0; rr < RT; ++rr) {
+          if (rr < cur.nrows) {
+            float* dst = p.acc + (slot0 + rr) * D + vc * 8;
+            *reinterpret_cast<float4*>(dst) = make_float4(acc[rr][0], acc[rr][1], acc[rr][2], acc[rr][3]);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[rr][4], acc[rr][5], acc[rr][6], acc[rr][7]);
+          }
         }
       }
+      if (lane < cur.nrows) {
+        float* ml = p.ml + (slot0 + lane) * 2;
+        ml[0] = m_run;
+        ml[1] = l_run;
+      }
+      if (!next_piece) break;
+      m_run = -INFINITY;
+      l_run = 0.0f;
+#pragma unroll
+      for (int rr = 0; rr < RT; ++rr)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[rr][e] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < JD; ++j) qb[j] = qn[j];
     }
-    if (lane < nrows) {
-      float* ml = p.ml + (slot0 + lane) * 2;
-      ml[0] = m_run;
-      ml[1] = l_run;
-    }
-    s = pe;
+    cur = nxt;
+    run0 = run_n;
+    my_base = base_n;
   }
 }
 
