@@ -44,6 +44,7 @@ COMMON_FLAGS = [
 # register files.
 FILE_FLAGS = {
     "prefill_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "prefill_mfma_fp8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

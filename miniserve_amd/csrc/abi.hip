@@ -422,7 +422,8 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
   if (!aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
   // Chunked prefill (more than one 16-row tile of query rows per KV head): the MFMA
   // prefill kernel writes the normalised output directly.
-  if (q_len > 1 && q_dtype == kv_dtype && (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
+  if (q_len > 1 && (kv_dtype == q_dtype || kv_dtype == MSATTN_FP8_E4M3) &&
+      (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
       head_dim == 128 && block_size % 16 == 0 && batch <= 65535 && num_heads > 0 &&
       num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
       static_cast<int64_t>(q_len) * (num_heads / num_kv_heads) > 16) {
@@ -467,8 +468,14 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
     pp.xcd_per = static_cast<int>((tasks + kXcds - 1) / kXcds);
     bool sup = false;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    const hipError_t e = q_dtype == MSATTN_BF16 ? launch_prefill_mfma<bf16_t>(pp, head_dim, st, &sup)
-                                                : launch_prefill_mfma<_Float16>(pp, head_dim, st, &sup);
+    const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
+    hipError_t e;
+    if (q_dtype == MSATTN_BF16)
+      e = kv_fp8 ? launch_prefill_mfma<bf16_t, fp8_t>(pp, head_dim, st, &sup)
+                 : launch_prefill_mfma<bf16_t, bf16_t>(pp, head_dim, st, &sup);
+    else
+      e = kv_fp8 ? launch_prefill_mfma<_Float16, fp8_t>(pp, head_dim, st, &sup)
+                 : launch_prefill_mfma<_Float16, _Float16>(pp, head_dim, st, &sup);
     if (!sup) return MSATTN_ERR_UNSUPPORTED;
     return hip_status(e);
   }
@@ -545,7 +552,8 @@ int msattn_paged_attention_prefix(const void* query, const void* k_cache, const 
   if (workspace_bytes < X.total) return MSATTN_ERR_WORKSPACE;
   // The shared-prefix pass runs the MFMA prefill kernel; other types and head sizes,
   // and calls without a shared prefix, attend in one pass over the whole context.
-  const bool cascade = X.prefix > 0 && q_dtype == kv_dtype &&
+  const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
+  const bool cascade = X.prefix > 0 && (kv_dtype == q_dtype || kv_fp8) &&
                        (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) && head_dim == 128 &&
                        block_size % 16 == 0;
   if (!cascade)
@@ -594,8 +602,13 @@ int msattn_paged_attention_prefix(const void* query, const void* k_cache, const 
   if (static_cast<int64_t>(pp.rblocks) * num_kv_heads >= (int64_t(1) << 31) || X.npart > 65535)
     return MSATTN_ERR_UNSUPPORTED;
   bool sup = false;
-  hipError_t e = q_dtype == MSATTN_BF16 ? launch_prefix_partials<bf16_t>(pp, head_dim, st, &sup)
-                                        : launch_prefix_partials<_Float16>(pp, head_dim, st, &sup);
+  hipError_t e;
+  if (q_dtype == MSATTN_BF16)
+    e = kv_fp8 ? launch_prefix_partials<bf16_t, fp8_t>(pp, head_dim, st, &sup)
+               : launch_prefix_partials<bf16_t, bf16_t>(pp, head_dim, st, &sup);
+  else
+    e = kv_fp8 ? launch_prefix_partials<_Float16, fp8_t>(pp, head_dim, st, &sup)
+               : launch_prefix_partials<_Float16, _Float16>(pp, head_dim, st, &sup);
   if (!sup) return MSATTN_ERR_UNSUPPORTED;
   if (e != hipSuccess) return MSATTN_ERR_HIP;
 

@@ -95,8 +95,11 @@ struct PrefillParams {
   int key_part, npart;
 };
 
-template <typename T, int D, int RB, bool PX>
+template <typename T, typename KT, int D, int RB, bool PX>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillParams p) {
+  typedef Kv8<T, KT> KV;  // a cache of T, or fp8 e4m3 widened to T while staged into LDS
+  typedef typename KV::raw_t raw_t;
+  constexpr int EB = static_cast<int>(sizeof(KT));
   static_assert(D == 128, "prefill MFMA kernel handles head_dim 128");
   constexpr int JD = D / 32;              // k-steps of S^T
   constexpr int ND = D / 16;              // 16-dim tiles of O^T
@@ -223,8 +226,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     l_run[rb] = 0.0f;
   }
 
-  const T* kbase = static_cast<const T*>(p.k);
-  const T* vbase = static_cast<const T*>(p.v);
+  const KT* kbase = static_cast<const KT*>(p.k);
+  const KT* vbase = static_cast<const KT*>(p.v);
   const int step_first = hi_all > lo_all ? lo_all / kPfStep : 0;
   const int step_end = hi_all > lo_all ? ceil_div(hi_all, kPfStep) : 0;
 
@@ -233,9 +236,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int st_c = gtid % CPR;
   const int st_r = gtid / CPR;
   constexpr int ROWS_PER_PASS = kPfGroupThreads / CPR;
-  uint4 kst[LPT], vst[LPT];
+  raw_t kst[LPT], vst[LPT];
 #pragma unroll
-  for (int j = 0; j < LPT; ++j) kst[j] = vst[j] = make_uint4(0u, 0u, 0u, 0u);
+  for (int j = 0; j < LPT; ++j) kst[j] = vst[j] = KV::keep_if(raw_t{}, false);
   int pg_base = -(1 << 30);  // s_pg[i] = physical page of logical page pg_base + i
 
   auto page_of = [&](int tok) { return p.bs_shift >= 0 ? tok >> p.bs_shift : tok / p.bs; };
@@ -264,8 +267,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   // every lane (scalar), and a lane only adds its constant in-tile offset. Each tile is
   // read through a buffer descriptor whose size ends at the last row below hi_all (rows
   // past it, and tiles that are holes, read as zeros).
-  const uint32_t st_off = static_cast<uint32_t>((st_r * p.slot_stride + st_c * 8) * 2);
-  const int64_t row_bytes = p.slot_stride * 2;
+  const uint32_t st_off = static_cast<uint32_t>((st_r * p.slot_stride + st_c * 8) * EB);
+  const int64_t row_bytes = p.slot_stride * EB;
   auto issue = [&](int step) {
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
@@ -278,13 +281,13 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
                                           static_cast<int64_t>(t0 - pg * p.bs) * p.slot_stride +
                                           static_cast<int64_t>(kvh) * p.head_stride
                                     : 0;
-      const int nbytes = tile_in ? static_cast<int>((rows_valid - 1) * row_bytes + D * 2) : 0;
-      kst[j] = buffer_load16(tile_rsrc(kbase + tbase, nbytes), st_off);
-      vst[j] = buffer_load16(tile_rsrc(vbase + tbase, nbytes), st_off);
+      const int nbytes = tile_in ? static_cast<int>((rows_valid - 1) * row_bytes + D * EB) : 0;
+      kst[j] = KV::template load<0>(tile_rsrc(kbase + tbase, nbytes), st_off);
+      vst[j] = KV::template load<0>(tile_rsrc(vbase + tbase, nbytes), st_off);
       if (t0 < lo_all) {  // a window's first tile: rows below it are zeros too
         const bool keep = t0 + st_r >= lo_all;
-        kst[j] = keep ? kst[j] : make_uint4(0u, 0u, 0u, 0u);
-        vst[j] = keep ? vst[j] : make_uint4(0u, 0u, 0u, 0u);
+        kst[j] = KV::keep_if(kst[j], keep);
+        vst[j] = KV::keep_if(vst[j], keep);
       }
     }
   };
@@ -292,8 +295,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int r = st_r + ROWS_PER_PASS * j;
-      *reinterpret_cast<uint4*>(&s_k[grp][buf][r * RSK + st_c * 8]) = kst[j];
-      *reinterpret_cast<uint4*>(&s_v[grp][buf][r * RSV + st_c * 8]) = vst[j];
+      *reinterpret_cast<uint4*>(&s_k[grp][buf][r * RSK + st_c * 8]) = KV::operand(kst[j]);
+      *reinterpret_cast<uint4*>(&s_v[grp][buf][r * RSV + st_c * 8]) = KV::operand(vst[j]);
     }
   };
 
@@ -520,46 +523,61 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   }
 }
 
-template <typename T>
+template <typename T, typename KT>
 hipError_t launch_prefill_mfma_impl(const PrefillParams& p, int D, hipStream_t stream,
                                     bool* supported) {
   *supported = D == 128;
   if (!*supported) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(kXcds * p.xcd_per));
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, kPfRB, false>), grid, dim3(kPfThreads), 0, stream, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 128, kPfRB, false>), grid, dim3(kPfThreads), 0,
+                     stream, p);
   return hipGetLastError();
 }
 
-template <typename T>
+template <typename T, typename KT>
 hipError_t launch_prefix_partials_impl(const PrefillParams& p, int D, hipStream_t stream,
                                        bool* supported) {
   *supported = D == 128;
   if (!*supported) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(p.rblocks * p.KVH), static_cast<unsigned>(p.npart), 1);
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, 128, kPfRB, true>), grid, dim3(kPfThreads), 0, stream, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 128, kPfRB, true>), grid, dim3(kPfThreads), 0,
+                     stream, p);
   return hipGetLastError();
 }
 
-// Launch for T in {bf16_t, _Float16} (defined in prefill_mfma.hip, the translation unit
-// compiled with the MFMA-in-VGPR option); *supported = false unless head_dim is 128.
-template <typename T>
+// Launch for T in {bf16_t, _Float16} over a cache of T or of fp8 e4m3 (defined in
+// prefill_mfma.hip and prefill_mfma_fp8.hip, the translation units compiled with the
+// MFMA-in-VGPR option); *supported = false unless head_dim is 128.
+template <typename T, typename KT>
 hipError_t launch_prefill_mfma(const PrefillParams& p, int D, hipStream_t stream, bool* supported);
-template <>
-hipError_t launch_prefill_mfma<bf16_t>(const PrefillParams& p, int D, hipStream_t stream,
-                                       bool* supported);
-template <>
-hipError_t launch_prefill_mfma<_Float16>(const PrefillParams& p, int D, hipStream_t stream,
-                                         bool* supported);
-
 // The shared-prefix partials pass (PX kernels), same types.
-template <typename T>
+template <typename T, typename KT>
 hipError_t launch_prefix_partials(const PrefillParams& p, int D, hipStream_t stream,
                                   bool* supported);
-template <>
-hipError_t launch_prefix_partials<bf16_t>(const PrefillParams& p, int D, hipStream_t stream,
-                                          bool* supported);
-template <>
-hipError_t launch_prefix_partials<_Float16>(const PrefillParams& p, int D, hipStream_t stream,
-                                            bool* supported);
+
+#define MSATTN_DECLARE_PF(T, KT)                                                               \
+  template <>                                                                                  \
+  hipError_t launch_prefill_mfma<T, KT>(const PrefillParams& p, int D, hipStream_t stream,     \
+                                        bool* supported);                                      \
+  template <>                                                                                  \
+  hipError_t launch_prefix_partials<T, KT>(const PrefillParams& p, int D, hipStream_t stream,  \
+                                           bool* supported);
+MSATTN_DECLARE_PF(bf16_t, bf16_t)
+MSATTN_DECLARE_PF(_Float16, _Float16)
+MSATTN_DECLARE_PF(bf16_t, fp8_t)
+MSATTN_DECLARE_PF(_Float16, fp8_t)
+#undef MSATTN_DECLARE_PF
+
+#define MSATTN_DEFINE_PF(T, KT)                                                                \
+  template <>                                                                                  \
+  hipError_t launch_prefill_mfma<T, KT>(const PrefillParams& p, int D, hipStream_t stream,     \
+                                        bool* supported) {                                     \
+    return launch_prefill_mfma_impl<T, KT>(p, D, stream, supported);                           \
+  }                                                                                            \
+  template <>                                                                                  \
+  hipError_t launch_prefix_partials<T, KT>(const PrefillParams& p, int D, hipStream_t stream,  \
+                                           bool* supported) {                                  \
+    return launch_prefix_partials_impl<T, KT>(p, D, stream, supported);                        \
+  }
 
 }  // namespace msattn

@@ -217,6 +217,39 @@ def test_fp8_kv_mfma_equals_dequantized(device, H, KVH, D, dtype, wide, window):
     assert not got[0].any()
 
 
+@pytest.mark.parametrize("H,KVH,q_len,dtype,causal,window,prefix", [
+    (28, 4, 512, torch.bfloat16, True, None, 0),     # chunked prefill (C5 shape, smaller)
+    (32, 8, 100, torch.float16, True, 64, 0),        # fp16 query, sliding window
+    (16, 2, 48, torch.bfloat16, False, None, 0),     # non-causal
+    (32, 8, 1, torch.bfloat16, True, None, 12),      # cascade decode: the prefix pass
+])
+def test_fp8_kv_prefill_equals_dequantized(device, H, KVH, q_len, dtype, causal, window, prefix):
+    """The MFMA prefill kernel (and the cascade's shared-prefix pass, which runs on it) over
+    an fp8 cache widens the chunks exactly as it stages them: bit-exact against the same
+    kernel on the cache converted to the query type, and within tolerance of the oracle."""
+    note(f"fp8 prefill H={H} KVH={KVH} q_len={q_len} {dtype} causal={causal} window={window} "
+         f"prefix={prefix}")
+    D, bs = 128, 16
+    lens = [max(q_len, L) for L in (700, 2048, 1031, 4096)]
+    if prefix:
+        q, kc, vc, table = shared_prefix_case(H, KVH, D, lens, dtype, bs, prefix, 260, seed=21)
+    else:
+        q, kc, vc, table = paged_case(H, KVH, D, lens, dtype, bs, (max(lens) + bs - 1) // bs + 1,
+                                      seed=20, q_len=q_len)
+    kc8, vc8 = kc.to(torch.float8_e4m3fn), vc.to(torch.float8_e4m3fn)
+    kd, vd = kc8.to(dtype), vc8.to(dtype)
+    cap = table.shape[1] * bs
+    kw = dict(causal=causal, window=window, max_context=cap)
+    if prefix:
+        kw["prefix_pages"] = prefix
+    qd = q.to(device)
+    got = paged_attention(qd, kc8.to(device), vc8.to(device), table, lens, **kw)
+    want = paged_attention(qd, kd.to(device), vd.to(device), table, lens, **kw)
+    assert torch.equal(got, want)
+    ref = dense.paged_attention_f64(q, kc8, vc8, table, lens, causal=causal, window=window)
+    assert rel_err(got, ref) < BF16_REL
+
+
 def rope_tables(max_pos, D, base=10000.0):
     inv = 1.0 / (base ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
     emb = torch.outer(torch.arange(max_pos, dtype=torch.float32), inv)
