@@ -424,7 +424,8 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
   // prefill kernel writes the normalised output directly.
   if (q_len > 1 && (kv_dtype == q_dtype || kv_dtype == MSATTN_FP8_E4M3) &&
       (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
-      head_dim == 128 && block_size % 16 == 0 && batch <= 65535 && num_heads > 0 &&
+      (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 && batch <= 65535 &&
+      num_heads > 0 &&
       num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
       static_cast<int64_t>(q_len) * (num_heads / num_kv_heads) > 16) {
     if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
@@ -554,7 +555,8 @@ int msattn_paged_attention_prefix(const void* query, const void* k_cache, const 
   // and calls without a shared prefix, attend in one pass over the whole context.
   const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
   const bool cascade = X.prefix > 0 && (kv_dtype == q_dtype || kv_fp8) &&
-                       (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) && head_dim == 128 &&
+                       (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
+                       (head_dim == 64 || head_dim == 128) &&
                        block_size % 16 == 0;
   if (!cascade)
     return msattn_paged_attention(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,

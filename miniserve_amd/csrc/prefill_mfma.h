@@ -1,4 +1,5 @@
-// Chunked-prefill paged attention on MFMA (gfx950): q_len > 1, bf16/fp16, head_dim 128.
+// Chunked-prefill paged attention on MFMA (gfx950): q_len > 1, bf16/fp16 query (over a
+// cache of its type or of fp8 e4m3), head_dim 64 or 128.
 //
 // One workgroup owns 16 * RB * 4 query rows of one (sequence b, KV head): rows are the
 // (query token i, GQA head g) pairs r = i * group + g. It has two groups of 4 waves, one
@@ -20,9 +21,11 @@
 //     lane names 4 dims of one token; lane i of a 16-lane group receives dim i of four
 //     tokens). Lane (g, n) accumulates O[row n][dims 16t + 4g + r], so the softmax
 //     rescale stays in the lane.
-// LDS row strides are chosen per access: K rows are 68 dwords apart (4 mod 64 banks: the
-// 16 rows of a 16-byte-per-lane read fall on disjoint banks), V rows 72 dwords (8 mod 64:
-// the 8-byte transposed reads of 8 consecutive rows tile the 64 banks).
+// LDS row strides are chosen per access: K rows are D + 8 elements apart (68 dwords for
+// head_dim 128, 4 mod 64 banks; 36 for 64: 36 n mod 64 takes 16 distinct multiples of 4),
+// so the 16 rows of a 16-byte-per-lane read fall on disjoint banks; V rows D + 16 (72
+// dwords, 8 mod 64; or 40), so the 8-byte transposed reads of 8 consecutive rows tile the
+// 64 banks.
 // The rows' outputs are normalised and written directly (no split-K partials).
 //
 // Semantics: PagedAttention.forward with q_len > 1 (miniserve/attention.py:205-250,
@@ -100,11 +103,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   typedef Kv8<T, KT> KV;  // a cache of T, or fp8 e4m3 widened to T while staged into LDS
   typedef typename KV::raw_t raw_t;
   constexpr int EB = static_cast<int>(sizeof(KT));
-  static_assert(D == 128, "prefill MFMA kernel handles head_dim 128");
+  static_assert(D == 64 || D == 128, "prefill MFMA kernel handles head_dim 64 and 128");
   constexpr int JD = D / 32;              // k-steps of S^T
   constexpr int ND = D / 16;              // 16-dim tiles of O^T
-  constexpr int RSK = D + 8;              // K LDS row stride (elements): 68 dwords
-  constexpr int RSV = D + 16;             // V LDS row stride (elements): 72 dwords
+  constexpr int RSK = D + 8;              // K LDS row stride (elements): 68 / 36 dwords
+  constexpr int RSV = D + 16;             // V LDS row stride (elements): 72 / 40 dwords
   constexpr int CPR = D * 2 / 16;         // 16-byte chunks per K/V row
   constexpr int LPT = kPfStep * CPR / kPfGroupThreads;  // chunks per thread per tensor per step
   static_assert(LPT * kPfGroupThreads == kPfStep * CPR, "staging split");
@@ -232,10 +235,14 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int step_end = hi_all > lo_all ? ceil_div(hi_all, kPfStep) : 0;
 
   // Staging: a group's thread gtid loads chunk st_c of token rows st_r + ROWS_PER_PASS * j
-  // of the group's steps.
+  // of the group's steps. A pass covers ROWS_PER_PASS / 16 tiles of 16 tokens (1 for
+  // head_dim 128, 2 for 64); a wave's rows lie in one of them, tile st_tile of the pass.
   const int st_c = gtid % CPR;
   const int st_r = gtid / CPR;
   constexpr int ROWS_PER_PASS = kPfGroupThreads / CPR;
+  static_assert(ROWS_PER_PASS % 16 == 0 && kWave / CPR <= 16, "a wave's rows in one tile");
+  const int st_tile = ROWS_PER_PASS > 16 ? __builtin_amdgcn_readfirstlane(st_r / 16) : 0;
+  const int st_row = st_r % 16;
   raw_t kst[LPT], vst[LPT];
 #pragma unroll
   for (int j = 0; j < LPT; ++j) kst[j] = vst[j] = KV::keep_if(raw_t{}, false);
@@ -267,12 +274,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   // every lane (scalar), and a lane only adds its constant in-tile offset. Each tile is
   // read through a buffer descriptor whose size ends at the last row below hi_all (rows
   // past it, and tiles that are holes, read as zeros).
-  const uint32_t st_off = static_cast<uint32_t>((st_r * p.slot_stride + st_c * 8) * EB);
+  const uint32_t st_off = static_cast<uint32_t>((st_row * p.slot_stride + st_c * 8) * EB);
   const int64_t row_bytes = p.slot_stride * EB;
   auto issue = [&](int step) {
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
-      const int t0 = step * kPfStep + ROWS_PER_PASS * j;  // first token of tile j
+      const int t0 = step * kPfStep + ROWS_PER_PASS * j + 16 * st_tile;  // the wave's tile
       const int pg = page_of(t0);
       const int phys = __builtin_amdgcn_readfirstlane(s_pg[pg - pg_base]);
       const int rows_valid = min(16, hi_all - t0);
@@ -285,7 +292,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       kst[j] = KV::template load<0>(tile_rsrc(kbase + tbase, nbytes), st_off);
       vst[j] = KV::template load<0>(tile_rsrc(vbase + tbase, nbytes), st_off);
       if (t0 < lo_all) {  // a window's first tile: rows below it are zeros too
-        const bool keep = t0 + st_r >= lo_all;
+        const bool keep = t0 + st_row >= lo_all;
         kst[j] = KV::keep_if(kst[j], keep);
         vst[j] = KV::keep_if(vst[j], keep);
       }
@@ -526,28 +533,36 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 template <typename T, typename KT>
 hipError_t launch_prefill_mfma_impl(const PrefillParams& p, int D, hipStream_t stream,
                                     bool* supported) {
-  *supported = D == 128;
+  *supported = D == 64 || D == 128;
   if (!*supported) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(kXcds * p.xcd_per));
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 128, kPfRB, false>), grid, dim3(kPfThreads), 0,
-                     stream, p);
+  if (D == 128)
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 128, kPfRB, false>), grid, dim3(kPfThreads), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 64, kPfRB, false>), grid, dim3(kPfThreads), 0,
+                       stream, p);
   return hipGetLastError();
 }
 
 template <typename T, typename KT>
 hipError_t launch_prefix_partials_impl(const PrefillParams& p, int D, hipStream_t stream,
                                        bool* supported) {
-  *supported = D == 128;
+  *supported = D == 64 || D == 128;
   if (!*supported) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(p.rblocks * p.KVH), static_cast<unsigned>(p.npart), 1);
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 128, kPfRB, true>), grid, dim3(kPfThreads), 0,
-                     stream, p);
+  if (D == 128)
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 128, kPfRB, true>), grid, dim3(kPfThreads), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 64, kPfRB, true>), grid, dim3(kPfThreads), 0,
+                       stream, p);
   return hipGetLastError();
 }
 
 // Launch for T in {bf16_t, _Float16} over a cache of T or of fp8 e4m3 (defined in
 // prefill_mfma.hip and prefill_mfma_fp8.hip, the translation units compiled with the
-// MFMA-in-VGPR option); *supported = false unless head_dim is 128.
+// MFMA-in-VGPR option); *supported = false unless head_dim is 64 or 128.
 template <typename T, typename KT>
 hipError_t launch_prefill_mfma(const PrefillParams& p, int D, hipStream_t stream, bool* supported);
 // The shared-prefix partials pass (PX kernels), same types.

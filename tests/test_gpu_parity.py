@@ -217,19 +217,21 @@ def test_fp8_kv_mfma_equals_dequantized(device, H, KVH, D, dtype, wide, window):
     assert not got[0].any()
 
 
-@pytest.mark.parametrize("H,KVH,q_len,dtype,causal,window,prefix", [
-    (28, 4, 512, torch.bfloat16, True, None, 0),     # chunked prefill (C5 shape, smaller)
-    (32, 8, 100, torch.float16, True, 64, 0),        # fp16 query, sliding window
-    (16, 2, 48, torch.bfloat16, False, None, 0),     # non-causal
-    (32, 8, 1, torch.bfloat16, True, None, 12),      # cascade decode: the prefix pass
+@pytest.mark.parametrize("H,KVH,D,q_len,dtype,causal,window,prefix", [
+    (28, 4, 128, 512, torch.bfloat16, True, None, 0),     # chunked prefill (C5 shape)
+    (32, 8, 128, 100, torch.float16, True, 64, 0),        # fp16 query, sliding window
+    (16, 2, 128, 48, torch.bfloat16, False, None, 0),     # non-causal
+    (14, 2, 64, 200, torch.bfloat16, True, None, 0),      # head_dim 64
+    (32, 8, 128, 1, torch.bfloat16, True, None, 12),      # cascade decode: the prefix pass
 ])
-def test_fp8_kv_prefill_equals_dequantized(device, H, KVH, q_len, dtype, causal, window, prefix):
+def test_fp8_kv_prefill_equals_dequantized(device, H, KVH, D, q_len, dtype, causal, window,
+                                           prefix):
     """The MFMA prefill kernel (and the cascade's shared-prefix pass, which runs on it) over
     an fp8 cache widens the chunks exactly as it stages them: bit-exact against the same
     kernel on the cache converted to the query type, and within tolerance of the oracle."""
-    note(f"fp8 prefill H={H} KVH={KVH} q_len={q_len} {dtype} causal={causal} window={window} "
-         f"prefix={prefix}")
-    D, bs = 128, 16
+    note(f"fp8 prefill H={H} KVH={KVH} D={D} q_len={q_len} {dtype} causal={causal} "
+         f"window={window} prefix={prefix}")
+    bs = 16
     lens = [max(q_len, L) for L in (700, 2048, 1031, 4096)]
     if prefix:
         q, kc, vc, table = shared_prefix_case(H, KVH, D, lens, dtype, bs, prefix, 260, seed=21)
@@ -478,18 +480,22 @@ def test_streamk_graph_replays(device):
 
 # ------------------------------------------------------------------ chunked prefill (MFMA)
 
-@pytest.mark.parametrize("H,KVH,q_len,lens,dtype,causal,window", [
-    (28, 4, 512, [4608, 4608], torch.bfloat16, True, None),   # C5 prefill shape
-    (28, 4, 100, [100, 1000, 357], torch.bfloat16, True, None),
-    (32, 8, 17, [17, 40, 3000], torch.bfloat16, True, None),
-    (32, 8, 64, [64, 700], torch.float16, True, None),
-    (8, 8, 33, [33, 90], torch.bfloat16, False, None),        # non-causal
-    (28, 4, 200, [1200, 300], torch.bfloat16, True, 128),     # sliding window
-    (16, 2, 80, [50, 2000], torch.bfloat16, True, None),      # context shorter than the chunk
+@pytest.mark.parametrize("H,KVH,D,q_len,lens,dtype,causal,window", [
+    (28, 4, 128, 512, [4608, 4608], torch.bfloat16, True, None),   # C5 prefill shape
+    (28, 4, 128, 100, [100, 1000, 357], torch.bfloat16, True, None),
+    (32, 8, 128, 17, [17, 40, 3000], torch.bfloat16, True, None),
+    (32, 8, 128, 64, [64, 700], torch.float16, True, None),
+    (8, 8, 128, 33, [33, 90], torch.bfloat16, False, None),        # non-causal
+    (28, 4, 128, 200, [1200, 300], torch.bfloat16, True, 128),     # sliding window
+    (16, 2, 128, 80, [50, 2000], torch.bfloat16, True, None),      # context shorter than the chunk
+    # head_dim 64 (Qwen2.5-0.5B geometry): a staging pass spans two 16-token tiles
+    (14, 2, 64, 512, [2560, 600], torch.bfloat16, True, None),
+    (14, 2, 64, 37, [37, 1500, 90], torch.float16, True, 100),
+    (8, 8, 64, 40, [40, 333], torch.bfloat16, False, None),
 ])
-def test_prefill_mfma(device, H, KVH, q_len, lens, dtype, causal, window):
-    note(f"prefill H={H} KVH={KVH} q_len={q_len} lens={lens} {dtype} causal={causal} window={window}")
-    D = 128
+def test_prefill_mfma(device, H, KVH, D, q_len, lens, dtype, causal, window):
+    note(f"prefill H={H} KVH={KVH} D={D} q_len={q_len} lens={lens} {dtype} causal={causal} "
+         f"window={window}")
     g = torch.Generator().manual_seed(q_len + H)
     width = max((L + 15) // 16 for L in lens) + 3
     q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=q_len)
@@ -580,8 +586,9 @@ CASCADE_CASES = [  # (H, KVH, D, dtype, bs, lens, prefix pages, table width in p
     (32, 8, 128, torch.bfloat16, 16, [30000, 9000, 20000, 1000], 256, 2048),
     # every key in the prefix: the suffix pass has no work
     (32, 8, 128, torch.bfloat16, 16, [480, 480, 480], 30, 30),
-    # without cascade kernels (head_dim 64, fp32): one pass over the whole context
+    # head_dim 64 (the prefix pass on the head_dim-64 prefill kernel)
     (14, 2, 64, torch.bfloat16, 16, [300, 50, 900], 8, 60),
+    # without cascade kernels (fp32): one pass over the whole context
     (4, 2, 64, torch.float32, 16, [300, 50, 900], 8, 60),
 ]
 
