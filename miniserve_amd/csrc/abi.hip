@@ -17,7 +17,7 @@ using namespace msattn;
 
 constexpr int kPartitionChoices[] = {kPartMax, kPartMax / 2, kPartMax / 4};
 #ifndef MSATTN_TARGET_SLOTS
-#define MSATTN_TARGET_SLOTS 1024
+#define MSATTN_TARGET_SLOTS 512
 #endif
 constexpr int64_t kTargetSlots = MSATTN_TARGET_SLOTS;  // workgroup slots wanted in a launch
 #ifndef MSATTN_STREAMK_MIN_TILES
