@@ -114,9 +114,17 @@ Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, i
 }
 
 // Cascade decode: the shared-prefix pass splits the prefix into npart key partitions
-// so that (row blocks x KV heads x npart) workgroups about fill the chip (kSkGrid), each
-// at least kPxMinPart tokens; its partials follow the regular workspace layout.
-constexpr int kPxMinPart = 2 * kPfStep;
+// so that (row blocks x KV heads x npart) workgroups about reach kPxGrid, each at least
+// kPxMinPart tokens; its partials follow the regular workspace layout.
+#ifndef MSATTN_PX_GRID
+#define MSATTN_PX_GRID 256
+#endif
+#ifndef MSATTN_PX_MIN_PART
+#define MSATTN_PX_MIN_PART 128
+#endif
+constexpr int kPxGrid = MSATTN_PX_GRID;          // workgroups the prefix pass aims for
+constexpr int kPxMinPart = MSATTN_PX_MIN_PART;   // shortest key partition (tokens)
+static_assert(kPxMinPart % kPfStep == 0, "partitions of whole steps");
 struct PrefixLayout {
   Layout base;
   int prefix;     // shared tokens
@@ -134,7 +142,7 @@ PrefixLayout prefix_layout(int batch, int num_heads, int num_kv_heads, int head_
   X.prefix = static_cast<int>(pt < max_context ? pt : max_context);
   const int rblocks = ceil_div(batch * (num_heads / num_kv_heads), kPfRows);
   const int64_t per_part = static_cast<int64_t>(rblocks) * num_kv_heads;
-  int want = static_cast<int>(ceil_div(static_cast<int64_t>(kSkGrid), per_part));
+  int want = static_cast<int>((kPxGrid + per_part - 1) / per_part);
   const int most = X.prefix > 0 ? ceil_div(X.prefix, kPxMinPart) : 1;
   want = want < 1 ? 1 : (want > most ? most : want);
   X.key_part = X.prefix > 0 ? ceil_div(ceil_div(X.prefix, want), kPfStep) * kPfStep : kPfStep;
