@@ -39,7 +39,7 @@ constexpr int kSkTableRun = 64;     // tile page ids fetched per table load
 #define MSATTN_SK_DEPTH 2
 #endif
 #ifndef MSATTN_SK_DEPTH_FP8
-#define MSATTN_SK_DEPTH_FP8 4
+#define MSATTN_SK_DEPTH_FP8 2
 #endif
 #ifndef MSATTN_SK_ROUNDS
 #define MSATTN_SK_ROUNDS 1
