@@ -17,9 +17,9 @@
 //    pi(4g + r), r = 0..3.
 //  * pi is chosen so that the 16-lane row g that holds those scores is also the
 //    row whose V lanes need them: V is loaded with LPR = D/8 lanes per token row,
-//    and the tokens of V lanes in DPP row g are exactly {pi(4g + r)}. The P.V
-//    FMAs then take P[n][token] from lane 16g + n through DPP row_newbcast,
-//    without LDS traffic.
+//    and the tokens of V lanes in DPP row g are exactly {pi(4g + r)}. P.V then
+//    takes P[n][token] from lane 16g + n through DPP row_newbcast, without LDS
+//    traffic, two tokens at a time on v_dot2_f32 (pv_tile below).
 //  * The 4 waves' (m, l, acc) are combined in LDS once at the end.
 //
 // Masking, key ranges and the partial format follow split_kernel and hence

@@ -18,9 +18,12 @@
 // [id][unit in group][row]. Workgroup 0 writes the layout (chunk size, prefix sums
 // of T_b) into the workspace header; merge.hip finds a row's pieces from it.
 //
-// The per-tile arithmetic is decode_mfma.h's: MFMA scores, online softmax, P.V
-// with DPP row broadcasts, two tiles' loads in flight through per-tile buffer
-// descriptors. The algorithm is the split decomposition of
+// The per-tile arithmetic is decode_mfma.h's: MFMA scores, online softmax, P.V on
+// v_dot2 with DPP row broadcasts, a ring of per-tile buffer descriptors keeping the
+// next tiles' loads in flight. A wave walks its chunk in runs of up to kSkTableRun
+// tiles and requests the next run's page ids (and, at a sequence boundary, the next
+// piece's query rows) before it streams the current one. The algorithm is the split
+// decomposition of
 // kernels/paged_attn_triton.py:102-171 with the masking of
 // miniserve/attention.py:135-153 (for q_len == 1: keys in [ctx - window, ctx)).
 #pragma once
