@@ -330,6 +330,57 @@ def test_shape_fuzz_50(device):
         assert err < FP32_ATOL, f"shape #{i}: err {err}"
 
 
+def test_mfma_routes_fuzz(device):
+    """Seeded shapes over every MFMA route (partition and stream-K decode, short q_len on
+    the decode kernel, chunked prefill, cascade decode), bf16/fp16 queries over caches of
+    their type or fp8, head_dim 64/128, pages of 16..64 tokens, windows, non-causal rows
+    and contexts shorter than the chunk: each against the float64 oracle."""
+    for i in range(40):
+        gen = torch.Generator().manual_seed(5000 + i)
+        pick = lambda seq: seq[int(torch.randint(0, len(seq), (1,), generator=gen))]
+        D = pick((64, 128))
+        KVH = pick((1, 2, 4, 8))
+        G = pick((1, 2, 4, 5, 7, 8, 16))
+        H = KVH * G
+        dtype = pick((torch.bfloat16, torch.float16))
+        kv_dtype = pick((dtype, dtype, torch.float8_e4m3fn))
+        bs = pick((16, 32, 48, 64))
+        B = int(torch.randint(1, 5, (1,), generator=gen))
+        route = pick(("decode", "decode", "wide", "short", "prefill", "prefill", "cascade"))
+        q_len = {"short": int(torch.randint(2, 4, (1,), generator=gen)),
+                 "prefill": int(torch.randint(8, 41, (1,), generator=gen))}.get(route, 1)
+        lens = [int(torch.randint(1, 1500, (1,), generator=gen)) for _ in range(B)]
+        if route == "prefill":
+            lens = [max(L, 1) for L in lens]
+        causal = route != "prefill" or bool(torch.randint(0, 4, (1,), generator=gen))
+        window = (pick((None, None, 64, 300)) if route in ("decode", "wide", "prefill")
+                  and causal else None)
+        pages = max((L + bs - 1) // bs for L in lens)
+        width = pages + 2
+        if route == "wide":
+            width = max(width, -(-65536 * 16 // (B * KVH * bs)))
+        prefix = 0
+        if route == "cascade":
+            prefix = int(torch.randint(1, max(2, min(lens) // bs + 2), (1,), generator=gen))
+            width = max(width, prefix + 1)
+        note(f"fuzz #{i} {route} B={B} H={H} KVH={KVH} D={D} q_len={q_len} {dtype} "
+             f"kv={kv_dtype} bs={bs} width={width} causal={causal} window={window} "
+             f"prefix={prefix} lens={lens}")
+        if prefix:
+            q, kc, vc, table = shared_prefix_case(H, KVH, D, lens, dtype, bs, prefix, width,
+                                                  seed=i)
+        else:
+            q, kc, vc, table = paged_case(H, KVH, D, lens, dtype, bs, width, seed=i, q_len=q_len)
+        kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+        kw = dict(causal=causal, window=window, max_context=width * bs)
+        if prefix:
+            kw["prefix_pages"] = prefix
+        out = run_hip(device, q, kc, vc, table, lens, **kw)
+        ref = dense.paged_attention_f64(q, kc, vc, table, lens, causal=causal, window=window)
+        err = rel_err(out, ref)
+        assert err < BF16_REL, f"fuzz #{i}: max-rel {err}"
+
+
 # ------------------------------------------------------------------ edge cases
 
 def test_ragged_zero_and_one(device):
