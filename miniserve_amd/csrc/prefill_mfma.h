@@ -276,12 +276,19 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   // past it, and tiles that are holes, read as zeros).
   const uint32_t st_off = static_cast<uint32_t>((st_row * p.slot_stride + st_c * 8) * EB);
   const int64_t row_bytes = p.slot_stride * EB;
-  auto issue = [&](int step) {
+  // The page ids of a step's tiles are read from the window ahead of the loads (plan),
+  // so the LDS latency of the lookups is not paid in front of each tile's loads.
+  auto plan = [&](int step, int (&phys)[LPT]) {
+#pragma unroll
+    for (int j = 0; j < LPT; ++j)
+      phys[j] = s_pg[page_of(step * kPfStep + ROWS_PER_PASS * j + 16 * st_tile) - pg_base];
+  };
+  auto issue = [&](int step, const int (&phys_planned)[LPT]) {
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int t0 = step * kPfStep + ROWS_PER_PASS * j + 16 * st_tile;  // the wave's tile
       const int pg = page_of(t0);
-      const int phys = __builtin_amdgcn_readfirstlane(s_pg[pg - pg_base]);
+      const int phys = __builtin_amdgcn_readfirstlane(phys_planned[j]);
       const int rows_valid = min(16, hi_all - t0);
       const bool tile_in = phys >= 0 && rows_valid > 0 && t0 + 16 > lo_all;
       const int64_t tbase = tile_in ? static_cast<int64_t>(phys) * p.blk_stride +
@@ -449,9 +456,16 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int s_first = step_first + grp;
   if (step_first < step_end) {
     ensure_pages(step_first, min(step_first + 3, step_end - 1));
-    if (s_first < step_end) issue(s_first);
+    int ph[LPT];
+    if (s_first < step_end) {
+      plan(s_first, ph);
+      issue(s_first, ph);
+    }
     stage(0);
-    if (s_first + 2 < step_end) issue(s_first + 2);
+    if (s_first + 2 < step_end) {
+      plan(s_first + 2, ph);
+      issue(s_first + 2, ph);
+    }
   }
   // Everything loaded before the loop (query rows, the first steps) has landed: the
   // loop then only waits for its own staging loads, not for every load in flight.
@@ -461,13 +475,16 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   for (int i = 0; i < npairs; ++i) {
     const int step = s_first + 2 * i;
     const int buf = i & 1;
-    if (step < step_end) compute(step, buf);
-    if (step + 2 < step_end) stage(buf ^ 1);  // its readers finished before the last barrier
+    // The page ids of this iteration's prefetch (step + 4) are read before the compute.
     const int pair_next = step_first + 2 * i + 4;  // the next prefetch, uniform over groups
+    int ph_next[LPT];
     if (pair_next < step_end) {
       ensure_pages(pair_next, min(pair_next + 1, step_end - 1));
-      if (step + 4 < step_end) issue(step + 4);
+      if (step + 4 < step_end) plan(step + 4, ph_next);
     }
+    if (step < step_end) compute(step, buf);
+    if (step + 2 < step_end) stage(buf ^ 1);  // its readers finished before the last barrier
+    if (step + 4 < step_end) issue(step + 4, ph_next);
     __syncthreads();  // buf ^ 1 is written; buf's reads are done
   }
 
