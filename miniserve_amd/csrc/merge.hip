@@ -22,7 +22,10 @@ namespace msattn {
 constexpr int kMergeThreads = 256;
 constexpr int kMergeWaves = kMergeThreads / kWave;
 constexpr int kMergeMaxDims = 4;  // dims per lane: head_dim <= 256
-constexpr int kMergeBatch = 8;    // acc rows loaded together
+#ifndef MSATTN_MERGE_BATCH
+#define MSATTN_MERGE_BATCH 8
+#endif
+constexpr int kMergeBatch = MSATTN_MERGE_BATCH;  // acc rows loaded together
 
 template <typename QT>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams p) {
