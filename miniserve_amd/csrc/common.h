@@ -161,23 +161,6 @@ template <> struct Chunk<fp8_t> {
   }
 };
 
-// ---------------------------------------------------------------------------
-// Cross-lane reductions over aligned groups of `Width` lanes (power of two).
-// ---------------------------------------------------------------------------
-template <int Width>
-__device__ __forceinline__ float group_sum(float x) {
-#pragma unroll
-  for (int o = Width / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, kWave);
-  return x;
-}
-
-template <int Width>
-__device__ __forceinline__ float group_max(float x) {
-#pragma unroll
-  for (int o = Width / 2; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));
-  return x;
-}
-
 // Max over the four 16-lane rows of the wave (lanes n, n + 16, n + 32, n + 48, for
 // each n), every lane receiving it. gfx950's row swaps exchange rows 2k <-> 2k + 1
 // (v_permlane16_swap) and the halves (v_permlane32_swap) of a register pair in the
@@ -209,6 +192,66 @@ __device__ __forceinline__ float rows4_sum(float v) {
   v += __shfl_xor(v, 16, kWave);
   return v + __shfl_xor(v, 32, kWave);
 #endif
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane reductions over aligned groups of `Width` lanes (power of two), every
+// lane of a group receiving the result. Within a 16-lane row they run on DPP lane
+// permutes (VALU): quad_perm [1,0,3,2] and [2,3,0,1] pair lanes i ^ 1 and i ^ 2,
+// row_half_mirror then pairs the two quads of an 8-lane half (lane i with 7 - i) and
+// row_mirror the two halves of the row (lane i with 15 - i); wider groups add the row
+// swaps of rows4_max / rows4_sum. (MSATTN_ROW_SWAPS=0: lane shuffles throughout.)
+// ---------------------------------------------------------------------------
+template <int Ctrl>
+__device__ __forceinline__ float dpp_mov(float v) {
+  const int x = __float_as_int(v);
+  return __int_as_float(__builtin_amdgcn_update_dpp(x, x, Ctrl, 0xF, 0xF, false));
+}
+
+template <int Width>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(Width >= 1 && Width <= 64 && (Width & (Width - 1)) == 0, "power-of-two width");
+#if MSATTN_ROW_SWAPS
+  if constexpr (Width >= 2) x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]
+  if constexpr (Width >= 4) x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]
+  if constexpr (Width >= 8) x += dpp_mov<0x141>(x);  // row_half_mirror
+  if constexpr (Width >= 16) x += dpp_mov<0x140>(x); // row_mirror
+  if constexpr (Width >= 32) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  }
+  if constexpr (Width >= 64) {
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  }
+#else
+#pragma unroll
+  for (int o = Width / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, kWave);
+#endif
+  return x;
+}
+
+template <int Width>
+__device__ __forceinline__ float group_max(float x) {
+  static_assert(Width >= 1 && Width <= 64 && (Width & (Width - 1)) == 0, "power-of-two width");
+#if MSATTN_ROW_SWAPS
+  if constexpr (Width >= 2) x = fmaxf(x, dpp_mov<0xB1>(x));
+  if constexpr (Width >= 4) x = fmaxf(x, dpp_mov<0x4E>(x));
+  if constexpr (Width >= 8) x = fmaxf(x, dpp_mov<0x141>(x));
+  if constexpr (Width >= 16) x = fmaxf(x, dpp_mov<0x140>(x));
+  if constexpr (Width >= 32) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  }
+  if constexpr (Width >= 64) {
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  }
+#else
+#pragma unroll
+  for (int o = Width / 2; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));
+#endif
+  return x;
 }
 
 __host__ __device__ constexpr int next_pow2(int x) {
