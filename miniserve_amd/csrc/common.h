@@ -254,6 +254,102 @@ __device__ __forceinline__ float group_max(float x) {
   return x;
 }
 
+// ---------------------------------------------------------------------------
+// Strided reduce-scatter: sums R x E values per lane over the lanes of equal
+// lane % Stride (Stride a power of two, 1..64), leaving each lane a 1/P share of the
+// totals, P = rs_parts(Stride) (4 below 32, 2 at 32, 1 at 64). A lane of share s =
+// rs_share<Stride>(lane) ends with out[i] = sum of acc[i / per][s * per + i % per],
+// per = E / P, i < R * per: a run of per consecutive elements of each row.
+//
+// A row swap of two different registers exchanges half of each: v_permlane32_swap(a, b)
+// leaves (a_lo, b_lo) and (a_hi, b_hi), so their sum holds a's total over the halves in
+// lanes 0-31 and b's in lanes 32-63, and v_permlane16_swap does the same for rows
+// 2k / 2k + 1. One swap and one add thus fold two values where an all-lanes reduction
+// needs two swaps, two copies and two adds; after both swaps row rho holds input value
+// 4i + (rho bit-reversed). Strides below 16 finish with DPP row rotations inside a row.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int rs_parts(int stride) {
+  return stride >= 64 ? 1 : (stride == 32 ? 2 : 4);
+}
+
+template <int Stride>
+__device__ __forceinline__ int rs_share(int lane) {
+  constexpr int P = rs_parts(Stride);
+  if constexpr (P == 4) {
+    const int rho = lane >> 4;
+    return ((rho & 1) << 1) | (rho >> 1);
+  } else if constexpr (P == 2) {
+    return lane >> 5;
+  } else {
+    return 0;
+  }
+}
+
+// True for the lanes whose shares are distinct: below stride 16 the lanes of a row
+// that differ only above lane % Stride hold copies.
+template <int Stride>
+__device__ __forceinline__ bool rs_owner(int lane) {
+  if constexpr (Stride >= 16) return true;
+  else return (lane & 15) < Stride;
+}
+
+template <int Stride, int R, int E>
+__device__ __forceinline__ void reduce_scatter(const float (&acc)[R][E],
+                                               float (&out)[R * E / rs_parts(Stride)]) {
+  static_assert(Stride >= 1 && Stride <= 64 && (Stride & (Stride - 1)) == 0, "stride 1..64");
+  constexpr int P = rs_parts(Stride);
+  static_assert(E % P == 0, "row length must split into the shares");
+  constexpr int per = E / P;
+  constexpr int N = R * E;
+  float x[N];
+#pragma unroll
+  for (int i = 0; i < N / P; ++i)
+#pragma unroll
+    for (int s = 0; s < P; ++s) x[P * i + s] = acc[i / per][s * per + i % per];
+#if MSATTN_ROW_SWAPS
+  if constexpr (P >= 2) {
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[2 * j]),
+                                                      __float_as_uint(x[2 * j + 1]), false, false);
+      x[j] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+    }
+  }
+  if constexpr (P == 4) {
+#pragma unroll
+    for (int j = 0; j < N / 4; ++j) {
+      const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[2 * j]),
+                                                      __float_as_uint(x[2 * j + 1]), false, false);
+      x[j] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+    }
+  }
+  if constexpr (Stride < 16) {
+#pragma unroll
+    for (int j = 0; j < N / P; ++j) {
+      if constexpr (Stride <= 1) x[j] += dpp_mov<0x121>(x[j]);  // row_ror:1
+      if constexpr (Stride <= 2) x[j] += dpp_mov<0x122>(x[j]);  // row_ror:2
+      if constexpr (Stride <= 4) x[j] += dpp_mov<0x124>(x[j]);  // row_ror:4
+      x[j] += dpp_mov<0x128>(x[j]);                             // row_ror:8
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < N / P; ++j) out[j] = x[j];
+#else
+  const int s = rs_share<Stride>(__lane_id());
+#pragma unroll
+  for (int j = 0; j < N; ++j)
+#pragma unroll
+    for (int o = Stride; o < kWave; o <<= 1) x[j] += __shfl_xor(x[j], o, kWave);
+#pragma unroll
+  for (int i = 0; i < N / P; ++i) {
+    float v = x[P * i];
+#pragma unroll
+    for (int t = 1; t < P; ++t) v = s == t ? x[P * i + t] : v;
+    out[i] = v;
+  }
+#endif
+}
+
 __host__ __device__ constexpr int next_pow2(int x) {
   int p = 1;
   while (p < x) p <<= 1;

@@ -561,48 +561,53 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     consume(k + 1, k1, v1, base1);
   }
 
-  // Wave totals: l over the 4 lane groups, acc over the V token groups.
+  // Wave totals: l over the 4 lane groups, acc over the V token groups (lanes of equal
+  // lane % LPR), reduce-scattered so a lane keeps two dims of each row: dims
+  // vc * 8 + 2 * share + {0, 1}.
   l_run = rows4_sum(l_run);
-#pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float a = acc[r][e];
-#pragma unroll
-      for (int o = LPR; o < kWave; o <<= 1) a += __shfl_xor(a, o, kWave);
-      acc[r][e] = a;
-    }
+  float red[RT * 2];
+  reduce_scatter<LPR>(acc, red);
   if (lane < RT) {
     s_ml[w][lane][0] = m_run;
     s_ml[w][lane][1] = l_run;
   }
-  if (va == 0) {
+  if (rs_owner<LPR>(lane)) {
+    const int d0 = vc * 8 + 2 * rs_share<LPR>(lane);
 #pragma unroll
     for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s_red[w][r][vc * 8 + e] = acc[r][e];
+      *reinterpret_cast<float2*>(&s_red[w][r][d0]) = make_float2(red[2 * r], red[2 * r + 1]);
   }
   __syncthreads();
 
-  // Combine the waves: rescale each to the common max.
-  for (int idx = tid; idx < nrows * D; idx += kMfmaThreads) {
-    const int r = idx / D;
-    const int d = idx - r * D;
+  // Combine the waves, four dims a thread: rescale each wave to the common max.
+  constexpr int D4 = D / 4;
+  for (int idx = tid; idx < nrows * D4; idx += kMfmaThreads) {
+    const int r = idx / D4;
+    const int d = (idx - r * D4) * 4;
+    float mw[kMfmaWaves];
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < kMfmaWaves; ++ww) M = fmaxf(M, s_ml[ww][r][0]);
-    float a = 0.0f;
+    for (int ww = 0; ww < kMfmaWaves; ++ww) {
+      mw[ww] = s_ml[ww][r][0];
+      M = fmaxf(M, mw[ww]);
+    }
+    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (M != -INFINITY) {
 #pragma unroll
       for (int ww = 0; ww < kMfmaWaves; ++ww) {
-        const float mw = s_ml[ww][r][0];
-        if (mw != -INFINITY) a = fmaf(s_red[ww][r][d], exp2f(mw - M), a);
+        if (mw[ww] == -INFINITY) continue;
+        const float f = __builtin_amdgcn_exp2f(mw[ww] - M);
+        const float4 v = *reinterpret_cast<const float4*>(&s_red[ww][r][d]);
+        a.x = fmaf(v.x, f, a.x);
+        a.y = fmaf(v.y, f, a.y);
+        a.z = fmaf(v.z, f, a.z);
+        a.w = fmaf(v.w, f, a.w);
       }
     }
     const int gr = row0 + r;
     const int i = gr / p.G;
     const int64_t orow = (static_cast<int64_t>(b) * p.q_len + i) * p.H + (kvh * p.G + (gr - i * p.G));
-    p.acc[(orow * p.max_parts + part) * D + d] = a;
+    *reinterpret_cast<float4*>(p.acc + (orow * p.max_parts + part) * D + d) = a;
   }
   if (tid < nrows) {
     float M = -INFINITY;
@@ -613,7 +618,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
 #pragma unroll
       for (int ww = 0; ww < kMfmaWaves; ++ww) {
         const float mw = s_ml[ww][tid][0];
-        if (mw != -INFINITY) L = fmaf(s_ml[ww][tid][1], exp2f(mw - M), L);
+        if (mw != -INFINITY) L = fmaf(s_ml[ww][tid][1], __builtin_amdgcn_exp2f(mw - M), L);
       }
     }
     float* ml = p.ml + (orow_n * p.max_parts + part) * 2;

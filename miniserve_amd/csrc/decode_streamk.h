@@ -354,24 +354,18 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
     if (!more_here) {
       // ---- wave totals and the piece's partial ----
       l_run = rows4_sum(l_run);
-#pragma unroll
-      for (int rr = 0; rr < RT; ++rr)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float a = acc[rr][e];
-#pragma unroll
-          for (int oo = LPR; oo < kWave; oo <<= 1) a += __shfl_xor(a, oo, kWave);
-          acc[rr][e] = a;
-        }
+      // acc over the V token groups (lanes of equal lane % LPR), reduce-scattered: a
+      // lane keeps dims vc * 8 + 2 * share + {0, 1} of each row.
+      float red[RT * 2];
+      reduce_scatter<LPR>(acc, red);
       const int64_t slot0 = (cur.pid * UG + ul) * RT;  // this unit's rows in the piece
-      if (va == 0) {
+      if (rs_owner<LPR>(lane)) {
+        const int d0 = vc * 8 + 2 * rs_share<LPR>(lane);
 #pragma unroll
         for (int rr = 0; rr < RT; ++rr) {
-          if (rr < cur.nrows) {
-            float* dst = p.acc + (slot0 + rr) * D + vc * 8;
-            *reinterpret_cast<float4*>(dst) = make_float4(acc[rr][0], acc[rr][1], acc[rr][2], acc[rr][3]);
-            *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[rr][4], acc[rr][5], acc[rr][6], acc[rr][7]);
-          }
+          if (rr < cur.nrows)
+            *reinterpret_cast<float2*>(p.acc + (slot0 + rr) * D + d0) =
+                make_float2(red[2 * rr], red[2 * rr + 1]);
         }
       }
       if (lane < cur.nrows) {

@@ -334,22 +334,19 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
     }
   }
 
-  // Reduce over the TPI token groups of the wave (lanes c, c + LPR, ...).
-#pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      float a = acc[r][e];
-#pragma unroll
-      for (int o = LPR; o < kWave; o <<= 1) a += __shfl_xor(a, o, kWave);
-      acc[r][e] = a;
-    }
+  // Reduce over the TPI token groups of the wave (lanes c, c + LPR, ...), reduce-scattered:
+  // a lane keeps elements share * PER .. + PER - 1 of its chunk in every row.
+  constexpr int RSP = rs_parts(LPR);
+  constexpr int PER = EPL / RSP;
+  float red[RT * PER];
+  reduce_scatter<LPR>(acc, red);
   __syncthreads();  // every wave is done reading weights from s_sc
-  if (tg == 0 && c_ok) {
+  if (rs_owner<LPR>(lane) && c_ok) {
+    const int e0 = c * EPL + rs_share<LPR>(lane) * PER;
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) s_sc[(w * RT + r) * D + c * EPL + e] = acc[r][e];
+      for (int e = 0; e < PER; ++e) s_sc[(w * RT + r) * D + e0 + e] = red[r * PER + e];
   }
   __syncthreads();
 
