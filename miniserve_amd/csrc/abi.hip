@@ -62,7 +62,10 @@ int largest_pow2_divisor_upto(int x, int cap) {
 
 // Stream-K grid: one 8-wave workgroup per CU (MI355X has 256 CUs); devices with
 // fewer CUs launch fewer.
-constexpr int kSkGrid = 256;
+#ifndef MSATTN_SK_GRID
+#define MSATTN_SK_GRID 256
+#endif
+constexpr int kSkGrid = MSATTN_SK_GRID;
 #ifndef MSATTN_SK_MIN_CHUNK
 #define MSATTN_SK_MIN_CHUNK 4
 #endif
@@ -322,7 +325,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
     const int units = num_kv_heads * p.rtiles;
     p.sk_group = largest_pow2_divisor_upto(units, kSkWaves);
     p.sk_unit_groups = units / p.sk_group;
-    const int grid = device_cus() < kSkGrid ? device_cus() : kSkGrid;
+    const int grid = device_cus() < 256 ? kSkGrid * device_cus() / 256 : kSkGrid;
     if (q_dtype == MSATTN_BF16)
       e = kv_fp8 ? launch_decode_streamk<bf16_t, fp8_t>(p, head_dim, RT, grid, st, &sup)
                  : launch_decode_streamk<bf16_t, bf16_t>(p, head_dim, RT, grid, st, &sup);

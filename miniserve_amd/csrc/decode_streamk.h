@@ -32,7 +32,14 @@
 
 namespace msattn {
 
-constexpr int kSkWaves = 8;
+// Waves per workgroup: one per SIMD. With two waves on a SIMD the older one's loads
+// win every issue slot of a saturated memory pipe, so the younger one streams only after
+// the older has finished its chunk; the page's other heads are then read late, and the
+// kernel's end is set by the starved half.
+#ifndef MSATTN_SK_WAVES
+#define MSATTN_SK_WAVES 4
+#endif
+constexpr int kSkWaves = MSATTN_SK_WAVES;
 constexpr int kSkThreads = kSkWaves * kWave;
 constexpr int kSkMaxBatch = 4096;   // sequences per launch on this path
 constexpr int kSkTableRun = 64;     // tile page ids fetched per table load
