@@ -248,7 +248,13 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
 
   // Runs of up to kSkTableRun tiles, piece after piece. The next run's page ids (and a
   // new piece's query rows) are requested before this run streams, so they have landed
-  // when it starts: a piece boundary costs no page-table round trip.
+  // when it starts: a piece boundary costs no page-table round trip. The tile ring runs
+  // on across runs: a run is rounded up to whole ring turns (the extra tiles read
+  // nothing), and its last turn already issues the next run's first tiles, whose loads
+  // are in flight while the piece's partial is written.
+  raw_t kq[DEPTH][JD], vq[DEPTH][NJ];
+  int64_t bq[DEPTH];
+  bool primed = false;  // the ring holds the run's first DEPTH - 1 tiles
   while (true) {
     const bool more_here = run0 + kSkTableRun < cur.ntiles;
     const bool next_piece = !more_here && cur.pe < s_end;
@@ -260,14 +266,24 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
       run_n = 0;
       load_q(nxt, qn);
     }
-    const int64_t base_n = (more_here || next_piece) ? table_run(nxt, run_n) : -1;
+    const bool has_next = more_here || next_piece;
+    const int64_t base_n = has_next ? table_run(nxt, run_n) : -1;
 
     const int nt = min(kSkTableRun, cur.ntiles - run0);
+    const int nt_ring = (nt + STEP - 1) / STEP * STEP;  // positions the ring walks
+    const int nt_next = has_next ? min(kSkTableRun, nxt.ntiles - run_n) : 0;
+    // Ring position k: tile k of this run, nothing (k < nt_ring), or tile k - nt_ring
+    // of the next run.
     auto tile_base = [&](int k) -> int64_t {
-      if (k >= nt) return -1;
+      int64_t src = my_base;
+      if (k >= nt) {
+        k -= nt_ring;
+        if (k < 0 || k >= nt_next) return -1;
+        src = base_n;
+      }
       const uint32_t lo = static_cast<uint32_t>(
-          __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(my_base)), k));
-      const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
+          __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(src)), k));
+      const int hi = __builtin_amdgcn_readlane(static_cast<int>(src >> 32), k);
       return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
     };
     auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) {
@@ -336,16 +352,16 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
 
     // A ring of DEPTH tile buffers: DEPTH - 1 tiles' loads stay in flight while a
     // tile is consumed, the next tile's loads going into the slot just freed.
-    // A tile index >= nt reads nothing and adds nothing (its descriptor has no
-    // records, all its keys are masked).
+    // A position in [nt, nt_ring) reads nothing and adds nothing (its descriptor has
+    // no records, all its keys are masked).
     {
-      raw_t kq[DEPTH][JD], vq[DEPTH][NJ];
-      int64_t bq[DEPTH];
-      static_for<DEPTH - 1>([&](auto dc) {
-        constexpr int d = decltype(dc)::value;
-        bq[d] = tile_base(d);
-        issue(bq[d], kq[d], vq[d]);
-      });
+      if (!primed) {
+        static_for<DEPTH - 1>([&](auto dc) {
+          constexpr int d = decltype(dc)::value;
+          bq[d] = tile_base(d);
+          issue(bq[d], kq[d], vq[d]);
+        });
+      }
       for (int k = 0; k < nt; k += STEP) {
         static_for<STEP>([&](auto dc) {
           constexpr int d = decltype(dc)::value;
@@ -356,6 +372,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
           consume(k + d, kq[cu], vq[cu], bq[cu]);
         });
       }
+      primed = has_next;
     }
 
     if (!more_here) {
