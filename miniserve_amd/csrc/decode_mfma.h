@@ -285,6 +285,15 @@ __device__ __forceinline__ void pv_tile(float (&acc)[RT][8], const float (&pr)[4
 #endif
 }
 
+// Workgroups of the partition kernel a CU may hold (0: as registers allow). Two on a CU
+// run one after the other (the older one's loads win the memory pipe), so a third only
+// lengthens that CU's queue while other CUs idle; capping residency through LDS leaves
+// the later workgroups to the dispatcher, which starts them on whichever CU frees first.
+#ifndef MSATTN_MFMA_WG_PER_CU
+#define MSATTN_MFMA_WG_PER_CU 2
+#endif
+constexpr int kMfmaWgPerCu = MSATTN_MFMA_WG_PER_CU;
+constexpr int kCuLdsBytes = 160 * 1024;  // gfx950 LDS per CU
 constexpr int kMfmaWaves = MSATTN_MFMA_WAVES;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
 constexpr int kMaxTilesPerWave = kPartMax / 16 / kMfmaWaves;  // partitions are <= kPartMax tokens
@@ -344,6 +353,13 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
 
   __shared__ float s_red[kMfmaWaves][RT][D];
   __shared__ float s_ml[kMfmaWaves][RT][2];
+  // LDS reserved beyond s_red / s_ml so that at most kMfmaWgPerCu workgroups share a
+  // CU (the store below never runs; it keeps the array allocated).
+  constexpr int kLdsUsed = static_cast<int>(sizeof(s_red) + sizeof(s_ml));
+  constexpr int kLdsWant = kMfmaWgPerCu > 0 ? kCuLdsBytes / (kMfmaWgPerCu + 1) + 2048 : 0;
+  constexpr int kPadFloats = kLdsWant > kLdsUsed ? (kLdsWant - kLdsUsed) / 4 : 1;
+  __shared__ float s_pad[kPadFloats];
+  if (p.batch < 0) s_pad[threadIdx.x % kPadFloats] = 0.0f;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
