@@ -254,6 +254,31 @@ __device__ __forceinline__ float group_max(float x) {
   return x;
 }
 
+// Inclusive prefix sum over the wave (lane i receives x_0 + ... + x_i): DPP row shifts
+// (lane i reads lane i - n of its 16-lane row; lanes without a source read 0) scan each
+// row, then every row adds the totals of the rows below it.
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+#if MSATTN_ROW_SWAPS
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(x, 15);
+  const int r1 = __builtin_amdgcn_readlane(x, 31);
+  const int r2 = __builtin_amdgcn_readlane(x, 47);
+  const int row = static_cast<int>(__lane_id()) >> 4;
+  return x + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+#else
+  const int lane = static_cast<int>(__lane_id());
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  return x;
+#endif
+}
+
 // ---------------------------------------------------------------------------
 // Strided reduce-scatter: sums R x E values per lane over the lanes of equal
 // lane % Stride (Stride a power of two, 1..64), leaving each lane a 1/P share of the

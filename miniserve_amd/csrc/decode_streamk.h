@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
 
   __shared__ int s_pre[kSkMaxBatch + 1];  // exclusive prefix of T_b
   __shared__ int s_ctx[kSkMaxBatch];      // context length of b, clamped to max_ctx
-  __shared__ int s_wsum[kSkWaves];
+  __shared__ int s_wsum[2][kSkWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -88,12 +88,15 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
   const int B = p.batch;
 
   // ---- tiles per sequence and their exclusive prefix sum (block scan) ----
-  constexpr int kPer = (kSkMaxBatch + kSkThreads - 1) / kSkThreads;
-  int tb[kPer];
-  int my_sum = 0;
+  // Sequence b = k * kSkThreads + tid: one coalesced load per slice of the batch, every
+  // slice's loads issued together; each slice is scanned in registers and across the
+  // waves through LDS (two buffers, so one barrier a slice), carrying the running total.
+  constexpr int kSlices = (kSkMaxBatch + kSkThreads - 1) / kSkThreads;
+  const int nslices = (B + kSkThreads - 1) / kSkThreads;
+  int tb[kSlices];
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int b = tid * kPer + k;
+  for (int k = 0; k < kSlices; ++k) {
+    const int b = k * kSkThreads + tid;
     int t = 0;
     if (b < B) {
       int ctx = p.lens[b];
@@ -103,34 +106,28 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
       t = ctx > lo ? ceil_div(ctx, 16) - lo / 16 : 0;
     }
     tb[k] = t;
-    my_sum += t;
   }
-  int incl = my_sum;  // inclusive scan over the wave
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int y = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += y;
-  }
-  if (lane == kWave - 1) s_wsum[w] = incl;
-  __syncthreads();
-  int wave_off = 0;
   int sumT = 0;
 #pragma unroll
-  for (int i = 0; i < kSkWaves; ++i) {
-    const int v = s_wsum[i];
-    if (i < w) wave_off += v;
-    sumT += v;
-  }
-  {
-    int run = wave_off + incl - my_sum;
+  for (int k = 0; k < kSlices; ++k) {
+    if (k < nslices) {
+      const int incl = wave_inclusive_sum(tb[k]);
+      if (lane == kWave - 1) s_wsum[k & 1][w] = incl;
+      __syncthreads();
+      int off = sumT;
+      int tot = 0;
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int b = tid * kPer + k;
-      if (b < B) s_pre[b] = run;
-      run += tb[k];
+      for (int i = 0; i < kSkWaves; ++i) {
+        const int v = s_wsum[k & 1][i];
+        if (i < w) off += v;
+        tot += v;
+      }
+      const int b = k * kSkThreads + tid;
+      if (b < B) s_pre[b] = off + incl - tb[k];
+      sumT += tot;
     }
-    if (tid == 0) s_pre[B] = sumT;
   }
+  if (tid == 0) s_pre[B] = sumT;
   __syncthreads();
 
   // ---- chunking ----
