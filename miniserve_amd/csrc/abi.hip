@@ -99,16 +99,19 @@ Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, i
   L.rows = static_cast<int64_t>(batch) * q_len * num_heads;
   L.slots = L.rows * L.max_parts;
   if (q_len == 1 && batch <= kSkMaxBatch) {
+    // Either stream-K shape (2-byte or fp8 cache: the size does not depend on the dtype).
     const int RT = mfma_rows_per_tile(num_heads / num_kv_heads);
     const int units = num_kv_heads * ceil_div(num_heads / num_kv_heads, RT);
-    const int UG = largest_pow2_divisor_upto(units, kSkWaves);
-    const int64_t segments = static_cast<int64_t>(units / UG) * batch;
-    const int64_t tiles = segments * ceil_div(max_context, 16);
-    const int64_t by_grid = static_cast<int64_t>(kSkGrid) * (kSkWaves / UG);
-    const int64_t by_size = (tiles + kSkMinChunk - 1) / kSkMinChunk;
-    const int64_t chunks = by_grid < by_size ? by_grid : by_size;
-    const int64_t sk = streamk_pieces(chunks, segments) * UG * RT;
-    if (sk > L.slots) L.slots = sk;
+    for (const int waves : {sk_waves(2), sk_waves(1)}) {
+      const int UG = largest_pow2_divisor_upto(units, waves);
+      const int64_t segments = static_cast<int64_t>(units / UG) * batch;
+      const int64_t tiles = segments * ceil_div(max_context, 16);
+      const int64_t by_grid = static_cast<int64_t>(kSkGrid) * (waves / UG);
+      const int64_t by_size = (tiles + kSkMinChunk - 1) / kSkMinChunk;
+      const int64_t chunks = by_grid < by_size ? by_grid : by_size;
+      const int64_t sk = streamk_pieces(chunks, segments) * UG * RT;
+      if (sk > L.slots) L.slots = sk;
+    }
   }
   L.hdr_bytes = round256(sizeof(int) * (kHdrPrefix + static_cast<size_t>(batch) + 1));
   L.ml_bytes = round256(static_cast<size_t>(L.slots) * 2 * sizeof(float));
@@ -316,14 +319,14 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   hipError_t e = hipSuccess;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   // Decode with enough work to fill the chip: stream-K over every (sequence,
-  // KV head) tile run, one 8-wave workgroup per CU. Small decodes keep the
-  // partition kernel, whose short runs start faster.
+  // KV head) tile run, one workgroup per CU. Small decodes keep the partition
+  // kernel, whose short runs start faster.
   const int64_t tile_capacity =
       static_cast<int64_t>(batch) * num_kv_heads * ceil_div(max_context, 16);
   if (use_mfma && q_len == 1 && batch <= kSkMaxBatch && tile_capacity >= kStreamKMinTiles) {
     *kind = 1;
     const int units = num_kv_heads * p.rtiles;
-    p.sk_group = largest_pow2_divisor_upto(units, kSkWaves);
+    p.sk_group = largest_pow2_divisor_upto(units, sk_waves(kv_fp8 ? 1 : 2));
     p.sk_unit_groups = units / p.sk_group;
     const int grid = device_cus() < 256 ? kSkGrid * device_cus() / 256 : kSkGrid;
     if (q_dtype == MSATTN_BF16)

@@ -5,7 +5,7 @@
 // by side); the work of a unit group over sequence b is its T_b 16-token tiles
 // (the tiles of b's key range). Listing every unit group's sequences in order
 // gives `total` slabs. The grid is fixed by the device (one workgroup of
-// kSkWaves waves per CU); the slab list is cut into equal contiguous chunks of
+// kSkWaves waves per CU: 4 for a 2-byte cache, 8 for fp8); the slab list is cut into equal contiguous chunks of
 // c slabs, one per wave sub-group (kSkWaves / UG sub-groups per workgroup),
 // and each of the UG waves of a sub-group walks that chunk for its own KV head.
 // So every wave streams the same amount of KV (no ragged tails), pays its
@@ -36,11 +36,19 @@ namespace msattn {
 // win every issue slot of a saturated memory pipe, so the younger one streams only after
 // the older has finished its chunk; the page's other heads are then read late, and the
 // kernel's end is set by the starved half.
+// An fp8 cache spends about twice the VALU work per byte (widening), so there a second
+// wave per SIMD pays: its conversions fill the first wave's waits (C3 4 %, C4 2 % faster
+// than one wave per SIMD; the same on a 2-byte cache is 2 % slower).
 #ifndef MSATTN_SK_WAVES
 #define MSATTN_SK_WAVES 4
 #endif
-constexpr int kSkWaves = MSATTN_SK_WAVES;
-constexpr int kSkThreads = kSkWaves * kWave;
+#ifndef MSATTN_SK_WAVES_FP8
+#define MSATTN_SK_WAVES_FP8 8
+#endif
+// Waves per workgroup for a cache of kv_bytes-byte elements.
+__host__ __device__ constexpr int sk_waves(int kv_bytes) {
+  return kv_bytes == 1 ? MSATTN_SK_WAVES_FP8 : MSATTN_SK_WAVES;
+}
 constexpr int kSkMaxBatch = 4096;   // sequences per launch on this path
 constexpr int kSkTableRun = 64;     // tile page ids fetched per table load
 // Tiles whose loads are in flight per wave (ring depth) for 2-byte and for fp8
@@ -61,7 +69,10 @@ __host__ __device__ constexpr int64_t streamk_pieces(int64_t n_chunks, int64_t n
 }
 
 template <typename T, typename KT, int D, int RT>
-__global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitParams p) {
+__global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_kernel(
+    const SplitParams p) {
+  constexpr int kSkWaves = sk_waves(sizeof(KT));
+  constexpr int kSkThreads = kSkWaves * kWave;
   typedef Kv8<T, KT> KV;
   typedef typename KV::raw_t raw_t;
   constexpr int DEPTH = sizeof(KT) == 1 ? MSATTN_SK_DEPTH_FP8 : MSATTN_SK_DEPTH;
@@ -413,7 +424,7 @@ __global__ __launch_bounds__(kSkThreads) void decode_streamk_kernel(const SplitP
 template <typename T, typename KT, int D, int RT>
 hipError_t launch_decode_streamk_one(const SplitParams& p, int grid, hipStream_t stream) {
   hipLaunchKernelGGL((decode_streamk_kernel<T, KT, D, RT>), dim3(static_cast<unsigned>(grid)),
-                     dim3(kSkThreads), 0, stream, p);
+                     dim3(sk_waves(sizeof(KT)) * kWave), 0, stream, p);
   return hipGetLastError();
 }
 

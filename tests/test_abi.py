@@ -46,7 +46,8 @@ def test_partition_policy(B, q_len, H, KVH, D, ctx, part):
     assert lib.msattn_partition_tokens(B, q_len, H, KVH, D, ctx) == part
     # header: 64 ints + B + 1 prefix sums; slots: rows x (partitions + end marker),
     # or stream-K pieces x UG x RT if larger: pieces = chunks + NUG x B, chunks at
-    # most 256 workgroups x 4 / UG waves and at most tiles / 4
+    # most 256 workgroups x waves / UG and at most tiles / 4, for the larger of the
+    # two stream-K shapes (4 waves for a 2-byte cache, 8 for fp8)
     r256 = lambda x: -(-x // 256) * 256
     rows = B * q_len * H
     slots = rows * (-(-ctx // part) + 1)
@@ -54,10 +55,11 @@ def test_partition_policy(B, q_len, H, KVH, D, ctx, part):
         G = H // KVH
         RT = 16 if G >= 16 else 1 << (G - 1).bit_length()
         units = KVH * -(-G // RT)
-        UG = max(u for u in (1, 2, 4) if units % u == 0)
-        segments = units // UG * B
-        chunks = min(256 * 4 // UG, -(-(segments * -(-ctx // 16)) // 4))
-        slots = max(slots, (chunks + segments) * UG * RT)
+        for waves in (4, 8):
+            UG = max(u for u in (1, 2, 4, 8) if u <= waves and units % u == 0)
+            segments = units // UG * B
+            chunks = min(256 * waves // UG, -(-(segments * -(-ctx // 16)) // 4))
+            slots = max(slots, (chunks + segments) * UG * RT)
     expect = r256(4 * (64 + B + 1)) + r256(slots * 2 * 4) + slots * D * 4
     assert lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) == expect
 

@@ -196,9 +196,12 @@ def test_triton_flash_backend_and_rope(device):
     (28, 4, 128, torch.float16, True, None),     # stream-K kernel, fp16 query
 ])
 def test_fp8_kv_mfma_equals_dequantized(device, H, KVH, D, dtype, wide, window):
-    """An fp8 (e4m3fn) cache on the MFMA kernels, widened in registers, gives exactly
-    the result of the same kernels on the cache converted to the query type first
-    (miniserve/attention.py:168-170 then .to(q.dtype)); and the float64 oracle."""
+    """An fp8 (e4m3fn) cache on the MFMA kernels, widened in registers, gives the result of
+    the same kernels on the cache converted to the query type first
+    (miniserve/attention.py:168-170 then .to(q.dtype)); and the float64 oracle. On the
+    partition kernel both runs split the work alike, so they agree bit for bit. The
+    stream-K kernel runs an fp8 cache with 8 waves per CU and a 2-byte cache with 4, so its
+    chunks differ and the two agree to summation order (two output ulps)."""
     note(f"fp8 MFMA H={H} KVH={KVH} D={D} {dtype} wide={wide} window={window}")
     lens = [0, 1, 17, 300, 1234, 77, 4096, 999]
     width = 65536 // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
@@ -211,7 +214,10 @@ def test_fp8_kv_mfma_equals_dequantized(device, H, KVH, D, dtype, wide, window):
                           max_context=cap)
     want = paged_attention(qd, kd.to(device), vd.to(device), table, lens, window=window,
                            max_context=cap)
-    assert torch.equal(got, want)
+    if wide:
+        assert rel_err(got, want.double().cpu().numpy()) < 2.0 ** -7
+    else:
+        assert torch.equal(got, want)
     ref = dense.paged_attention_f64(q, kc8, vc8, table, lens, window=window)
     assert rel_err(got, ref) < BF16_REL
     assert not got[0].any()
