@@ -85,8 +85,8 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
  * sizes the launch grid; pass table_width * block_size for a capture-safe call.
  * window <= 0 means no sliding window. Runs msattn_paged_attention_partials
  * followed by msattn_merge_partials, except for chunked prefill on the MFMA kernel
- * (bf16/fp16 query, cache of its type or fp8 e4m3, head_dim 128, more than 16 query
- * rows per KV head), which writes the output directly.
+ * (bf16/fp16 query, cache of its type or fp8 e4m3, head_dim 64 or 128, more than 16
+ * query rows per KV head), which writes the output directly.
  */
 int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
                            int64_t cache_block_stride, int64_t cache_slot_stride,
@@ -169,7 +169,7 @@ size_t msattn_prefix_workspace_bytes(int batch, int num_heads, int num_kv_heads,
  * a second pass reads each sequence's own keys from prefix_pages * block_size on;
  * the merge folds both. A row whose context ends inside the prefix sees only its
  * own length. Types or head sizes without the cascade kernels (anything but a bf16 or
- * fp16 query over a cache of its type or of fp8 e4m3, head_dim 128, block_size a
+ * fp16 query over a cache of its type or of fp8 e4m3, head_dim 64 or 128, block_size a
  * multiple of 16), and
  * prefix_pages == 0, run msattn_paged_attention. The reference has no cascade
  * kernel: its decode re-reads the shared pages per sequence
