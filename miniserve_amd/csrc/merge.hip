@@ -26,6 +26,12 @@ constexpr int kMergeMaxDims = 4;  // dims per lane: head_dim <= 256
 #define MSATTN_MERGE_BATCH 8
 #endif
 constexpr int kMergeBatch = MSATTN_MERGE_BATCH;  // acc rows loaded together
+// The same for a cascade decode's shared-prefix partials, which fill every slot (32 per
+// row on C4): one round of loads where the decode source's batch would take four.
+#ifndef MSATTN_MERGE_PREFIX_BATCH
+#define MSATTN_MERGE_PREFIX_BATCH 32
+#endif
+constexpr int kMergePrefixBatch = MSATTN_MERGE_PREFIX_BATCH;
 
 template <typename QT>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams p) {
@@ -86,8 +92,9 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
   // max and weights, then folds the acc rows kMergeBatch at a time with all of a batch's
   // loads in flight together. The first batch's acc rows do not depend on (m, l) and are
   // loaded together with them.
-  auto fold_source = [&](const float* src_ml, const float* src_acc, int64_t base,
+  auto fold_source = [&](auto batch_c, const float* src_ml, const float* src_acc, int64_t base,
                          int64_t stride, int64_t n, bool markers) {
+    constexpr int kMergeBatch = decltype(batch_c)::value;
     for (int64_t j0 = 0; j0 < n; j0 += kWave) {
       const int64_t j = j0 + lane;
       const int cmax = static_cast<int>(n - j0 < kWave ? n - j0 : kWave);
@@ -152,8 +159,10 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
       if (end) break;
     }
   };
-  fold_source(p.ml, p.acc, base, stride, n, markers);
-  if (p.npp > 0) fold_source(p.pml, p.pacc, row * p.npp, 1, p.npp, false);
+  fold_source(std::integral_constant<int, kMergeBatch>{}, p.ml, p.acc, base, stride, n, markers);
+  if (p.npp > 0)
+    fold_source(std::integral_constant<int, kMergePrefixBatch>{}, p.pml, p.pacc, row * p.npp, 1,
+                p.npp, false);
 
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   QT* out = static_cast<QT*>(p.out) + row * D;
