@@ -149,9 +149,22 @@ typedef float mf_f32x2 __attribute__((ext_vector_type(2)));
 template <typename T, typename KT> struct Kv8;
 template <typename T> struct Kv8<T, T> {
   typedef uint4 raw_t;
+  // MFMA k-chunk j (8 dims) of lane group g of the scores' K and Q operands starts at
+  // dim 8 (4j + g).
+  __host__ __device__ static constexpr int qk_dim0(int j, int g, int /*JD*/) {
+    return 8 * (4 * j + g);
+  }
   template <int AUX>
   __device__ static raw_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return buffer_load16<AUX>(r, off);
+  }
+  // A K row's chunks for lane group g (row_off: the row's byte offset in the tile).
+  template <int AUX, int JD>
+  __device__ static void load_k(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int g,
+                                raw_t (&kb)[JD]) {
+#pragma unroll
+    for (int j = 0; j < JD; ++j)
+      kb[j] = buffer_load16<AUX>(r, row_off + static_cast<uint32_t>(qk_dim0(j, g, JD)) * 2u);
   }
   __device__ static uint4 operand(const raw_t& x) { return x; }         // 8 x T, packed
   // Dim e of two tokens' chunks as one packed T pair (token a low): o[e] = (a[e], b[e]).
@@ -171,11 +184,31 @@ template <typename T> struct Kv8<T, T> {
 };
 template <typename T> struct Kv8<T, fp8_t> {
   typedef uint2 raw_t;
+  // K/Q chunk j of lane group g starts at dim 8 (JD g + j): a lane's JD chunks are 8 JD
+  // contiguous bytes of an fp8 K row, loaded 16 at a time. (The chunks of 8 (4j + g) would
+  // take JD 8-byte loads that each touch 16 rows for 32 bytes; the memory pipe's request
+  // count, not the bytes, then bounds the kernel.) The dot product does not depend on
+  // which dims share an MFMA, as long as Q and K use the same split.
+  __host__ __device__ static constexpr int qk_dim0(int j, int g, int JD) {
+    return 8 * (JD * g + j);
+  }
   template <int AUX>
   __device__ static raw_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, AUX);
     return make_uint2(v.x, v.y);
+  }
+  template <int AUX, int JD>
+  __device__ static void load_k(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int g,
+                                raw_t (&kb)[JD]) {
+    static_assert(JD % 2 == 0, "pairs of chunks per 16-byte load");
+#pragma unroll
+    for (int h = 0; h < JD / 2; ++h) {
+      const uint4 x = buffer_load16<AUX>(
+          r, row_off + static_cast<uint32_t>(qk_dim0(2 * h, g, JD)));
+      kb[2 * h] = make_uint2(x.x, x.y);
+      kb[2 * h + 1] = make_uint2(x.z, x.w);
+    }
   }
   // bytes 0..7 -> fp32 pairs (v_cvt_pk_f32_fp8, OCP e4m3 on gfx950)
   __device__ static void unpack(const raw_t& x, float* o) {
@@ -308,21 +341,40 @@ __host__ __device__ constexpr int tile_token(int i) {
   return TPI * (r / APR) + g * APR + (r % APR);
 }
 
-// Rotate-half RoPE on one query row held as MFMA B-operand chunks: chunk j holds
-// dims (4j + g) * 8 .. +7, and its partner (dims -/+ D/2) is chunk j +/- JD/2 of the
-// same lane. The rotated row is rounded back to T, as the unfused
+// Rotate-half RoPE on one query row held as MFMA B-operand chunks: chunk j of lane
+// group g holds dims Kv8<T, KT>::qk_dim0(j, g) .. +7, and its partner (dims -/+ D/2) is
+// chunk j +/- JD/2 of the same lane (2-byte caches: dims 8 (4j + g)), or, for an fp8
+// cache (dims 8 (JD g + j)), chunk j of lane group g +/- 2, the lane 32 away, which one
+// v_permlane32_swap brings over. The rotated row is rounded back to T, as the unfused
 // (q * cos + rotate_half(q) * sin).to(T) of miniserve/attention.py:41-62 /
-// kernels/paged_attn_triton.py:211-220 would be.
-template <typename T, int D>
+// kernels/paged_attn_triton.py:211-220 would be. Lanes l and l ^ 32 (the same query row)
+// are both active or both not.
+template <typename T, typename KT, int D>
 __device__ __forceinline__ void rope_chunks(uint4 (&qb)[D / 32], const float* cs, const float* sn,
                                             int g) {
   constexpr int JD = D / 32;
+  constexpr bool kCross = sizeof(KT) == 1;  // the partner chunk sits in the other half-wave
   float q[JD][8];
+  float qp[JD][8];
 #pragma unroll
   for (int j = 0; j < JD; ++j) Chunk<T>::unpack(qb[j], q[j]);
+  if constexpr (kCross) {
+    const bool lo = g < 2;
+#pragma unroll
+    for (int j = 0; j < JD; ++j) {
+      const uint32_t w[4] = {qb[j].x, qb[j].y, qb[j].z, qb[j].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const auto t = __builtin_amdgcn_permlane32_swap(w[k], w[k], false, false);
+        o[k] = lo ? t[1] : t[0];
+      }
+      Chunk<T>::unpack(make_uint4(o[0], o[1], o[2], o[3]), qp[j]);
+    }
+  }
 #pragma unroll
   for (int j = 0; j < JD; ++j) {
-    const int d0 = (4 * j + g) * 8;
+    const int d0 = Kv8<T, KT>::qk_dim0(j, g, JD);
     const float4 c0 = *reinterpret_cast<const float4*>(cs + d0);
     const float4 c1 = *reinterpret_cast<const float4*>(cs + d0 + 4);
     const float4 s0 = *reinterpret_cast<const float4*>(sn + d0);
@@ -332,7 +384,11 @@ __device__ __forceinline__ void rope_chunks(uint4 (&qb)[D / 32], const float* cs
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float r = j < JD / 2 ? -q[j + JD / 2][e] : q[j - JD / 2][e];
+      float r;
+      if constexpr (kCross)
+        r = g < 2 ? -qp[j][e] : qp[j][e];
+      else
+        r = j < JD / 2 ? -q[j + JD / 2][e] : q[j - JD / 2][e];
       o[e] = rope_mix(q[j][e], r, c[e], sv[e]);
     }
     qb[j] = Chunk<T>::pack(o);
@@ -457,18 +513,17 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
 #pragma unroll
     for (int j = 0; j < JD; ++j) {
       qb[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (n < nrows) qb[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + (4 * j + g) * 8);
+      if (n < nrows) qb[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + KV::qk_dim0(j, g, JD));
     }
     if (p.rope_cos != nullptr && n < nrows) {
       const int64_t po = static_cast<int64_t>(rope_position(p, b)) * D;
-      rope_chunks<T, D>(qb, p.rope_cos + po, p.rope_sin + po, g);
+      rope_chunks<T, KT, D>(qb, p.rope_cos + po, p.rope_sin + po, g);
     }
   }
 
   // Per-lane byte offsets inside a tile (32-bit: a tile spans 16 slots).
   constexpr int EB = static_cast<int>(sizeof(KT));
-  const uint32_t k_lane_off =
-      static_cast<uint32_t>((tile_token<D>(n) * p.slot_stride + g * 8) * EB);  // + 32*EB*j
+  const uint32_t k_row_off = static_cast<uint32_t>(tile_token<D>(n) * p.slot_stride * EB);
   uint32_t v_lane_off[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
@@ -498,8 +553,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     const int64_t b0 = ok ? base : 0;
     const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
     const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
-#pragma unroll
-    for (int j = 0; j < JD; ++j) kb[j] = KV::template load<0>(rk, k_lane_off + 32 * EB * j);
+    KV::template load_k<0, JD>(rk, k_row_off, g, kb);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) vb[j] = KV::template load<0>(rv, v_lane_off[j]);
   };

@@ -224,18 +224,19 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
     }
     return mb;
   };
-  // The piece's query rows as the MFMA B operand (lane (g, n): row n, dims 8 (4j + g) ..).
+  // The piece's query rows as the MFMA B operand (lane (g, n): row n, chunk j at dim
+  // KV::qk_dim0(j, g), the split the K loads use).
   auto load_q = [&](const Piece& pc, uint4 (&q)[JD]) {
     const T* qp = static_cast<const T*>(p.q);
     const int64_t orow_n = static_cast<int64_t>(pc.b) * p.H + pc.kvh * p.G + pc.row0 + n;
 #pragma unroll
     for (int j = 0; j < JD; ++j) {
       q[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (n < pc.nrows) q[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + (4 * j + g) * 8);
+      if (n < pc.nrows) q[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + KV::qk_dim0(j, g, JD));
     }
     if (p.rope_cos != nullptr && n < pc.nrows) {
       const int64_t po = static_cast<int64_t>(rope_position(p, pc.b)) * D;
-      rope_chunks<T, D>(q, p.rope_cos + po, p.rope_sin + po, g);
+      rope_chunks<T, KT, D>(q, p.rope_cos + po, p.rope_sin + po, g);
     }
   };
 
@@ -299,10 +300,8 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
       const int64_t b0 = ok ? base : 0;
       const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
       const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
-      const uint32_t koff = (k_lane_tok * static_cast<uint32_t>(p.slot_stride) + g * 8) * EB;
-#pragma unroll
-      for (int j = 0; j < JD; ++j)
-        kb[j] = KV::template load<MSATTN_LOAD_AUX>(rk, koff + 32 * EB * j);
+      KV::template load_k<MSATTN_LOAD_AUX, JD>(
+          rk, k_lane_tok * static_cast<uint32_t>(p.slot_stride) * EB, g, kb);
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
         vb[j] = KV::template load<MSATTN_LOAD_AUX>(
