@@ -184,13 +184,14 @@ template <typename T> struct Kv8<T, T> {
 };
 template <typename T> struct Kv8<T, fp8_t> {
   typedef uint2 raw_t;
-  // K/Q chunk j of lane group g starts at dim 8 (JD g + j): a lane's JD chunks are 8 JD
-  // contiguous bytes of an fp8 K row, loaded 16 at a time. (The chunks of 8 (4j + g) would
-  // take JD 8-byte loads that each touch 16 rows for 32 bytes; the memory pipe's request
-  // count, not the bytes, then bounds the kernel.) The dot product does not depend on
-  // which dims share an MFMA, as long as Q and K use the same split.
-  __host__ __device__ static constexpr int qk_dim0(int j, int g, int JD) {
-    return 8 * (JD * g + j);
+  // K/Q chunks 2h and 2h + 1 of lane group g are dims 64 h + 16 g .. + 15: one 16-byte
+  // load per lane, and the four lane groups of a row cover its bytes 64 h .. 64 h + 63.
+  // (The chunks of 8 (4j + g) would take JD 8-byte loads that each touch 16 rows for 32
+  // bytes; the memory pipe's request count, not the bytes, then bounds the kernel.) The
+  // dot product does not depend on which dims share an MFMA, as long as Q and K use the
+  // same split.
+  __host__ __device__ static constexpr int qk_dim0(int j, int g, int /*JD*/) {
+    return 64 * (j >> 1) + 16 * g + 8 * (j & 1);
   }
   template <int AUX>
   __device__ static raw_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -343,8 +344,9 @@ __host__ __device__ constexpr int tile_token(int i) {
 
 // Rotate-half RoPE on one query row held as MFMA B-operand chunks: chunk j of lane
 // group g holds dims Kv8<T, KT>::qk_dim0(j, g) .. +7, and its partner (dims -/+ D/2) is
-// chunk j +/- JD/2 of the same lane (2-byte caches: dims 8 (4j + g)), or, for an fp8
-// cache (dims 8 (JD g + j)), chunk j of lane group g +/- 2, the lane 32 away, which one
+// chunk j +/- JD/2 of the same lane (2-byte caches: dims 8 (4j + g); an fp8 cache at
+// D = 128: dims 64 (j / 2) + 16 g + 8 (j % 2)), or, for an fp8 cache at D = 64 (dims
+// 16 g + 8 j), chunk j of lane group g +/- 2, the lane 32 away, which one
 // v_permlane32_swap brings over. The rotated row is rounded back to T, as the unfused
 // (q * cos + rotate_half(q) * sin).to(T) of miniserve/attention.py:41-62 /
 // kernels/paged_attn_triton.py:211-220 would be. Lanes l and l ^ 32 (the same query row)
@@ -353,7 +355,7 @@ template <typename T, typename KT, int D>
 __device__ __forceinline__ void rope_chunks(uint4 (&qb)[D / 32], const float* cs, const float* sn,
                                             int g) {
   constexpr int JD = D / 32;
-  constexpr bool kCross = sizeof(KT) == 1;  // the partner chunk sits in the other half-wave
+  constexpr bool kCross = sizeof(KT) == 1 && D == 64;  // the partner is in the other half-wave
   float q[JD][8];
   float qp[JD][8];
 #pragma unroll

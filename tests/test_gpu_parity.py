@@ -233,7 +233,10 @@ def test_fp8_kv_prefill_equals_dequantized(device, H, KVH, D, q_len, dtype, caus
                                            prefix):
     """The MFMA prefill kernel (and the cascade's shared-prefix pass, which runs on it) over
     an fp8 cache widens the chunks exactly as it stages them: bit-exact against the same
-    kernel on the cache converted to the query type, and within tolerance of the oracle."""
+    kernel on the cache converted to the query type, and within tolerance of the oracle.
+    A cascade decode's suffix pass runs on the decode kernels, whose fp8 split of the head
+    dims over the score MFMAs differs from the 2-byte one: there the whole result agrees to
+    summation order (two output ulps)."""
     note(f"fp8 prefill H={H} KVH={KVH} D={D} q_len={q_len} {dtype} causal={causal} "
          f"window={window} prefix={prefix}")
     bs = 16
@@ -252,7 +255,10 @@ def test_fp8_kv_prefill_equals_dequantized(device, H, KVH, D, q_len, dtype, caus
     qd = q.to(device)
     got = paged_attention(qd, kc8.to(device), vc8.to(device), table, lens, **kw)
     want = paged_attention(qd, kd.to(device), vd.to(device), table, lens, **kw)
-    assert torch.equal(got, want)
+    if prefix:
+        assert rel_err(got, want.double().cpu().numpy()) < 2.0 ** -7
+    else:
+        assert torch.equal(got, want)
     ref = dense.paged_attention_f64(q, kc8, vc8, table, lens, causal=causal, window=window)
     assert rel_err(got, ref) < BF16_REL
 
