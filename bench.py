@@ -1,6 +1,7 @@
 """Paged-decode benchmark on one MI355X (gfx950).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+                    [--kv-fp8] [--no-cascade] [--prefill] [--graph-steps G]
 
 A step is one layer's paged-attention decode over the whole batch (split-K
 partials kernel + merge kernel), replayed from a captured hipGraph with the
@@ -47,6 +48,9 @@ def parse():
     ap.add_argument("--graph-steps", type=int, default=0,
                     help="steps captured per graph (0: largest divisor of --steps up to 10)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kv-fp8", action="store_true",
+                    help="decode over the same caches stored as fp8 e4m3 (half the KV bytes; "
+                         "the query and the arithmetic stay bf16)")
     ap.add_argument("--no-cascade", action="store_true",
                     help="decode a shared-prefix workload (config 4) in one pass per sequence "
                          "instead of the cascade entry point")
@@ -129,6 +133,9 @@ def main():
           f"D={w.head_dim} layers={w.layers} pool={w.num_blocks} pages, "
           f"ctx {min(w.lens)}..{max(w.lens)} (sum {sum(w.lens)}) in {time.time() - t0:.1f}s",
           file=sys.stderr, flush=True)
+    if args.kv_fp8:  # the same values rounded to e4m3; algorithmic bytes follow the dtype
+        w.k_caches = [c.to(torch.float8_e4m3fn) for c in w.k_caches]
+        w.v_caches = [c.to(torch.float8_e4m3fn) for c in w.v_caches]
 
     B, H, KVH, D, bs = w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
     table = w.table.to(device=dev, dtype=torch.int32).contiguous()
@@ -145,7 +152,7 @@ def main():
     part_tokens = lib.msattn_partition_tokens(B, 1, H, KVH, D, max_ctx)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     outs = [torch.empty_like(q) for _ in range(w.layers)]
-    qcode, kvcode = nat.dtype_code(w.dtype), nat.dtype_code(w.dtype)
+    qcode, kvcode = nat.dtype_code(w.dtype), nat.dtype_code(w.k_caches[0].dtype)
 
     def step():
         for layer in range(w.layers):
@@ -230,7 +237,7 @@ def main():
     achieved = per_layer_bytes / (split_avg * 1e-3) / 1e9
 
     traffic = None
-    tfile = PROFILES / f"traffic_{w.name}.json"
+    tfile = PROFILES / f"traffic_{w.name}{'-fp8' if args.kv_fp8 else ''}.json"
     if tfile.exists():
         try:
             traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
@@ -260,6 +267,7 @@ def main():
             "pool_pages": w.num_blocks, "partition_tokens": part_tokens,
             "algorithmic_bytes_per_layer": per_layer_bytes,
             "shared_prefix_pages": w.shared_prefix_pages, "cascade": bool(cascade),
+            "kv_dtype": "fp8_e4m3" if args.kv_fp8 else str(w.dtype).replace("torch.", ""),
             "steps_per_graph": gsteps, "us_per_step_one_per_graph": round(ms_single * 1e3, 2),
         },
         "roofline": {
@@ -276,7 +284,7 @@ def main():
         },
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not args.kv_fp8:  # the baseline is the bf16 cache's
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
