@@ -60,8 +60,8 @@ int largest_pow2_divisor_upto(int x, int cap) {
   return u;
 }
 
-// Stream-K grid: one 8-wave workgroup per CU (MI355X has 256 CUs); devices with
-// fewer CUs launch fewer.
+// Stream-K grid: one workgroup per CU (MI355X has 256 CUs; 4 waves for a 2-byte cache,
+// 8 for fp8); devices with fewer CUs launch proportionally fewer.
 #ifndef MSATTN_SK_GRID
 #define MSATTN_SK_GRID 256
 #endif

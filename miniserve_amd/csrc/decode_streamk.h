@@ -4,10 +4,11 @@
 // rows that read one KV head. Units are grouped UG at a time (UG KV heads side
 // by side); the work of a unit group over sequence b is its T_b 16-token tiles
 // (the tiles of b's key range). Listing every unit group's sequences in order
-// gives `total` slabs. The grid is fixed by the device (one workgroup of
-// kSkWaves waves per CU: 4 for a 2-byte cache, 8 for fp8); the slab list is cut into equal contiguous chunks of
-// c slabs, one per wave sub-group (kSkWaves / UG sub-groups per workgroup),
-// and each of the UG waves of a sub-group walks that chunk for its own KV head.
+// gives `total` slabs. The grid is fixed by the device (one workgroup of kSkWaves
+// waves per CU: 4 for a 2-byte cache, 8 for fp8); the slab list is cut into equal
+// contiguous chunks of c slabs, one per wave sub-group (kSkWaves / UG sub-groups per
+// workgroup), and each of the UG waves of a sub-group walks that chunk for its own KV
+// head.
 // So every wave streams the same amount of KV (no ragged tails), pays its
 // set-up once per run of tiles, and the UG heads of a page are read together.
 //
@@ -22,8 +23,8 @@
 // v_dot2 with DPP row broadcasts, a ring of per-tile buffer descriptors keeping the
 // next tiles' loads in flight. A wave walks its chunk in runs of up to kSkTableRun
 // tiles and requests the next run's page ids (and, at a sequence boundary, the next
-// piece's query rows) before it streams the current one. The algorithm is the split
-// decomposition of
+// piece's query rows) before it streams the current one; the tile ring runs on across
+// runs and pieces. The algorithm is the split decomposition of
 // kernels/paged_attn_triton.py:102-171 with the masking of
 // miniserve/attention.py:135-153 (for q_len == 1: keys in [ctx - window, ctx)).
 #pragma once
