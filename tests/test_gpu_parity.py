@@ -506,6 +506,32 @@ def test_streamk_decode(device, H, KVH, D, dtype, window):
         assert torch.equal(out[1, 0, h].cpu(), vc[table[1, 0], 0, h // (H // KVH)])
 
 
+@pytest.mark.parametrize("batch,max_ctx,width", [
+    (257, 300, 128),    # two slices of the in-kernel context-length scan
+    (700, 300, 48),     # three slices
+    (4096, 128, 8),     # the path's largest batch: sixteen slices
+])
+def test_streamk_large_batch(device, batch, max_ctx, width):
+    """Stream-K decode over batches past one 256-sequence slice of its context-length scan
+    (tables wide enough for the stream-K route: batch x KV heads x width >= 65536 tiles),
+    against the float64 oracle; empty and one-token contexts included."""
+    H, KVH, D = 14, 2, 64
+    g = torch.Generator().manual_seed(batch)
+    lens = [int(x) for x in torch.randint(0, max_ctx + 1, (batch,), generator=g)]
+    lens[0], lens[1] = 0, 1
+    note(f"stream-K large batch B={batch} ctx<={max_ctx} width={width}")
+    assert batch * KVH * width >= 65536
+    q, kc, vc, table = wide_table_case(H, KVH, D, lens, torch.bfloat16, width, seed=batch + 1)
+    out = run_hip(device, q, kc, vc, table, lens, max_context=width * 16)
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens)
+    err = rel_err(out, ref)
+    note(f"stream-K large batch max-rel {err:.3e}")
+    assert err < BF16_REL
+    assert not out[0].any()
+    for h in range(H):
+        assert torch.equal(out[1, 0, h].cpu(), vc[table[1, 0], 0, h // (H // KVH)])
+
+
 def test_streamk_graph_replays(device):
     """Stream-K decode captured in a graph: replays with new lengths match eager bit-exactly."""
     note("stream-K graph")
