@@ -80,7 +80,10 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
  * Replaces PagedAttention.forward (miniserve/attention.py:205-250: gather
  * :155-171, mask :135-153, GQA expansion :245-247, SDPA :249) and the split-K
  * launcher flash_decode (kernels/paged_attn_triton.py:286-344).
- * cache_*_stride are in elements and shared by k_cache and v_cache.
+ * cache_*_stride are in elements and shared by k_cache and v_cache. The MFMA
+ * kernels address a 16-token tile with 32-bit byte offsets; caches whose tile span
+ * (15 * cache_slot_stride + head_dim elements) reaches 2^31 bytes take the generic
+ * kernel, which addresses with 64-bit offsets.
  * max_context bounds context_lens (entries above it are clamped to it) and
  * sizes the launch grid; pass table_width * block_size for a capture-safe call.
  * window <= 0 means no sliding window. Runs msattn_paged_attention_partials

@@ -160,6 +160,16 @@ PrefixLayout prefix_layout(int batch, int num_heads, int num_kv_heads, int head_
   return X;
 }
 
+// The MFMA kernels (decode partition, stream-K, prefill) read a 16-token tile through a
+// buffer descriptor with 32-bit byte offsets from the tile's first row: the tile's span
+// (15 slot strides plus one row) must stay below 2^31 bytes. Caches laid out with a
+// larger slot stride (a permuted view of a large pool) take the generic kernel, which
+// addresses with 64-bit offsets.
+bool tile_span_ok(int64_t slot_stride, int head_dim, int kv_dtype) {
+  if (slot_stride >= (int64_t(1) << 31)) return false;
+  return (15 * slot_stride + head_dim) * dtype_bytes(kv_dtype) < (int64_t(1) << 31);
+}
+
 int hip_status(hipError_t e) { return e == hipSuccess ? MSATTN_OK : MSATTN_ERR_HIP; }
 
 // Compute units of the current device (cached per device).
@@ -273,7 +283,8 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
   const bool use_mfma = (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
                         (kv_dtype == q_dtype || kv_fp8) && (head_dim == 64 || head_dim == 128) &&
-                        block_size % 16 == 0;
+                        block_size % 16 == 0 &&
+                        tile_span_ok(cache_slot_stride, head_dim, kv_dtype);
   const int RT = use_mfma ? mfma_rows_per_tile(rows) : rows_per_tile(rows);
   char* ws = static_cast<char*>(workspace);
   SplitParams p;
@@ -439,6 +450,7 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
   if (q_len > 1 && (kv_dtype == q_dtype || kv_dtype == MSATTN_FP8_E4M3) &&
       (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
       (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 && batch <= 65535 &&
+      tile_span_ok(cache_slot_stride, head_dim, kv_dtype) &&
       num_heads > 0 &&
       num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
       static_cast<int64_t>(q_len) * (num_heads / num_kv_heads) > 16) {
@@ -571,7 +583,8 @@ int msattn_paged_attention_prefix(const void* query, const void* k_cache, const 
   const bool cascade = X.prefix > 0 && (kv_dtype == q_dtype || kv_fp8) &&
                        (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
                        (head_dim == 64 || head_dim == 128) &&
-                       block_size % 16 == 0;
+                       block_size % 16 == 0 &&
+                       tile_span_ok(cache_slot_stride, head_dim, kv_dtype);
   if (!cascade)
     return msattn_paged_attention(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
                                   cache_head_stride, block_table, context_lens, out, workspace,

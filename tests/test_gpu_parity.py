@@ -645,6 +645,52 @@ def test_mfma_paths_other_page_sizes(device, bs):
         assert rel_err(out, ref) < BF16_REL
 
 
+def test_slot_stride_past_32_bit_tile_span(device):
+    """Caches stored [block_size, num_blocks, KVH, D] and passed as the permuted view
+    [num_blocks, block_size, KVH, D]: the slot stride is num_blocks * KVH * D elements, so a
+    16-token tile spans 15 * 70000 * 1024 * 2 B = 2.15 GB, past what a 32-bit buffer offset
+    reaches. Decode, chunked prefill and cascade decode must still match the float64 oracle
+    (within 2e-2 max-rel); the oracle sees compact copies of the same pages."""
+    H, KVH, D, bs, nb = 32, 8, 128, 16, 70_000
+    assert 15 * nb * KVH * D * 2 >= 2 ** 31
+    g = torch.Generator().manual_seed(11)
+    lens = [300, 40, 1000]
+    need = [(L + bs - 1) // bs for L in lens]
+    used = torch.randperm(nb, generator=g)[: sum(need)]
+    table = torch.zeros(len(lens), max(need), dtype=torch.long)
+    cur = 0
+    for b, n in enumerate(need):
+        table[b, :n] = used[cur:cur + n]
+        cur += n
+    kbig = torch.zeros(bs, nb, KVH, D, dtype=torch.bfloat16, device=device)
+    vbig = torch.zeros_like(kbig)
+    kc, vc = kbig.permute(1, 0, 2, 3), vbig.permute(1, 0, 2, 3)
+    assert kc.stride(1) == nb * KVH * D
+    kvals = torch.randn(len(used), bs, KVH, D, generator=g).to(torch.bfloat16)
+    vvals = torch.randn(len(used), bs, KVH, D, generator=g).to(torch.bfloat16)
+    kc[used.to(device)] = kvals.to(device)
+    vc[used.to(device)] = vvals.to(device)
+    remap = torch.zeros(nb, dtype=torch.long)
+    remap[used] = torch.arange(len(used))
+    try:
+        for q_len in (1, 24):  # 24 x 4 rows per KV head: the chunked-prefill route
+            note(f"slot stride {kc.stride(1)}: q_len={q_len} lens={lens}")
+            q = torch.randn(len(lens), q_len, H, D, generator=g).to(torch.bfloat16)
+            out = paged_attention(q.to(device), kc, vc, table, lens)
+            ref = dense.paged_attention_f64(q, kvals, vvals, remap[table], lens)
+            assert rel_err(out, ref) < BF16_REL
+        shared = table.clone()
+        shared[:, :2] = table[0, :2]  # two pages every row shares
+        note(f"slot stride {kc.stride(1)}: cascade, 2 shared pages")
+        q = torch.randn(len(lens), 1, H, D, generator=g).to(torch.bfloat16)
+        out = paged_attention(q.to(device), kc, vc, shared, lens, prefix_pages=2)
+        ref = dense.paged_attention_f64(q, kvals, vvals, remap[shared], lens)
+        assert rel_err(out, ref) < BF16_REL
+    finally:
+        del kc, vc, kbig, vbig
+        torch.cuda.empty_cache()
+
+
 # ------------------------------------------------------------------ cascade decode
 
 def shared_prefix_case(H, KVH, D, lens, dtype, bs, prefix_pages, width, seed):
