@@ -60,9 +60,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--stream-probe", action="store_true",
-                    help="instead of the decode bench, time a plain streaming kernel "
-                         "(out = in * 1 over 1 GiB fp32): the measured HBM ceiling and the "
-                         "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
+                    help="instead of the decode bench, time torch's out = in * 1 over 1 GiB "
+                         "fp32 (the reference dispatch for scaling rocprofv3 "
+                         "FETCH_SIZE/WRITE_SIZE) and the plain streaming-read kernel")
     return ap.parse_args()
 
 
@@ -89,6 +89,42 @@ def stream_probe(steps: int):
                       "value": round(gbs, 1), "unit": "GB/s", "ms_per_dispatch": round(ms, 4),
                       "bytes_read_per_dispatch": 1 << 30, "bytes_written_per_dispatch": 1 << 30,
                       "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+    rd = stream_read_gbs(dev, max(steps, 5))
+    print(json.dumps({"metric": "streaming read kernel HBM bandwidth (msattn_probe_stream_read)",
+                      "value": round(rd, 1), "unit": "GB/s", "bytes_read_per_dispatch": 2 << 30,
+                      "frac_of_hbm_peak": round(rd / HBM_PEAK_GBS, 4)}), flush=True)
+
+
+def stream_read_gbs(dev, launches: int = 20) -> float:
+    """GB/s of msattn_probe_stream_read (a plain 16-byte-load read kernel) over 2 GiB,
+    timed with HIP events on the stream it is launched on: the read rate a plain kernel
+    reaches on this device, reported beside the decode kernel's."""
+    import torch
+
+    from miniserve_amd import _native as nat
+
+    nbytes = 2 << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    sink = torch.empty((nbytes + 65535) // 65536, dtype=torch.int32, device=dev)
+    lib, stream = nat.lib(), nat.stream_handle(dev)
+
+    def launch():
+        nat.check("msattn_probe_stream_read",
+                  lib.msattn_probe_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(), stream))
+
+    for _ in range(3):
+        launch()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(launches):
+        launch()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / launches
+    del buf, sink
+    torch.cuda.empty_cache()
+    return nbytes / (ms * 1e-3) / 1e9
 
 
 def graph_steps(args) -> int:
@@ -236,6 +272,8 @@ def main():
     value_gbs = per_layer_bytes * w.layers / (ms_per_step * 1e-3) / 1e9
     achieved = per_layer_bytes / (split_avg * 1e-3) / 1e9
 
+    read_ceiling = stream_read_gbs(dev)
+
     traffic = None
     tfile = PROFILES / f"traffic_{w.name}{'-fp8' if args.kv_fp8 else ''}.json"
     if tfile.exists():
@@ -281,6 +319,8 @@ def main():
             "kernel_avg_us": round(split_avg * 1e3, 2),
             "kernel_median_us": round(split_ms[len(split_ms) // 2] * 1e3, 2),
             "merge_avg_us": round(merge_avg * 1e3, 2),
+            "stream_read_gbs": round(read_ceiling, 1),
+            "frac_of_stream_read": round(achieved / read_ceiling, 4),
         },
         "cpu_baseline": None,
     }

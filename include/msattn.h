@@ -214,6 +214,17 @@ int msattn_gather_kv(const void* cache, int64_t cache_block_stride, int64_t cach
                      int num_kv_heads, int head_dim, int block_size, int num_blocks,
                      int table_width, int kv_dtype, void* stream);
 
+/*
+ * Measurement helper, with no counterpart in the reference: one launch of a plain
+ * streaming-read kernel over `bytes` (a multiple of 16) of device memory at `buf`
+ * (16-byte aligned), each workgroup reading a contiguous 64 KiB chunk. Timing it
+ * gives the HBM read rate a plain kernel reaches on the device, beside which the
+ * decode kernels' rates are reported. `sink` is device memory of
+ * ceil(bytes / 65536) uint32 entries that the kernel may write (it keeps the loads
+ * from being dropped); its contents carry no meaning.
+ */
+int msattn_probe_stream_read(const void* buf, size_t bytes, void* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,7 @@ SIGNATURES = {
     "msattn_gather_kv": (c_int, [
         c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    "msattn_probe_stream_read": (c_int, [c_vp, c_size, c_vp, c_vp]),
 }
 
 _lib = None

@@ -175,3 +175,15 @@ def test_check_maps_status_to_exceptions():
     with pytest.raises(nat.MsattnError):
         nat.check("f", nat.ERR_HIP)
     nat.check("f", nat.OK)
+
+
+def test_stream_read_probe_rejects_bad_arguments():
+    """msattn_probe_stream_read returns before any HIP call on a bad argument: null or
+    misaligned pointers, a size that is zero or not a multiple of 16."""
+    lib = nat.lib()
+    assert lib.msattn_probe_stream_read(None, 1 << 20, 256, None) == nat.ERR_INVALID_ARG
+    assert lib.msattn_probe_stream_read(256, 1 << 20, None, None) == nat.ERR_INVALID_ARG
+    assert lib.msattn_probe_stream_read(256, 0, 256, None) == nat.ERR_INVALID_ARG
+    assert lib.msattn_probe_stream_read(256, (1 << 20) + 8, 256, None) == nat.ERR_INVALID_ARG
+    assert lib.msattn_probe_stream_read(264, 1 << 20, 256, None) == nat.ERR_INVALID_ARG
+    assert lib.msattn_probe_stream_read(256, 1 << 20, 258, None) == nat.ERR_INVALID_ARG

@@ -907,3 +907,17 @@ def test_graph_capture_replay(device):
         eager = paged_attention(static_q, kc, vc, static_table, new_lens, max_context=cap)
         torch.cuda.synchronize()
         assert torch.equal(replayed, eager), f"replay {rep}"
+
+
+def test_stream_read_probe(device):
+    """The streaming-read probe runs over a buffer that is not a whole number of its
+    64 KiB chunks, and the sink keeps its contents unless the fold hits the sentinel."""
+    from miniserve_amd import _native as nat
+    nbytes = (3 << 20) + 4096
+    buf = torch.ones(nbytes // 4, dtype=torch.float32, device=device)
+    sink = torch.zeros((nbytes + 65535) // 65536, dtype=torch.int32, device=device)
+    st = nat.lib().msattn_probe_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(),
+                                            nat.stream_handle(device))
+    assert st == nat.OK
+    torch.cuda.synchronize()
+    assert not sink.any()
