@@ -19,7 +19,9 @@ Differences, deliberate:
     attention.py:131, :236) would;
   * pad rows (table -1, ctx 0) are true no-ops: write_kv skips hole pages and a
     row with no key gets zeros, where the reference's pad rows write into and read
-    from the cache's last page.
+    from the cache's last page: their context length becomes 1 through
+    `row_starts = ctx` (model_runner.py:70-76, 273) and page id -1 wraps to
+    num_blocks - 1 (attention.py:131-133, 171).
 """
 from __future__ import annotations
 
