@@ -15,7 +15,13 @@ namespace {
 
 using namespace msattn;
 
-constexpr int kPartitionChoices[] = {kPartMax, kPartMax / 2, kPartMax / 4};
+// Partition sizes, largest first: a launch takes the largest that reaches kTargetSlots
+// workgroups, else the smallest. The smallest serves the small, latency-bound decodes
+// (C1: 4 sequences of at most 512 tokens), where more, shorter workgroups shorten the
+// launch; every choice holds a whole number of 16-token tiles per MFMA wave.
+constexpr int kPartitionChoices[] = {kPartMax, kPartMax / 2, kPartMax / 4, kPartMax / 8};
+static_assert(kPartMax / 8 >= 16 * kMfmaWaves && (kPartMax / 8) % (16 * kMfmaWaves) == 0,
+              "every partition choice splits into whole tiles per wave");
 #ifndef MSATTN_TARGET_SLOTS
 #define MSATTN_TARGET_SLOTS 512
 #endif

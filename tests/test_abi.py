@@ -39,7 +39,8 @@ def test_abi_version_and_status_strings():
     (64, 1, 32, 8, 128, 8192, 512),     # C3
     (8, 1, 32, 8, 128, 131072, 512),    # C4
     (32, 1, 14, 2, 64, 2048, 256),      # C2: few (row, head) units -> smaller partitions
-    (4, 1, 14, 2, 64, 512, 128),        # C1
+    (4, 1, 14, 2, 64, 512, 64),         # C1: the smallest partitions
+    (16, 1, 28, 4, 128, 4608, 512),     # C5 decode
 ])
 def test_partition_policy(B, q_len, H, KVH, D, ctx, part):
     lib = nat.lib()
