@@ -48,9 +48,12 @@ def parse():
     ap.add_argument("--graph-steps", type=int, default=0,
                     help="steps captured per graph (0: largest divisor of --steps up to 10)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kv-fp8", action="store_true",
-                    help="decode over the same caches stored as fp8 e4m3 (half the KV bytes; "
-                         "the query and the arithmetic stay bf16)")
+    ap.add_argument("--kv-dtype", choices=["same", "fp8", "fp32"], default="same",
+                    help="store the caches as fp8 e4m3 (half the KV bytes) or fp32 (twice; the "
+                         "reference runner's cache type, model_runner.py:122-123) instead of the "
+                         "config dtype; the query stays in the config dtype and the cache is "
+                         "cast to it as it is read. Bytes follow the cache's element size.")
+    ap.add_argument("--kv-fp8", action="store_true", help="same as --kv-dtype fp8")
     ap.add_argument("--no-cascade", action="store_true",
                     help="decode a shared-prefix workload (config 4) in one pass per sequence "
                          "instead of the cascade entry point")
@@ -63,7 +66,10 @@ def parse():
                     help="instead of the decode bench, time torch's out = in * 1 over 1 GiB "
                          "fp32 (the reference dispatch for scaling rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE) and the plain streaming-read kernel")
-    return ap.parse_args()
+    args = ap.parse_args()
+    if args.kv_fp8:
+        args.kv_dtype = "fp8"
+    return args
 
 
 def stream_probe(steps: int):
@@ -169,9 +175,10 @@ def main():
           f"D={w.head_dim} layers={w.layers} pool={w.num_blocks} pages, "
           f"ctx {min(w.lens)}..{max(w.lens)} (sum {sum(w.lens)}) in {time.time() - t0:.1f}s",
           file=sys.stderr, flush=True)
-    if args.kv_fp8:  # the same values rounded to e4m3; algorithmic bytes follow the dtype
-        w.k_caches = [c.to(torch.float8_e4m3fn) for c in w.k_caches]
-        w.v_caches = [c.to(torch.float8_e4m3fn) for c in w.v_caches]
+    kv_torch = {"fp8": torch.float8_e4m3fn, "fp32": torch.float32}.get(args.kv_dtype)
+    if kv_torch is not None:  # the same values stored as kv_torch; bytes follow the dtype
+        w.k_caches = [c.to(kv_torch) for c in w.k_caches]
+        w.v_caches = [c.to(kv_torch) for c in w.v_caches]
 
     B, H, KVH, D, bs = w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
     table = w.table.to(device=dev, dtype=torch.int32).contiguous()
@@ -275,7 +282,7 @@ def main():
     read_ceiling = stream_read_gbs(dev)
 
     traffic = None
-    tfile = PROFILES / f"traffic_{w.name}{'-fp8' if args.kv_fp8 else ''}.json"
+    tfile = PROFILES / f"traffic_{w.name}{'' if args.kv_dtype == 'same' else '-' + args.kv_dtype}.json"
     if tfile.exists():
         try:
             traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
@@ -305,7 +312,7 @@ def main():
             "pool_pages": w.num_blocks, "partition_tokens": part_tokens,
             "algorithmic_bytes_per_layer": per_layer_bytes,
             "shared_prefix_pages": w.shared_prefix_pages, "cascade": bool(cascade),
-            "kv_dtype": "fp8_e4m3" if args.kv_fp8 else str(w.dtype).replace("torch.", ""),
+            "kv_dtype": str(w.k_caches[0].dtype).replace("torch.", ""),
             "steps_per_graph": gsteps, "us_per_step_one_per_graph": round(ms_single * 1e3, 2),
         },
         "roofline": {
@@ -324,7 +331,7 @@ def main():
         },
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline and not args.kv_fp8:  # the baseline is the bf16 cache's
+    if not args.no_cpu_baseline and args.kv_dtype == "same":  # the config dtype's baseline
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

@@ -45,6 +45,7 @@ COMMON_FLAGS = [
 FILE_FLAGS = {
     "prefill_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "prefill_mfma_fp8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "prefill_mfma_f32kv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

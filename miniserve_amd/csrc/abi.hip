@@ -194,16 +194,59 @@ int device_cus() {
   return n;
 }
 
+// Generic kernel for every (query, cache) type pair: the cache is read as stored and
+// cast to the query type (miniserve/attention.py:240-241).
+template <typename QT>
+hipError_t dispatch_split_q(const SplitParams& p, int kv_dtype, int D, int RT, hipStream_t s,
+                            bool* sup) {
+  switch (kv_dtype) {
+    case MSATTN_F32: return launch_split<QT, float>(p, D, RT, s, sup);
+    case MSATTN_F16: return launch_split<QT, _Float16>(p, D, RT, s, sup);
+    case MSATTN_BF16: return launch_split<QT, bf16_t>(p, D, RT, s, sup);
+    case MSATTN_FP8_E4M3: return launch_split<QT, fp8_t>(p, D, RT, s, sup);
+    default: break;
+  }
+  *sup = false;
+  return hipSuccess;
+}
+
 hipError_t dispatch_split(const SplitParams& p, int q_dtype, int kv_dtype, int D, int RT,
                           hipStream_t s, bool* sup) {
   *sup = false;
-  if (q_dtype == MSATTN_F32 && kv_dtype == MSATTN_F32) return launch_split<float, float>(p, D, RT, s, sup);
-  if (q_dtype == MSATTN_F16 && kv_dtype == MSATTN_F16) return launch_split<_Float16, _Float16>(p, D, RT, s, sup);
-  if (q_dtype == MSATTN_BF16 && kv_dtype == MSATTN_BF16) return launch_split<bf16_t, bf16_t>(p, D, RT, s, sup);
-  if (q_dtype == MSATTN_F32 && kv_dtype == MSATTN_FP8_E4M3) return launch_split<float, fp8_t>(p, D, RT, s, sup);
-  if (q_dtype == MSATTN_F16 && kv_dtype == MSATTN_FP8_E4M3) return launch_split<_Float16, fp8_t>(p, D, RT, s, sup);
-  if (q_dtype == MSATTN_BF16 && kv_dtype == MSATTN_FP8_E4M3) return launch_split<bf16_t, fp8_t>(p, D, RT, s, sup);
+  switch (q_dtype) {
+    case MSATTN_F32: return dispatch_split_q<float>(p, kv_dtype, D, RT, s, sup);
+    case MSATTN_F16: return dispatch_split_q<_Float16>(p, kv_dtype, D, RT, s, sup);
+    case MSATTN_BF16: return dispatch_split_q<bf16_t>(p, kv_dtype, D, RT, s, sup);
+    default: break;
+  }
   return hipSuccess;
+}
+
+// The MFMA kernels (partition and stream-K decode, chunked prefill, the cascade's prefix
+// pass) take a bf16/fp16 query over a cache of its own type, of fp8 e4m3 (widened
+// exactly) or of fp32 (rounded to the query type as loaded), head_dim 64 or 128, pages
+// of whole 16-token tiles, a tile span their 32-bit offsets reach, and a query they can
+// read with 16-byte loads.
+bool mfma_route_ok(const void* query, int q_dtype, int kv_dtype, int head_dim, int block_size,
+                   int64_t slot_stride) {
+  return (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
+         (kv_dtype == q_dtype || kv_dtype == MSATTN_FP8_E4M3 || kv_dtype == MSATTN_F32) &&
+         (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 &&
+         tile_span_ok(slot_stride, head_dim, kv_dtype) && aligned(query, 16);
+}
+
+// Launch an MFMA kernel family for (query type T, the cache's type): F is a generic
+// callable taking (T{}, KT{}) tags.
+template <typename T, typename F>
+hipError_t with_kv_type(int kv_dtype, F&& f) {
+  if (kv_dtype == MSATTN_FP8_E4M3) return f(T{}, fp8_t{});
+  if (kv_dtype == MSATTN_F32) return f(T{}, float{});
+  return f(T{}, T{});
+}
+template <typename F>
+hipError_t with_mfma_types(int q_dtype, int kv_dtype, F&& f) {
+  if (q_dtype == MSATTN_BF16) return with_kv_type<bf16_t>(kv_dtype, f);
+  return with_kv_type<_Float16>(kv_dtype, f);
 }
 
 int check_cache_args(const void* k_cache, const void* v_cache, int64_t blk, int64_t slot,
@@ -283,14 +326,10 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
 
   const int G = num_heads / num_kv_heads;
   const int rows = q_len * G;
-  // MFMA path: a bf16/fp16 query over a KV cache of its own type or of fp8 e4m3,
-  // head_dim 64 or 128, pages holding whole 16-token tiles. Everything else takes
-  // the generic kernel.
+  // MFMA path where mfma_route_ok allows it; everything else takes the generic kernel.
   const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
-  const bool use_mfma = (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
-                        (kv_dtype == q_dtype || kv_fp8) && (head_dim == 64 || head_dim == 128) &&
-                        block_size % 16 == 0 &&
-                        tile_span_ok(cache_slot_stride, head_dim, kv_dtype);
+  const bool use_mfma = mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size,
+                                      cache_slot_stride);
   const int RT = use_mfma ? mfma_rows_per_tile(rows) : rows_per_tile(rows);
   char* ws = static_cast<char*>(workspace);
   SplitParams p;
@@ -346,22 +385,17 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
     p.sk_group = largest_pow2_divisor_upto(units, sk_waves(kv_fp8 ? 1 : 2));
     p.sk_unit_groups = units / p.sk_group;
     const int grid = device_cus() < 256 ? kSkGrid * device_cus() / 256 : kSkGrid;
-    if (q_dtype == MSATTN_BF16)
-      e = kv_fp8 ? launch_decode_streamk<bf16_t, fp8_t>(p, head_dim, RT, grid, st, &sup)
-                 : launch_decode_streamk<bf16_t, bf16_t>(p, head_dim, RT, grid, st, &sup);
-    else
-      e = kv_fp8 ? launch_decode_streamk<_Float16, fp8_t>(p, head_dim, RT, grid, st, &sup)
-                 : launch_decode_streamk<_Float16, _Float16>(p, head_dim, RT, grid, st, &sup);
+    e = with_mfma_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
+      return launch_decode_streamk<decltype(t), decltype(kt)>(p, head_dim, RT, grid, st, &sup);
+    });
     if (!sup) return MSATTN_ERR_UNSUPPORTED;
     return hip_status(e);
   }
   *kind = 0;  // the partition kernels below
-  if (use_mfma && q_dtype == MSATTN_BF16) {
-    e = kv_fp8 ? launch_decode_mfma<bf16_t, fp8_t>(p, head_dim, RT, st, &sup)
-               : launch_decode_mfma<bf16_t, bf16_t>(p, head_dim, RT, st, &sup);
-  } else if (use_mfma) {
-    e = kv_fp8 ? launch_decode_mfma<_Float16, fp8_t>(p, head_dim, RT, st, &sup)
-               : launch_decode_mfma<_Float16, _Float16>(p, head_dim, RT, st, &sup);
+  if (use_mfma) {
+    e = with_mfma_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
+      return launch_decode_mfma<decltype(t), decltype(kt)>(p, head_dim, RT, st, &sup);
+    });
   } else {
     e = dispatch_split(p, q_dtype, kv_dtype, head_dim, RT, st, &sup);
   }
@@ -450,14 +484,11 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
                            int table_width, int max_context, int causal, int window,
                            float scale, int q_dtype, int kv_dtype, void* stream) {
   if (!out) return MSATTN_ERR_INVALID_ARG;
-  if (!aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
+  if (!dtype_ok(q_dtype) || !aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
   // Chunked prefill (more than one 16-row tile of query rows per KV head): the MFMA
-  // prefill kernel writes the normalised output directly.
-  if (q_len > 1 && (kv_dtype == q_dtype || kv_dtype == MSATTN_FP8_E4M3) &&
-      (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
-      (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 && batch <= 65535 &&
-      tile_span_ok(cache_slot_stride, head_dim, kv_dtype) &&
-      num_heads > 0 &&
+  // prefill kernel writes the normalised output directly, four elements (8 bytes) a store.
+  if (q_len > 1 && mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, cache_slot_stride) &&
+      aligned(out, 8) && batch <= 65535 && num_heads > 0 &&
       num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
       static_cast<int64_t>(q_len) * (num_heads / num_kv_heads) > 16) {
     if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
@@ -468,7 +499,6 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
                                     cache_head_stride, kv_dtype, block_size, num_blocks,
                                     table_width);
     if (rc != MSATTN_OK) return rc;
-    if (!aligned(query, 16)) return MSATTN_ERR_INVALID_ARG;
     const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
     if (workspace_bytes < L.total()) return MSATTN_ERR_WORKSPACE;
     PrefillParams pp{};
@@ -501,14 +531,9 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
     pp.xcd_per = static_cast<int>((tasks + kXcds - 1) / kXcds);
     bool sup = false;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
-    hipError_t e;
-    if (q_dtype == MSATTN_BF16)
-      e = kv_fp8 ? launch_prefill_mfma<bf16_t, fp8_t>(pp, head_dim, st, &sup)
-                 : launch_prefill_mfma<bf16_t, bf16_t>(pp, head_dim, st, &sup);
-    else
-      e = kv_fp8 ? launch_prefill_mfma<_Float16, fp8_t>(pp, head_dim, st, &sup)
-                 : launch_prefill_mfma<_Float16, _Float16>(pp, head_dim, st, &sup);
+    const hipError_t e = with_mfma_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
+      return launch_prefill_mfma<decltype(t), decltype(kt)>(pp, head_dim, st, &sup);
+    });
     if (!sup) return MSATTN_ERR_UNSUPPORTED;
     return hip_status(e);
   }
@@ -578,19 +603,16 @@ int msattn_paged_attention_prefix(const void* query, const void* k_cache, const 
   const int rc = check_cache_args(k_cache, v_cache, cache_block_stride, cache_slot_stride,
                                   cache_head_stride, kv_dtype, block_size, num_blocks, table_width);
   if (rc != MSATTN_OK) return rc;
-  if (!aligned(query, 16) || !aligned(out, dtype_bytes(q_dtype)) || !aligned(workspace, 16))
+  if (!aligned(query, dtype_bytes(q_dtype)) || !aligned(out, dtype_bytes(q_dtype)) ||
+      !aligned(workspace, 16))
     return MSATTN_ERR_INVALID_ARG;
   const PrefixLayout X = prefix_layout(batch, num_heads, num_kv_heads, head_dim, block_size,
                                        max_context, prefix_pages);
   if (workspace_bytes < X.total) return MSATTN_ERR_WORKSPACE;
   // The shared-prefix pass runs the MFMA prefill kernel; other types and head sizes,
   // and calls without a shared prefix, attend in one pass over the whole context.
-  const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
-  const bool cascade = X.prefix > 0 && (kv_dtype == q_dtype || kv_fp8) &&
-                       (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
-                       (head_dim == 64 || head_dim == 128) &&
-                       block_size % 16 == 0 &&
-                       tile_span_ok(cache_slot_stride, head_dim, kv_dtype);
+  const bool cascade = X.prefix > 0 && mfma_route_ok(query, q_dtype, kv_dtype, head_dim,
+                                                     block_size, cache_slot_stride);
   if (!cascade)
     return msattn_paged_attention(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
                                   cache_head_stride, block_table, context_lens, out, workspace,
@@ -637,13 +659,9 @@ int msattn_paged_attention_prefix(const void* query, const void* k_cache, const 
   if (static_cast<int64_t>(pp.rblocks) * num_kv_heads >= (int64_t(1) << 31) || X.npart > 65535)
     return MSATTN_ERR_UNSUPPORTED;
   bool sup = false;
-  hipError_t e;
-  if (q_dtype == MSATTN_BF16)
-    e = kv_fp8 ? launch_prefix_partials<bf16_t, fp8_t>(pp, head_dim, st, &sup)
-               : launch_prefix_partials<bf16_t, bf16_t>(pp, head_dim, st, &sup);
-  else
-    e = kv_fp8 ? launch_prefix_partials<_Float16, fp8_t>(pp, head_dim, st, &sup)
-               : launch_prefix_partials<_Float16, _Float16>(pp, head_dim, st, &sup);
+  const hipError_t e = with_mfma_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
+    return launch_prefix_partials<decltype(t), decltype(kt)>(pp, head_dim, st, &sup);
+  });
   if (!sup) return MSATTN_ERR_UNSUPPORTED;
   if (e != hipSuccess) return MSATTN_ERR_HIP;
 

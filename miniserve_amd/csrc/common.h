@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace msattn {
 
 constexpr int kWave = 64;
@@ -98,6 +100,24 @@ template <typename T> __device__ __forceinline__ float round_to(float v) {
   Elt<T>::store(&t, v);
   return Elt<T>::load(&t);
 }
+
+// K/V as a query of type QT sees them. The reference casts the gathered K/V to the
+// query dtype before attending (miniserve/attention.py:240-241): a widening cast (fp8 or
+// a 2-byte type to fp32, fp8 to a 2-byte type) is exact and leaves the value alone; a
+// narrowing one (fp32 to bf16/fp16, bf16 <-> fp16) rounds to nearest even, as
+// torch.Tensor.to does.
+template <typename QT, typename KT> struct KvCast {
+  static constexpr bool kRounds = !std::is_same<QT, float>::value &&
+                                  !std::is_same<QT, KT>::value &&
+                                  !std::is_same<KT, fp8_t>::value;
+  template <int N>
+  __device__ static void apply(float (&x)[N]) {
+    if constexpr (kRounds) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) x[e] = round_to<QT>(x[e]);
+    }
+  }
+};
 
 // Unpack one 16-byte chunk (four dwords) of KV elements into fp32.
 template <typename T> struct Chunk;

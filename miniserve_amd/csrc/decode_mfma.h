@@ -1,4 +1,6 @@
-// Paged decode partials with MFMA scores (gfx950, bf16/fp16 KV, head_dim 64 or 128).
+// Paged decode partials with MFMA scores (gfx950): a bf16/fp16 query over a cache of its
+// type, of fp8 e4m3 or of fp32 (converted to the query type in registers), head_dim 64
+// or 128.
 //
 // Same contract and workspace output as split_kernel (split_kernel.h): one
 // workgroup per (sequence b, KV head, row tile, context partition), writing the
@@ -252,6 +254,51 @@ template <typename T> struct Kv8<T, fp8_t> {
   }
 };
 
+// An fp32 cache read by a bf16/fp16 query: eight elements are 32 bytes (two 16-byte
+// loads), kept raw while in flight and rounded to T (nearest even) once they arrive.
+// That is the reference's cast of the gathered K/V to query.dtype
+// (miniserve/attention.py:240-241) done in registers, so the result is that of the same
+// kernel run on the cache converted to T beforehand. Chunks follow the split of a cache
+// of T (dims 8 (4j + g)): the four lane groups of a row read 128 contiguous bytes per
+// chunk index.
+template <typename T> struct Kv8<T, float> {
+  struct raw_t {
+    uint4 lo, hi;
+  };
+  __host__ __device__ static constexpr int qk_dim0(int j, int g, int /*JD*/) {
+    return 8 * (4 * j + g);
+  }
+  template <int AUX>
+  __device__ static raw_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return raw_t{buffer_load16<AUX>(r, off), buffer_load16<AUX>(r, off + 16u)};
+  }
+  template <int AUX, int JD>
+  __device__ static void load_k(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int g,
+                                raw_t (&kb)[JD]) {
+#pragma unroll
+    for (int j = 0; j < JD; ++j)
+      kb[j] = load<AUX>(r, row_off + static_cast<uint32_t>(qk_dim0(j, g, JD)) * 4u);
+  }
+  __device__ static float f(uint32_t w) { return __uint_as_float(w); }
+  // eight fp32 values -> eight T values (nearest even), packed
+  __device__ static uint4 operand(const raw_t& x) {
+    return make_uint4(Pack2<T>::pack(f(x.lo.x), f(x.lo.y)), Pack2<T>::pack(f(x.lo.z), f(x.lo.w)),
+                      Pack2<T>::pack(f(x.hi.x), f(x.hi.y)), Pack2<T>::pack(f(x.hi.z), f(x.hi.w)));
+  }
+  // Dim e of two tokens' chunks rounded to T and packed (token a low).
+  __device__ static void pairs(const raw_t& a, const raw_t& b, uint32_t (&o)[8]) {
+    const uint32_t wa[8] = {a.lo.x, a.lo.y, a.lo.z, a.lo.w, a.hi.x, a.hi.y, a.hi.z, a.hi.w};
+    const uint32_t wb[8] = {b.lo.x, b.lo.y, b.lo.z, b.lo.w, b.hi.x, b.hi.y, b.hi.z, b.hi.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = Pack2<T>::pack(f(wa[e]), f(wb[e]));
+  }
+  // The values the MFMA operand holds, as fp32 (rounded to T).
+  __device__ static void unpack(const raw_t& x, float* o) { Chunk<T>::unpack(operand(x), o); }
+  __device__ static raw_t keep_if(const raw_t& x, bool keep) {
+    return keep ? x : raw_t{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+  }
+};
+
 #ifndef MSATTN_PV_DOT2
 #define MSATTN_PV_DOT2 1
 #endif
@@ -347,10 +394,13 @@ __host__ __device__ constexpr int tile_token(int i) {
 // chunk j +/- JD/2 of the same lane (2-byte caches: dims 8 (4j + g); an fp8 cache at
 // D = 128: dims 64 (j / 2) + 16 g + 8 (j % 2)), or, for an fp8 cache at D = 64 (dims
 // 16 g + 8 j), chunk j of lane group g +/- 2, the lane 32 away, which one
-// v_permlane32_swap brings over. The rotated row is rounded back to T, as the unfused
-// (q * cos + rotate_half(q) * sin).to(T) of miniserve/attention.py:41-62 /
-// kernels/paged_attn_triton.py:211-220 would be. Lanes l and l ^ 32 (the same query row)
-// are both active or both not.
+// v_permlane32_swap brings over. The rotation is that of kernels/paged_attn_triton.py:211-220
+// (fp32 tables, fp32 products and sum); the rotated row is then rounded back to T, as the
+// matrix cores take a T operand: the result is (q * cos + rotate_half(q) * sin).to(T)
+// (miniserve/attention.py:41-62 with fp32 tables), where the reference's Triton kernel and
+// flash_decode_reference (:134-138) keep the rotated query in fp32. That one rounding of
+// the query (relative 2^-9 for bf16) is the only difference. Lanes l and l ^ 32 (the same
+// query row) are both active or both not.
 template <typename T, typename KT, int D>
 __device__ __forceinline__ void rope_chunks(uint4 (&qb)[D / 32], const float* cs, const float* sn,
                                             int g) {
@@ -726,6 +776,8 @@ MSATTN_DECLARE_MFMA_LAUNCHER(bf16_t, bf16_t)
 MSATTN_DECLARE_MFMA_LAUNCHER(_Float16, _Float16)
 MSATTN_DECLARE_MFMA_LAUNCHER(bf16_t, fp8_t)
 MSATTN_DECLARE_MFMA_LAUNCHER(_Float16, fp8_t)
+MSATTN_DECLARE_MFMA_LAUNCHER(bf16_t, float)
+MSATTN_DECLARE_MFMA_LAUNCHER(_Float16, float)
 #undef MSATTN_DECLARE_MFMA_LAUNCHER
 
 }  // namespace msattn

@@ -1,4 +1,5 @@
-// Stream-K paged decode (q_len == 1) for gfx950: bf16/fp16 KV, head_dim 64 or 128.
+// Stream-K paged decode (q_len == 1) for gfx950: a bf16/fp16 query over a cache of its
+// type, of fp8 e4m3 or of fp32, head_dim 64 or 128.
 //
 // Work decomposition. A "unit" is (row tile, KV head): the up-to-16 GQA query
 // rows that read one KV head. Units are grouped UG at a time (UG KV heads side
@@ -442,6 +443,8 @@ MSATTN_DECLARE_SK_LAUNCHER(bf16_t, bf16_t)
 MSATTN_DECLARE_SK_LAUNCHER(_Float16, _Float16)
 MSATTN_DECLARE_SK_LAUNCHER(bf16_t, fp8_t)
 MSATTN_DECLARE_SK_LAUNCHER(_Float16, fp8_t)
+MSATTN_DECLARE_SK_LAUNCHER(bf16_t, float)
+MSATTN_DECLARE_SK_LAUNCHER(_Float16, float)
 #undef MSATTN_DECLARE_SK_LAUNCHER
 
 #define MSATTN_SK_RT(T, KT, D)                                                      \

@@ -598,6 +598,8 @@ MSATTN_DECLARE_PF(bf16_t, bf16_t)
 MSATTN_DECLARE_PF(_Float16, _Float16)
 MSATTN_DECLARE_PF(bf16_t, fp8_t)
 MSATTN_DECLARE_PF(_Float16, fp8_t)
+MSATTN_DECLARE_PF(bf16_t, float)
+MSATTN_DECLARE_PF(_Float16, float)
 #undef MSATTN_DECLARE_PF
 
 #define MSATTN_DEFINE_PF(T, KT)                                                                \

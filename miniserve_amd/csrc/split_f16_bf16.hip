@@ -1,0 +1,10 @@
+// Generic split-K partial kernels for a fp16 query over a bf16 KV cache:
+// K/V rounded to the query type (nearest even) as loaded, the reference's
+// .to(query.dtype) of the gathered rows (miniserve/attention.py:240-241).
+#include "split_kernel.h"
+
+namespace msattn {
+
+MSATTN_SPLIT_LAUNCHER(_Float16, bf16_t)
+
+}  // namespace msattn

@@ -1,37 +1,9 @@
-// Split-K partial kernels instantiated for query _Float16, KV cache fp8_t.
-// Head dims compiled: 16, 32, 64, 96, 128, 256; rows per tile 1, 2, 4, 8.
+// Generic split-K partial kernels for a fp16 query over a fp8 e4m3 KV cache:
+// K/V widened exactly to the query type.
 #include "split_kernel.h"
 
 namespace msattn {
 
-template <>
-hipError_t launch_split<_Float16, fp8_t>(const SplitParams& p, int D, int RT, hipStream_t stream,
-                                    bool* supported) {
-  *supported = true;
-  switch (D) {
-    case 16:
-      MSATTN_SPLIT_RT(_Float16, fp8_t, 16)
-      break;
-    case 32:
-      MSATTN_SPLIT_RT(_Float16, fp8_t, 32)
-      break;
-    case 64:
-      MSATTN_SPLIT_RT(_Float16, fp8_t, 64)
-      break;
-    case 96:
-      MSATTN_SPLIT_RT(_Float16, fp8_t, 96)
-      break;
-    case 128:
-      MSATTN_SPLIT_RT(_Float16, fp8_t, 128)
-      break;
-    case 256:
-      MSATTN_SPLIT_RT(_Float16, fp8_t, 256)
-      break;
-    default:
-      break;
-  }
-  *supported = false;
-  return hipSuccess;
-}
+MSATTN_SPLIT_LAUNCHER(_Float16, fp8_t)
 
 }  // namespace msattn

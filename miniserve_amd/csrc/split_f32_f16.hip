@@ -1,0 +1,9 @@
+// Generic split-K partial kernels for a fp32 query over a fp16 KV cache:
+// K/V widened exactly to the query type.
+#include "split_kernel.h"
+
+namespace msattn {
+
+MSATTN_SPLIT_LAUNCHER(float, _Float16)
+
+}  // namespace msattn

@@ -23,6 +23,10 @@
 //   3  P.V: the same token walk over V, fp32 accumulators per lane, reduced
 //      across lanes and waves through LDS.
 //
+// K/V elements are widened to fp32 and, when the cache type is wider than or differs
+// from the query type, rounded to the query type first (KvCast, common.h): the cast of
+// the gathered K/V to query.dtype in miniserve/attention.py:240-241.
+//
 // The algorithm is the split decomposition of kernels/paged_attn_triton.py
 // (_split_kernel :176-248, reference restatement :102-171); the masking rules
 // are PagedAttention.build_mask (miniserve/attention.py:135-153).
@@ -259,6 +263,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
     for (int u = 0; u < U; ++u) {
       float kf[EPL];
       CK::unpack(raw[u], kf);
+      KvCast<QT, KT>::apply(kf);
       float dot[RT];
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
@@ -324,6 +329,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
       if (tt[u] >= 0) {
         float vf[EPL];
         CK::unpack(raw[u], vf);
+        KvCast<QT, KT>::apply(vf);
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
           const float pr = s_sc[tt[u] * RT + r];
@@ -389,25 +395,59 @@ hipError_t launch_split_one(const SplitParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-#define MSATTN_SPLIT_RT(QT, KT, D)                                           \
-  switch (RT) {                                                              \
-    case 1: return launch_split_one<QT, KT, D, 1>(p, stream);                \
-    case 2: return launch_split_one<QT, KT, D, 2>(p, stream);                \
-    case 4: return launch_split_one<QT, KT, D, 4>(p, stream);                \
-    case 8: return launch_split_one<QT, KT, D, 8>(p, stream);                \
-    default: break;                                                          \
+// One head size: row tiles of 1, 2, 4 or 8 query rows; head sizes whose K/V row is not
+// whole 16-byte chunks of the cache type are not compiled.
+template <typename QT, typename KT, int D>
+hipError_t launch_split_d(const SplitParams& p, int RT, hipStream_t stream, bool* supported) {
+  if constexpr ((D * Elt<KT>::kBytes) % 16 == 0) {
+    switch (RT) {
+      case 1: return launch_split_one<QT, KT, D, 1>(p, stream);
+      case 2: return launch_split_one<QT, KT, D, 2>(p, stream);
+      case 4: return launch_split_one<QT, KT, D, 4>(p, stream);
+      case 8: return launch_split_one<QT, KT, D, 8>(p, stream);
+      default: break;
+    }
+  }
+  *supported = false;
+  return hipSuccess;
+}
+
+// Explicit specializations, one per compiled dtype pair (split_<pair>.hip): head dims
+// 16, 24, 32, 64, 96, 128 and 256 (24 only where a row is whole 16-byte chunks).
+#define MSATTN_SPLIT_LAUNCHER(QT, KT)                                                      \
+  template <>                                                                              \
+  hipError_t launch_split<QT, KT>(const SplitParams& p, int D, int RT, hipStream_t stream, \
+                                  bool* supported) {                                       \
+    *supported = true;                                                                     \
+    switch (D) {                                                                           \
+      case 16: return launch_split_d<QT, KT, 16>(p, RT, stream, supported);                \
+      case 24: return launch_split_d<QT, KT, 24>(p, RT, stream, supported);                \
+      case 32: return launch_split_d<QT, KT, 32>(p, RT, stream, supported);                \
+      case 64: return launch_split_d<QT, KT, 64>(p, RT, stream, supported);                \
+      case 96: return launch_split_d<QT, KT, 96>(p, RT, stream, supported);                \
+      case 128: return launch_split_d<QT, KT, 128>(p, RT, stream, supported);              \
+      case 256: return launch_split_d<QT, KT, 256>(p, RT, stream, supported);              \
+      default: break;                                                                      \
+    }                                                                                      \
+    *supported = false;                                                                    \
+    return hipSuccess;                                                                     \
   }
 
-// Explicit specializations, one per compiled dtype pair (split_<pair>.hip).
 #define MSATTN_DECLARE_SPLIT(QT, KT)                                                   \
   template <>                                                                          \
   hipError_t launch_split<QT, KT>(const SplitParams& p, int D, int RT, hipStream_t stream, \
                                   bool* supported);
 MSATTN_DECLARE_SPLIT(float, float)
-MSATTN_DECLARE_SPLIT(_Float16, _Float16)
-MSATTN_DECLARE_SPLIT(bf16_t, bf16_t)
+MSATTN_DECLARE_SPLIT(float, _Float16)
+MSATTN_DECLARE_SPLIT(float, bf16_t)
 MSATTN_DECLARE_SPLIT(float, fp8_t)
+MSATTN_DECLARE_SPLIT(_Float16, float)
+MSATTN_DECLARE_SPLIT(_Float16, _Float16)
+MSATTN_DECLARE_SPLIT(_Float16, bf16_t)
 MSATTN_DECLARE_SPLIT(_Float16, fp8_t)
+MSATTN_DECLARE_SPLIT(bf16_t, float)
+MSATTN_DECLARE_SPLIT(bf16_t, _Float16)
+MSATTN_DECLARE_SPLIT(bf16_t, bf16_t)
 MSATTN_DECLARE_SPLIT(bf16_t, fp8_t)
 #undef MSATTN_DECLARE_SPLIT
 

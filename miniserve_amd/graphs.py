@@ -110,6 +110,14 @@ class GraphedDecodeRunner:
         """Capture the step for (bucket, input set); returns its replay callable."""
         dev = self._device
         buf = self._in[set_idx]
+        # The warm-up below really runs the step on this set, which may still hold an
+        # earlier decode's rows: their pages may since belong to other sequences, and
+        # write_kv would overwrite those. Every row becomes a pad row first (all pages
+        # holes, no context), so the warm-up writes and reads nothing; decode() fills the
+        # set before any replay.
+        buf["table"].fill_(-1)
+        buf["start"].zero_()
+        buf["lens"].zero_()
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):  # warm-up outside capture

@@ -18,8 +18,13 @@ import numpy as np
 import torch
 
 
-def gather_rows(cache: torch.Tensor, table_row, length: int) -> np.ndarray:
-    """Float64 [length, kv_heads, head_dim] rows of one sequence (integer page map)."""
+def gather_rows(cache: torch.Tensor, table_row, length: int,
+                cast_to: torch.dtype | None = None) -> np.ndarray:
+    """Float64 [length, kv_heads, head_dim] rows of one sequence (integer page map).
+
+    ``cast_to``: the rows are first converted to that dtype, as the reference casts the
+    gathered K/V to the query dtype before attending (miniserve/attention.py:240-241).
+    """
     bs = cache.shape[1]
     pos = torch.arange(length)
     phys = torch.as_tensor(np.asarray(table_row, dtype=np.int64))[pos // bs]
@@ -27,6 +32,8 @@ def gather_rows(cache: torch.Tensor, table_row, length: int) -> np.ndarray:
         rows = cache.view(torch.uint8)[phys, pos % bs].view(torch.float8_e4m3fn)
     else:
         rows = cache[phys, pos % bs]
+    if cast_to is not None:
+        rows = rows.to(cast_to)
     return rows.double().numpy()
 
 
@@ -66,8 +73,13 @@ def attend_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, keep: np.ndarray, sc
 def paged_attention_f64(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                         block_table, context_lens, causal: bool = True,
                         window: int | None = None, scale: float | None = None,
-                        rows: list[int] | None = None) -> np.ndarray:
-    """Float64 [batch, q_len, H, D] (only `rows` filled when given, others zero)."""
+                        rows: list[int] | None = None, kv_cast: bool = False) -> np.ndarray:
+    """Float64 [batch, q_len, H, D] (only `rows` filled when given, others zero).
+
+    ``kv_cast``: K/V rows are converted to the query dtype before the float64 math, the
+    reference's ``.to(query.dtype)`` of the gathered rows (attention.py:240-241); it
+    matters when the cache type is wider than the query's or differs from it.
+    """
     B, q_len, H, D = query.shape
     scale = 1.0 / math.sqrt(D) if scale is None else scale
     table = torch.as_tensor(block_table)
@@ -81,7 +93,8 @@ def paged_attention_f64(query: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
         L = lens[b]
         if L <= 0:
             continue
-        k = gather_rows(k_cache, table[b], L)
-        v = gather_rows(v_cache, table[b], L)
+        cast = query.dtype if kv_cast else None
+        k = gather_rows(k_cache, table[b], L, cast)
+        v = gather_rows(v_cache, table[b], L, cast)
         out[b] = attend_f64(qf[b], k, v, keep_mask(L, q_len, causal, window), scale)
     return out

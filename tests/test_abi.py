@@ -94,7 +94,8 @@ def _attn_args(**over):
     (dict(sstride=2 * 64 + 1), nat.ERR_INVALID_ARG),      # row not 16-byte aligned
     (dict(ws_bytes=16), nat.ERR_WORKSPACE),
     (dict(D=40, bstride=16 * 2 * 40, sstride=2 * 40, hstride=40), nat.ERR_UNSUPPORTED),
-    (dict(qd=nat.F32, kvd=nat.BF16), nat.ERR_UNSUPPORTED),
+    (dict(query=1), nat.ERR_INVALID_ARG),                  # query not aligned to its element
+    (dict(out=2), nat.ERR_INVALID_ARG),                    # output not aligned to its element
 ])
 def test_paged_attention_argument_errors(over, status):
     """Every error path returns before any HIP call, so it runs without a GPU."""
@@ -162,7 +163,7 @@ def _prefix_args(pages=1, query_offset=0, **over):
     (dict(qd=nat.FP8_E4M3), nat.ERR_INVALID_ARG),
     (dict(scale=float("inf")), nat.ERR_INVALID_ARG),
     (dict(ws_bytes=16), nat.ERR_WORKSPACE),
-    (dict(query_offset=2), nat.ERR_INVALID_ARG),          # query not 16-byte aligned
+    (dict(query_offset=2), nat.ERR_INVALID_ARG),          # fp32 query not 4-byte aligned
 ])
 def test_prefix_entry_argument_errors(over, status):
     """msattn_paged_attention_prefix returns before any HIP call on a bad argument."""

@@ -90,3 +90,42 @@ def test_graph_runner_bucket_contract():
         GraphedDecodeRunner([object()], table_width=4, buckets=(4, 2))
     with pytest.raises(ValueError, match="sorted, start at 1"):
         GraphedDecodeRunner([object()], table_width=4, buckets=(0, 2))
+
+
+@pytest.mark.parametrize("pos_shape", ["seq", "batch_seq"])
+@pytest.mark.parametrize("with_k", [True, False])
+def test_apply_rope_closed_form(pos_shape, with_k):
+    """apply_rope (miniserve/attention.py:41-62) against the rotation written out element
+    by element: out[..., d] = x[d] cos[p, d] - x[d + D/2] sin[p, d] for d < D/2 and
+    x[d] cos[p, d] + x[d - D/2] sin[p, d] above, with cos/sin cast to the input dtype."""
+    from miniserve_amd import apply_rope
+
+    g = torch.Generator().manual_seed(2)
+    B, H, KVH, S, D = 2, 4, 2, 3, 8
+    q = torch.randn(B, H, S, D, generator=g)
+    k = torch.randn(B, KVH, S, D, generator=g) if with_k else None
+    cos = torch.randn(16, D, generator=g)
+    sin = torch.randn(16, D, generator=g)
+    pos = torch.tensor([5, 0, 9]) if pos_shape == "seq" else torch.tensor([[5, 0, 9], [1, 15, 2]])
+    q_rot, k_rot = apply_rope(q, k, cos, sin, pos)
+
+    def closed(x):
+        out = torch.empty_like(x)
+        for b in range(x.shape[0]):
+            for h in range(x.shape[1]):
+                for s in range(S):
+                    p = int(pos[s] if pos.ndim == 1 else pos[b, s])
+                    for d in range(D):
+                        partner = -x[b, h, s, d + D // 2] if d < D // 2 else x[b, h, s, d - D // 2]
+                        out[b, h, s, d] = x[b, h, s, d] * cos[p, d] + partner * sin[p, d]
+        return out
+
+    assert torch.allclose(q_rot, closed(q), atol=1e-6)
+    if with_k:
+        assert torch.allclose(k_rot, closed(k), atol=1e-6)
+    else:
+        assert k_rot is None
+    # a planted mistake (partner without the sign flip) fails the same comparison
+    bad = q * cos[pos].unsqueeze(1 if pos.ndim == 2 else 0) + \
+        torch.cat([q[..., D // 2:], q[..., :D // 2]], -1) * sin[pos].unsqueeze(1 if pos.ndim == 2 else 0)
+    assert not torch.allclose(bad, closed(q), atol=1e-3)

@@ -142,3 +142,40 @@ def test_decode_steps_match_oracle(device):
         assert torch.equal(runner.layers[0].k_cache.cpu(), kc_ref)
         assert torch.equal(runner.layers[0].v_cache.cpu(), vc_ref)
         ctx = [c + 1 for c in ctx]
+
+
+def test_capture_of_new_bucket_leaves_freed_pages_alone(device):
+    """Capturing a bucket warms the step up on its input sets. After a decode, a set still
+    holds that step's rows; if one of their pages has since been freed and reused by
+    another sequence, the warm-up must not write the old k/v into it."""
+    g = torch.Generator().manual_seed(5)
+    pool, width = 64, 4
+    pa = PagedAttention(H, KVH, D, num_blocks=pool, block_size=BS, dtype=torch.bfloat16,
+                        kv_dtype=torch.bfloat16, device=device)
+    kc = torch.randn(pool, BS, KVH, D, generator=g).to(torch.bfloat16).to(device)
+    vc = torch.randn(pool, BS, KVH, D, generator=g).to(torch.bfloat16).to(device)
+    runner = GraphedDecodeRunner([DecodeLayer(pa, kc, vc)], table_width=width, buckets=(1, 2, 4))
+    tables = torch.randperm(pool, generator=g)[: 2 * width].view(2, width)
+    ctx = [10, 20]
+    for _ in range(2):  # both input sets now hold these rows (bucket 2 captured)
+        q = torch.randn(1, 2, 1, H, D, generator=g).to(torch.bfloat16).to(device)
+        k = torch.randn(1, 2, 1, KVH, D, generator=g).to(torch.bfloat16).to(device)
+        v = torch.randn(1, 2, 1, KVH, D, generator=g).to(torch.bfloat16).to(device)
+        runner.decode(q, k, v, [r.tolist() for r in tables], ctx)
+    # The pages the last step wrote into are freed and handed to another sequence,
+    # which fills them with its own keys and values.
+    freed = [int(tables[b, ctx[b] // BS]) for b in range(2)]
+    for p in freed:
+        kc[p] = 7.0
+        vc[p] = -7.0
+    k_before, v_before = kc.clone(), vc.clone()
+    note("capture bucket 4 after the pages were reused")
+    other = torch.randperm(pool, generator=g)[: 3 * width].view(3, width)
+    other = [[p for p in row.tolist() if p not in freed][:width] for row in other]
+    q = torch.zeros(1, 3, 1, H, D, dtype=torch.bfloat16, device=device)
+    k = torch.zeros(1, 3, 1, KVH, D, dtype=torch.bfloat16, device=device)
+    runner.decode(q, k, k, other, [0, 0, 0])  # bucket 4: a new capture
+    torch.cuda.synchronize()
+    for p in freed:
+        assert torch.equal(kc[p], k_before[p]) and torch.equal(vc[p], v_before[p]), \
+            f"page {p} was overwritten by the capture's warm-up"

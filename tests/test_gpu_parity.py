@@ -316,6 +316,33 @@ def test_rope_in_kernel_matches_unfused(device, H, KVH, D, dtype, kv_dtype, wide
     assert rel_err(fused, ref) < (1e-4 if dtype == torch.float32 else BF16_REL)
 
 
+@pytest.mark.parametrize("H,KVH,D,dtype,wide", [
+    (32, 8, 128, torch.bfloat16, True),     # stream-K MFMA kernel
+    (14, 2, 64, torch.bfloat16, False),     # partition MFMA kernel
+    (28, 4, 128, torch.float16, False),     # partition MFMA kernel, fp16
+])
+def test_rope_low_precision_against_fp32_rotation(device, H, KVH, D, dtype, wide):
+    """The reference's fused RoPE keeps the rotated query in fp32
+    (kernels/paged_attn_triton.py:211-220; flash_decode_reference :134-138), while the
+    MFMA kernels round it to the query type to feed the bf16/fp16 matrix cores: one
+    rounding of the rotated query (relative 2^-9 for bf16). Against the oracle's split-K
+    decode with the fp32 rotation (split_k.split_k_decode) the result stays within the
+    2e-2 max-rel bar."""
+    note(f"rope vs fp32 rotation H={H} KVH={KVH} D={D} {dtype} wide={wide}")
+    lens = [1, 300, 77, 1234, 16, 999]
+    width = 65536 // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
+    q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=D + H + 1)
+    cos, sin = rope_tables(max(lens) + 8, D)
+    pos = torch.tensor([L - 1 for L in lens])
+    fused = paged_attention(q.to(device), kc.to(device), vc.to(device), table, lens,
+                            max_context=width * 16,
+                            rope=(cos.to(device), sin.to(device), pos.to(device)))
+    ref = split_k.split_k_decode(q, kc, vc, table, lens, cos=cos, sin=sin, position=pos)
+    err = rel_err(fused, ref.double().numpy())
+    note(f"max-rel {err:.3e}")
+    assert err < BF16_REL
+
+
 def test_rope_contract(device):
     """Decode-only, as the reference's fused path; malformed tables are rejected."""
     q, kc, vc, table, _ = scenario(4, 2, 64, [40], block_size=16)
@@ -440,6 +467,34 @@ def test_holes_are_masked(device):
     vc2 = torch.stack([vc[p] for p in keep_pages])
     ref = dense.paged_attention_f64(q, kc2, vc2, torch.tensor([[0, 1, 2]]), [48])
     assert abs_err(out, ref) < FP32_ATOL
+
+
+def test_query_and_output_not_16_byte_aligned(device):
+    """The MFMA kernels read the query (and the prefill kernel writes the output) with
+    16- and 8-byte vector accesses; a query or output aligned only to its element size
+    takes the generic kernel (and a cascade decode the one-pass decode) instead, with the
+    same result within the bar."""
+    H, KVH, D = 32, 8, 128
+    lens = [300, 1000, 64, 2000]
+    for q_len, prefix in ((1, 0), (40, 0), (1, 2)):
+        note(f"misaligned query/out: q_len={q_len} prefix={prefix}")
+        q, kc, vc, table = paged_case(H, KVH, D, lens, torch.bfloat16, 16,
+                                      (max(lens) + 15) // 16 + 1, seed=q_len + prefix,
+                                      q_len=q_len)
+        if prefix:
+            table[:, :prefix] = table[0, :prefix]
+        n = q.numel()
+        qbuf = torch.empty(n + 1, dtype=torch.bfloat16, device=device)
+        qm = qbuf[1:].view(q.shape)
+        qm.copy_(q.to(device))
+        obuf = torch.empty(n + 1, dtype=torch.bfloat16, device=device)
+        om = obuf[1:].view(q.shape)
+        assert qm.data_ptr() % 16 and om.data_ptr() % 16
+        got = paged_attention(qm, kc.to(device), vc.to(device), table, lens, out=om,
+                              prefix_pages=prefix or None)
+        assert got.data_ptr() == om.data_ptr()
+        ref = dense.paged_attention_f64(q, kc, vc, table, lens)
+        assert rel_err(got, ref) < BF16_REL
 
 
 def test_partition_invariance(device):

@@ -339,3 +339,39 @@ def test_planted_mistakes_are_caught():
     finally:
         dense.attend_f64 = orig
     assert np.abs(bad - good).max() > 1e-3
+
+
+# ---------------------------------------------------------------- K/V cast to the query dtype
+
+@pytest.mark.parametrize("q_dtype,kv_dtype", [(torch.bfloat16, torch.float32),
+                                              (torch.float16, torch.float32),
+                                              (torch.float16, torch.bfloat16),
+                                              (torch.bfloat16, torch.float16)])
+def test_dense_kv_cast_context_one(q_dtype, kv_dtype):
+    """Context 1: the output is V[0] as the query dtype holds it (attention.py:240-241
+    casts the gathered rows to query.dtype). V values 1 + 2^-10 round to 1.0 in bf16 and
+    stay in fp16, so dropping the cast, or casting to the wrong type, fails."""
+    q, _, _, kc, vc, table, _ = scenario(4, 2, 8, [9, 9], q_len=1, scatter=True, seed=3)
+    q = q.to(q_dtype)
+    kc = kc.to(kv_dtype)
+    vc = torch.full_like(vc, 1.0 + 2.0 ** -10, dtype=torch.float32).to(kv_dtype)
+    vc[table[0, 0], 0] = 1.0e-8  # below half of fp16's smallest subnormal: fp16 rounds it to 0
+    out = dense.paged_attention_f64(q, kc, vc, table, [1, 1], kv_cast=True)
+    for b in range(2):
+        v0 = vc[table[b, 0], 0].to(q_dtype).double().numpy()
+        for h in range(4):
+            assert np.array_equal(out[b, 0, h], v0[h // 2])
+    uncast = dense.paged_attention_f64(q, kc, vc, table, [1, 1])
+    assert not np.array_equal(out, uncast)
+
+
+def test_dense_kv_cast_matches_sdpa_restatement():
+    """The float64 oracle with the cast against the SDPA restatement (which casts the
+    gathered rows itself, attention.py:240-241): a bf16 query over an fp32 cache."""
+    q, _, _, kc, vc, table, lens = scenario(8, 2, 64, [130, 77, 300], scatter=True, seed=12)
+    qb = q.to(torch.bfloat16)
+    a = paged_sdpa.paged_attention_sdpa(qb, kc, vc, table, lens).double().numpy()
+    b = dense.paged_attention_f64(qb, kc, vc, table, lens, kv_cast=True)
+    assert np.abs(a - b).max() / np.abs(b).max() < 2e-2
+    same = dense.paged_attention_f64(q, kc, vc, table, lens, kv_cast=True)
+    assert np.array_equal(same, dense.paged_attention_f64(q, kc, vc, table, lens))
