@@ -101,6 +101,31 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
                            float scale, int q_dtype, int kv_dtype, void* stream);
 
 /*
+ * msattn_paged_attention without the workspace arguments, for callers that cannot
+ * allocate (code under hipGraph capture that must not call hipMalloc, tight serving
+ * loops, harnesses that forbid allocation). No counterpart in the reference, whose
+ * launcher allocates its partials per call (kernels/paged_attn_triton.py:320-323).
+ * Same arguments, results and errors as msattn_paged_attention, with the same kernels;
+ * the split-K partials go to a scratch array of MSATTN_NOALLOC_SCRATCH_BYTES that the
+ * library holds on each device it runs on (allocated with the library's code object,
+ * kept until the process ends); its address is looked up on the first call on a device.
+ * A call whose msattn_workspace_bytes exceeds that size returns MSATTN_ERR_WORKSPACE
+ * (chunked prefill on the MFMA kernel needs no scratch and is not limited); it calls no
+ * allocator. Every call on one device shares that device's scratch: calls that overlap
+ * in time on one device (two streams, two threads) race and must be serialised by the
+ * caller. The scratch keeps the last call's contents; nothing in it needs clearing.
+ */
+#define MSATTN_NOALLOC_SCRATCH_BYTES (64u << 20)
+int msattn_paged_attention_noalloc(const void* query, const void* k_cache, const void* v_cache,
+                                   int64_t cache_block_stride, int64_t cache_slot_stride,
+                                   int64_t cache_head_stride, const int32_t* block_table,
+                                   const int32_t* context_lens, void* out, int batch, int q_len,
+                                   int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                   int num_blocks, int table_width, int max_context, int causal,
+                                   int window, float scale, int q_dtype, int kv_dtype,
+                                   void* stream);
+
+/*
  * msattn_paged_attention for decode (q_len == 1) with rotate-half RoPE applied to
  * the query inside the attention kernels: row b's query becomes
  * q * cos[p] + rotate_half(q) * sin[p], p = position[b] (clamped to

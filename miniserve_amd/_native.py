@@ -36,6 +36,10 @@ SIGNATURES = {
         c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_size,
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
         c_float, c_int, c_int, c_vp]),
+    "msattn_paged_attention_noalloc": (c_int, [
+        c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
+        c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+        c_float, c_int, c_int, c_vp]),
     "msattn_paged_attention_rope": (c_int, [
         c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_size,
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,

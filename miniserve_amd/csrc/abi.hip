@@ -4,6 +4,7 @@
 #include <cstdint>
 
 #include <atomic>
+#include <mutex>
 
 #include "decode_mfma.h"
 #include "decode_streamk.h"
@@ -475,22 +476,38 @@ int msattn_merge_partials(const void* workspace, size_t workspace_bytes,
                     num_kv_heads, head_dim, max_context, q_dtype, nullptr, nullptr, 0, -1, stream);
 }
 
-int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
-                           int64_t cache_block_stride, int64_t cache_slot_stride,
-                           int64_t cache_head_stride, const int32_t* block_table,
-                           const int32_t* context_lens, void* out, void* workspace,
-                           size_t workspace_bytes, int batch, int q_len, int num_heads,
-                           int num_kv_heads, int head_dim, int block_size, int num_blocks,
-                           int table_width, int max_context, int causal, int window,
-                           float scale, int q_dtype, int kv_dtype, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Chunked prefill (more than one 16-row tile of query rows per KV head) on the MFMA
+// prefill kernel, which writes the normalised output directly, four elements (8 bytes)
+// a store, and uses no workspace.
+bool direct_prefill_route(const void* query, const void* out, int64_t cache_slot_stride,
+                          int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                          int block_size, int q_dtype, int kv_dtype) {
+  return q_len > 1 &&
+         mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, cache_slot_stride) &&
+         aligned(out, 8) && batch <= 65535 && num_heads > 0 && num_kv_heads > 0 &&
+         num_heads % num_kv_heads == 0 &&
+         static_cast<int64_t>(q_len) * (num_heads / num_kv_heads) > 16;
+}
+
+// msattn_paged_attention's body. `prefill_needs_ws`: whether the direct prefill route
+// checks the workspace size too (the workspace entry point's contract), although that
+// route does not touch it.
+int attention_impl(const void* query, const void* k_cache, const void* v_cache,
+                   int64_t cache_block_stride, int64_t cache_slot_stride,
+                   int64_t cache_head_stride, const int32_t* block_table,
+                   const int32_t* context_lens, void* out, void* workspace,
+                   size_t workspace_bytes, int batch, int q_len, int num_heads,
+                   int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                   int table_width, int max_context, int causal, int window, float scale,
+                   int q_dtype, int kv_dtype, bool prefill_needs_ws, void* stream) {
   if (!out) return MSATTN_ERR_INVALID_ARG;
   if (!dtype_ok(q_dtype) || !aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
-  // Chunked prefill (more than one 16-row tile of query rows per KV head): the MFMA
-  // prefill kernel writes the normalised output directly, four elements (8 bytes) a store.
-  if (q_len > 1 && mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, cache_slot_stride) &&
-      aligned(out, 8) && batch <= 65535 && num_heads > 0 &&
-      num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
-      static_cast<int64_t>(q_len) * (num_heads / num_kv_heads) > 16) {
+  if (direct_prefill_route(query, out, cache_slot_stride, batch, q_len, num_heads, num_kv_heads,
+                           head_dim, block_size, q_dtype, kv_dtype)) {
     if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
     if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
       return MSATTN_ERR_INVALID_ARG;
@@ -500,7 +517,7 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
                                     table_width);
     if (rc != MSATTN_OK) return rc;
     const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
-    if (workspace_bytes < L.total()) return MSATTN_ERR_WORKSPACE;
+    if (prefill_needs_ws && workspace_bytes < L.total()) return MSATTN_ERR_WORKSPACE;
     PrefillParams pp{};
     pp.q = query;
     pp.k = k_cache;
@@ -546,6 +563,82 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
   if (rc != MSATTN_OK) return rc;
   return merge_impl(workspace, workspace_bytes, context_lens, out, batch, q_len, num_heads,
                     num_kv_heads, head_dim, max_context, q_dtype, nullptr, nullptr, 0, kind, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of msattn_paged_attention_noalloc: one fixed array per device, allocated with
+// the code object (no hipMalloc at call time) and held until the process ends. Host code
+// must not use the array's name as a device address: its address on each device comes
+// from hipGetSymbolAddress, looked up once per device on that device's first call.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = MSATTN_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (its address found on the first call).
+int current_scratch(void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MSATTN_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+      return MSATTN_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return MSATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
+                           int64_t cache_block_stride, int64_t cache_slot_stride,
+                           int64_t cache_head_stride, const int32_t* block_table,
+                           const int32_t* context_lens, void* out, void* workspace,
+                           size_t workspace_bytes, int batch, int q_len, int num_heads,
+                           int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                           int table_width, int max_context, int causal, int window,
+                           float scale, int q_dtype, int kv_dtype, void* stream) {
+  return attention_impl(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                        cache_head_stride, block_table, context_lens, out, workspace,
+                        workspace_bytes, batch, q_len, num_heads, num_kv_heads, head_dim,
+                        block_size, num_blocks, table_width, max_context, causal, window, scale,
+                        q_dtype, kv_dtype, true, stream);
+}
+
+int msattn_paged_attention_noalloc(const void* query, const void* k_cache, const void* v_cache,
+                                   int64_t cache_block_stride, int64_t cache_slot_stride,
+                                   int64_t cache_head_stride, const int32_t* block_table,
+                                   const int32_t* context_lens, void* out, int batch, int q_len,
+                                   int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                   int num_blocks, int table_width, int max_context, int causal,
+                                   int window, float scale, int q_dtype, int kv_dtype,
+                                   void* stream) {
+  // Every size check comes before the first HIP call.
+  if (!out || !dtype_ok(q_dtype) || q_dtype == MSATTN_FP8_E4M3) return MSATTN_ERR_INVALID_ARG;
+  if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
+    return MSATTN_ERR_INVALID_ARG;
+  const bool direct = direct_prefill_route(query, out, cache_slot_stride, batch, q_len,
+                                           num_heads, num_kv_heads, head_dim, block_size,
+                                           q_dtype, kv_dtype);
+  if (!direct) {
+    const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
+    if (L.total() > kScratchBytes) return MSATTN_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  const int rc = current_scratch(&ws);
+  if (rc != MSATTN_OK) return rc;
+  return attention_impl(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                        cache_head_stride, block_table, context_lens, out, ws, kScratchBytes,
+                        batch, q_len, num_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                        table_width, max_context, causal, window, scale, q_dtype, kv_dtype,
+                        false, stream);
 }
 
 int msattn_paged_attention_rope(const void* query, const void* k_cache, const void* v_cache,

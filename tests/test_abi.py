@@ -189,3 +189,24 @@ def test_stream_read_probe_rejects_bad_arguments():
     assert lib.msattn_probe_stream_read(256, (1 << 20) + 8, 256, None) == nat.ERR_INVALID_ARG
     assert lib.msattn_probe_stream_read(264, 1 << 20, 256, None) == nat.ERR_INVALID_ARG
     assert lib.msattn_probe_stream_read(256, 1 << 20, 258, None) == nat.ERR_INVALID_ARG
+
+
+def test_noalloc_entry_checks_before_any_hip_call():
+    """msattn_paged_attention_noalloc rejects bad arguments, and geometries whose
+    workspace exceeds its scratch (MSATTN_NOALLOC_SCRATCH_BYTES, 64 MiB), before it
+    looks up the scratch or launches anything."""
+    lib = nat.lib()
+    buf, args = _attn_args()
+    a = args[:9] + args[11:]  # drop workspace and workspace_bytes
+    bad_out = list(a)
+    bad_out[8] = None
+    assert lib.msattn_paged_attention_noalloc(*bad_out) == nat.ERR_INVALID_ARG
+    bad_geom = list(a)
+    bad_geom[11:13] = [6, 4]  # H % KVH != 0
+    assert lib.msattn_paged_attention_noalloc(*bad_geom) == nat.ERR_INVALID_ARG
+    big = list(a)
+    # batch 512, H32/KVH8/D128, 16k context: a 276 MB workspace
+    big[9], big[11], big[12], big[13], big[16], big[17] = 512, 32, 8, 128, 1024, 16384
+    big[-3] = big[-2] = nat.BF16
+    assert lib.msattn_workspace_bytes(512, 1, 32, 8, 128, 16384) > 64 << 20
+    assert lib.msattn_paged_attention_noalloc(*big) == nat.ERR_WORKSPACE
