@@ -86,10 +86,14 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
  * kernel, which addresses with 64-bit offsets.
  * max_context bounds context_lens (entries above it are clamped to it) and
  * sizes the launch grid; pass table_width * block_size for a capture-safe call.
- * window <= 0 means no sliding window. Runs msattn_paged_attention_partials
- * followed by msattn_merge_partials, except for chunked prefill on the MFMA kernel
- * (bf16/fp16 query, cache of its type or fp8 e4m3, head_dim 64 or 128, more than 16
- * query rows per KV head), which writes the output directly.
+ * window <= 0 means no sliding window. q_dtype and kv_dtype may differ: the cache is
+ * cast to the query type as it is read (exact when widening, round to nearest even when
+ * narrowing), as the reference casts the gathered K/V to query.dtype
+ * (miniserve/attention.py:240-241). Runs msattn_paged_attention_partials followed by
+ * msattn_merge_partials, except for chunked prefill on the MFMA kernel (bf16/fp16 query
+ * 16-byte aligned, output 8-byte aligned, cache of the query's type, fp8 e4m3 or fp32,
+ * head_dim 64 or 128, more than 16 query rows per KV head), which writes the output
+ * directly.
  */
 int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
                            int64_t cache_block_stride, int64_t cache_slot_stride,
