@@ -281,13 +281,26 @@ def main():
 
     read_ceiling = stream_read_gbs(dev)
 
-    traffic = None
-    tfile = PROFILES / f"traffic_{w.name}{'' if args.kv_dtype == 'same' else '-' + args.kv_dtype}.json"
+    # HBM traffic per launch of the dominant kernel comes from rocprofv3 counter runs
+    # (FETCH_SIZE, WRITE_SIZE) recorded in profiles/; it is reported only when that record
+    # was taken on the library this run loaded (same sha256), else null with the reason.
+    traffic, traffic_note = None, None
+    tname = f"traffic_{w.name}{'' if args.kv_dtype == 'same' else '-' + args.kv_dtype}.json"
+    tfile = PROFILES / tname
+    lib_sha = library_sha256()
     if tfile.exists():
         try:
-            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+            rec = json.loads(tfile.read_text())
         except (ValueError, OSError):
-            traffic = None
+            rec = {}
+        if rec.get("library_sha256") == lib_sha:
+            traffic = rec.get("hbm_bytes_per_launch")
+            traffic_note = f"profiles/{tname}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this library"
+        else:
+            traffic_note = (f"profiles/{tname} was measured on library "
+                            f"{rec.get('library_sha256')}, not on this one ({lib_sha})")
+    else:
+        traffic_note = f"no profiles/{tname} for this workload"
 
     result = {
         "metric": METRIC,
@@ -323,6 +336,8 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_note,
+            "library_sha256": lib_sha,
             "kernel_avg_us": round(split_avg * 1e3, 2),
             "kernel_median_us": round(split_ms[len(split_ms) // 2] * 1e3, 2),
             "merge_avg_us": round(merge_avg * 1e3, 2),
@@ -398,6 +413,28 @@ def prefill_bench(args):
     }), flush=True)
 
 
+def library_sha256() -> str:
+    """First 16 hex digits of the sha256 of the libmsattn.so this run loads."""
+    import hashlib
+
+    from miniserve_amd import _native as nat
+
+    return hashlib.sha256(nat.LIB_PATH.read_bytes()).hexdigest()[:16]
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo, what lscpu reports as 'Model name')."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(w, target_s: float):
     """The reference's CPU path (oracle restatement of attention.py:205-250, torch SDPA)
     on a bounded sample of the same batch: the first rows whose contexts sum to a share
@@ -440,6 +477,7 @@ def cpu_baseline(w, target_s: float):
         "sample": f"rows 0..{n_rows - 1} of {w.name} ({tokens} of {full_tokens} context tokens), "
                   f"median of 5 runs of the oracle's SDPA restatement in {str(w.dtype)[6:]}",
         "us_per_layer_extrapolated": round(med * 1e6 * full_tokens / tokens, 1),
+        "cpu_model": cpu_model(),
         "torch": torch.__version__,
     }
 

@@ -33,8 +33,11 @@ constexpr int kMergeBatch = MSATTN_MERGE_BATCH;  // acc rows loaded together
 #endif
 constexpr int kMergePrefixBatch = MSATTN_MERGE_PREFIX_BATCH;
 
-template <typename QT>
+// DPL: dims per lane (head_dim <= 64 * DPL), so the acc rows in flight take only the
+// registers the head size needs.
+template <typename QT, int DPL>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams p) {
+  constexpr int kMergeMaxDims = DPL;
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kMergeWaves + w;
@@ -173,11 +176,18 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
   }
 }
 
+template <typename QT, int DPL>
+static hipError_t launch_merge_d(const MergeParams& p, hipStream_t stream) {
+  const unsigned blocks = static_cast<unsigned>((p.rows + kMergeWaves - 1) / kMergeWaves);
+  hipLaunchKernelGGL((merge_kernel<QT, DPL>), dim3(blocks), dim3(kMergeThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <typename QT>
 static hipError_t launch_merge_t(const MergeParams& p, hipStream_t stream) {
-  const unsigned blocks = static_cast<unsigned>((p.rows + kMergeWaves - 1) / kMergeWaves);
-  hipLaunchKernelGGL(merge_kernel<QT>, dim3(blocks), dim3(kMergeThreads), 0, stream, p);
-  return hipGetLastError();
+  if (p.D <= kWave) return launch_merge_d<QT, 1>(p, stream);
+  if (p.D <= 2 * kWave) return launch_merge_d<QT, 2>(p, stream);
+  return launch_merge_d<QT, kMergeMaxDims>(p, stream);
 }
 
 hipError_t launch_merge(const MergeParams& p, int q_dtype, hipStream_t stream, bool* supported) {

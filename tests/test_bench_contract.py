@@ -43,3 +43,9 @@ def test_cpu_baseline_object():
     assert set(r) >= {"value", "unit", "cores", "kind", "sample"}
     assert r["kind"] == "port" and r["unit"] == "GB/s" and r["value"] > 0
     assert r["cores"] >= 1 and "C1" in r["sample"]
+    assert r["cpu_model"] and r["cpu_model"] != "unknown"
+
+
+def test_library_hash_names_the_loaded_library():
+    h = bench.library_sha256()
+    assert len(h) == 16 and int(h, 16) >= 0
