@@ -246,7 +246,8 @@ int msattn_gather_kv(const void* cache, int64_t cache_block_stride, int64_t cach
 /*
  * Measurement helper, with no counterpart in the reference: one launch of a plain
  * streaming-read kernel over `bytes` (a multiple of 16) of device memory at `buf`
- * (16-byte aligned), each workgroup reading a contiguous 64 KiB chunk. Timing it
+ * (16-byte aligned), each workgroup reading a contiguous 64 KiB chunk with nontemporal
+ * 16-byte loads. Timing it
  * gives the HBM read rate a plain kernel reaches on the device, beside which the
  * decode kernels' rates are reported. `sink` is device memory of
  * ceil(bytes / 65536) uint32 entries that the kernel may write (it keeps the loads
