@@ -37,10 +37,14 @@
 #ifndef MSATTN_PF_RB
 #define MSATTN_PF_RB 2
 #endif
-// P.V ordering: 0 = all softmax first, V operands shared (measured faster); 1 = row
-// block by row block, the next block's softmax overlapping the previous one's MFMAs.
-#ifndef MSATTN_PF_INTERLEAVE
-#define MSATTN_PF_INTERLEAVE 0
+// K/V of a cache of the query's type copied into LDS by the load unit (1), or staged
+// through registers like the converted caches (0).
+#ifndef MSATTN_PF_DMA
+#define MSATTN_PF_DMA 1
+#endif
+// Interleaving of MFMA and VALU work requested from the scheduler on the copy path.
+#ifndef MSATTN_PF_SCHED
+#define MSATTN_PF_SCHED 1
 #endif
 
 namespace msattn {
@@ -66,10 +70,54 @@ constexpr int kXcds = 8;
 #ifndef MSATTN_PF_PRIO
 #define MSATTN_PF_PRIO 1
 #endif
-constexpr float kPfRescaleSlack = 8.0f;         // base-2 headroom before the max moves
+constexpr float kPfRescaleSlack = 8.0f;
+// s_waitcnt immediate (gfx9 encoding) waiting for every vector memory operation only.
+constexpr int kWaitVm0 = 0x0F70;         // base-2 headroom before the max moves
 
 typedef short pf_s4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) pf_s4 lds_s4;  // an LDS pointer target
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) uint4 lds_u4;
+
+// Chunk swizzle of the copied K/V rows (16-byte chunk c of token row r stored at chunk
+// position c ^ pf_swz(r); depends on r % 16 only). head_dim 128 (16 chunks per row): the
+// 16 rows of a K operand read get 16 distinct positions, and the 8 rows of a transposed V
+// read (tokens 8k .. 8k + 7, one 32-byte chunk pair each) 8 distinct pairs. head_dim 64
+// (8 chunks, two rows per 64 banks): the same within each row parity.
+// A use of v's registers at this point of the program (no instruction): values computed
+// before it stay before it.
+__device__ __forceinline__ void keep_here(const uint4& v) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the constraint names a GPU register class
+  asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+#endif
+}
+
+// Instruction order asked of the scheduler for a half-step block of the copy path: NM
+// MFMAs, each followed by NV VALU instructions (the other half-step's softmax), the LDS
+// reads of the MFMA operands free to move. Group masks: 0x008 MFMA, 0x002 VALU.
+template <int NM, int NV>
+__device__ __forceinline__ void pf_sched_half() {
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+  }
+}
+
+// One copy instruction: lane l's 16 bytes at buffer offset voff land at LDS dst + 16 l
+// bytes (buffer_load_dwordx4 ... lds; the LDS address is wave-uniform).
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, uint16_t* dst, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass of this file drops kernels that use it
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, voff, 0, 0, 0);
+#endif
+}
+
+template <int D>
+__device__ __forceinline__ int pf_swz(int r) {
+  if constexpr (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  const int x = (r >> 1) & 7;
+  return ((x & 3) << 1) | (x >> 2);
+}
 
 struct PrefillParams {
   const void* q;
@@ -100,23 +148,29 @@ struct PrefillParams {
 
 template <typename T, typename KT, int D, int RB, bool PX>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillParams p) {
-  typedef Kv8<T, KT> KV;  // a cache of T, or fp8 e4m3 widened to T while staged into LDS
+  typedef Kv8<T, KT> KV;  // a cache of T, or of fp8 e4m3 / fp32 converted to T in registers
   typedef typename KV::raw_t raw_t;
   constexpr int EB = static_cast<int>(sizeof(KT));
   static_assert(D == 64 || D == 128, "prefill MFMA kernel handles head_dim 64 and 128");
+  static_assert(RB == 1 || RB == 2, "one or two 16-row blocks per wave");
+  // A cache of the query's type is copied into LDS by the load unit; other caches pass
+  // through registers, where they are converted.
+  constexpr bool DMA = MSATTN_PF_DMA && std::is_same<T, KT>::value;
   constexpr int JD = D / 32;              // k-steps of S^T
   constexpr int ND = D / 16;              // 16-dim tiles of O^T
-  constexpr int RSK = D + 8;              // K LDS row stride (elements): 68 / 36 dwords
-  constexpr int RSV = D + 16;             // V LDS row stride (elements): 72 / 40 dwords
-  constexpr int CPR = D * 2 / 16;         // 16-byte chunks per K/V row
-  constexpr int LPT = kPfStep * CPR / kPfGroupThreads;  // chunks per thread per tensor per step
-  static_assert(LPT * kPfGroupThreads == kPfStep * CPR, "staging split");
+  // LDS row strides (elements): unpadded, swizzled rows for the copies; padded rows for
+  // register staging (K: 68 / 36 dwords, V: 72 / 40 dwords).
+  constexpr int RSK = DMA ? D : D + 8;
+  constexpr int RSV = DMA ? D : D + 16;
   constexpr int WROWS = 16 * RB;          // query rows per wave
   constexpr int BROWS = WROWS * kPfWaves; // query rows per workgroup
 
-  // [key group][buffer][token row]
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[kPfGroups][2][kPfStep * RSK];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[kPfGroups][2][kPfStep * RSV];
+  // One array per buffer slot, [key group][token row * stride]: the compiler then sees
+  // that a copy into one slot does not write the slots being read.
+  __shared__ __attribute__((aligned(256))) uint16_t s_k0[kPfGroups][kPfStep * RSK];
+  __shared__ __attribute__((aligned(256))) uint16_t s_k1[kPfGroups][kPfStep * RSK];
+  __shared__ __attribute__((aligned(256))) uint16_t s_v0[kPfGroups][kPfStep * RSV];
+  __shared__ __attribute__((aligned(256))) uint16_t s_v1[kPfGroups][kPfStep * RSV];
   __shared__ int s_pg[kPfPageChunk];
 
   const int tid = threadIdx.x;
@@ -124,10 +178,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int wg = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int grp = wg / kPfWaves;  // key group: steps step_first + grp, + 2, ...
   const int w = wg - grp * kPfWaves;  // wave within the group: its query rows
-  const int gtid = tid - grp * kPfGroupThreads;
   const int g = lane >> 4;
   const int n = lane & 15;
-
   // Task = (sequence, KV head) pair-major, then row block; larger (later) row blocks
   // first: they see the most keys under a causal mask.
   unsigned bx = blockIdx.x;
@@ -164,14 +216,19 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   // This lane's query rows (MFMA column n of each of the wave's row blocks).
   bool row_ok[RB];
   int lo_n[RB], hi_n[RB];
-  int64_t orow[RB];
+  // Index of row block rb's query row in the [tokens, heads] query / output arrays
+  // (recomputed where needed rather than held through the key loop).
+  auto out_row = [&](int rb) {
+    const int row = row0 + w * WROWS + rb * 16 + n;
+    const int i = row / p.G;
+    return (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
+  };
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = row0 + w * WROWS + rb * 16 + n;
     row_ok[rb] = row < p.rows_per_kvh;
     lo_n[rb] = 0;
     hi_n[rb] = 0;
-    orow[rb] = 0;
     if (row_ok[rb]) {
       const int i = row / p.G;
       const int qpos = ctx - p.q_len + i;
@@ -183,7 +240,6 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
         lo_n[rb] = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
       }
       if (hi_n[rb] < lo_n[rb]) hi_n[rb] = lo_n[rb];
-      orow[rb] = (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
     }
   }
   // Keys every row of this wave sees: [wave_lo, wave_hi) (rows grow with the query).
@@ -215,7 +271,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 #pragma unroll
       for (int j = 0; j < JD; ++j) {
         qb[rb][j] = make_uint4(0u, 0u, 0u, 0u);
-        if (row_ok[rb]) qb[rb][j] = *reinterpret_cast<const uint4*>(qp + orow[rb] * D + 32 * j + 8 * g);
+        if (row_ok[rb]) qb[rb][j] = *reinterpret_cast<const uint4*>(qp + out_row(rb) * D + 32 * j + 8 * g);
       }
   }
 
@@ -234,20 +290,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int step_first = hi_all > lo_all ? lo_all / kPfStep : 0;
   const int step_end = hi_all > lo_all ? ceil_div(hi_all, kPfStep) : 0;
 
-  // Staging: a group's thread gtid loads chunk st_c of token rows st_r + ROWS_PER_PASS * j
-  // of the group's steps. A pass covers ROWS_PER_PASS / 16 tiles of 16 tokens (1 for
-  // head_dim 128, 2 for 64); a wave's rows lie in one of them, tile st_tile of the pass.
-  const int st_c = gtid % CPR;
-  const int st_r = gtid / CPR;
-  constexpr int ROWS_PER_PASS = kPfGroupThreads / CPR;
-  static_assert(ROWS_PER_PASS % 16 == 0 && kWave / CPR <= 16, "a wave's rows in one tile");
-  const int st_tile = ROWS_PER_PASS > 16 ? __builtin_amdgcn_readfirstlane(st_r / 16) : 0;
-  const int st_row = st_r % 16;
-  raw_t kst[LPT], vst[LPT];
-#pragma unroll
-  for (int j = 0; j < LPT; ++j) kst[j] = vst[j] = KV::keep_if(raw_t{}, false);
   int pg_base = -(1 << 30);  // s_pg[i] = physical page of logical page pg_base + i
-
   auto page_of = [&](int tok) { return p.bs_shift >= 0 ? tok >> p.bs_shift : tok / p.bs; };
   // Make s_pg cover the pages of steps [s_lo, s_hi]: called by every thread (it may
   // hold barriers); reloads the window from the first page of s_lo when needed.
@@ -269,238 +312,414 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       __syncthreads();
     }
   };
-  // A step's row j * 16 + r is row r of its 16-token tile j; block_size % 16 == 0 puts a
-  // tile in one page, so the page lookup and the tile's base offset are the same for
-  // every lane (scalar), and a lane only adds its constant in-tile offset. Each tile is
-  // read through a buffer descriptor whose size ends at the last row below hi_all (rows
-  // past it, and tiles that are holes, read as zeros).
-  const uint32_t st_off = static_cast<uint32_t>((st_row * p.slot_stride + st_c * 8) * EB);
   const int64_t row_bytes = p.slot_stride * EB;
-  // The page ids of a step's tiles are read from the window ahead of the loads (plan),
-  // so the LDS latency of the lookups is not paid in front of each tile's loads.
-  auto plan = [&](int step, int (&phys)[LPT]) {
-#pragma unroll
-    for (int j = 0; j < LPT; ++j)
-      phys[j] = s_pg[page_of(step * kPfStep + ROWS_PER_PASS * j + 16 * st_tile) - pg_base];
-  };
-  auto issue = [&](int step, const int (&phys_planned)[LPT]) {
-#pragma unroll
-    for (int j = 0; j < LPT; ++j) {
-      const int t0 = step * kPfStep + ROWS_PER_PASS * j + 16 * st_tile;  // the wave's tile
-      const int pg = page_of(t0);
-      const int phys = __builtin_amdgcn_readfirstlane(phys_planned[j]);
-      const int rows_valid = min(16, hi_all - t0);
-      const bool tile_in = phys >= 0 && rows_valid > 0 && t0 + 16 > lo_all;
-      const int64_t tbase = tile_in ? static_cast<int64_t>(phys) * p.blk_stride +
-                                          static_cast<int64_t>(t0 - pg * p.bs) * p.slot_stride +
-                                          static_cast<int64_t>(kvh) * p.head_stride
-                                    : 0;
-      const int nbytes = tile_in ? static_cast<int>((rows_valid - 1) * row_bytes + D * EB) : 0;
-      kst[j] = KV::template load<0>(tile_rsrc(kbase + tbase, nbytes), st_off);
-      vst[j] = KV::template load<0>(tile_rsrc(vbase + tbase, nbytes), st_off);
-      if (t0 < lo_all) {  // a window's first tile: rows below it are zeros too
-        const bool keep = t0 + st_row >= lo_all;
-        kst[j] = KV::keep_if(kst[j], keep);
-        vst[j] = KV::keep_if(vst[j], keep);
-      }
-    }
-  };
-  auto stage = [&](int buf) {  // the registers loaded by issue() into LDS buffer `buf`
-#pragma unroll
-    for (int j = 0; j < LPT; ++j) {
-      const int r = st_r + ROWS_PER_PASS * j;
-      *reinterpret_cast<uint4*>(&s_k[grp][buf][r * RSK + st_c * 8]) = KV::operand(kst[j]);
-      *reinterpret_cast<uint4*>(&s_v[grp][buf][r * RSV + st_c * 8]) = KV::operand(vst[j]);
-    }
-  };
 
-  // Transposed-read coordinates: lane s of a 16-lane group names 4 dims (4 * (s & 3) ..)
-  // of token (s >> 2) + base; lane i then receives dim i of those four tokens.
-  const int tr_tok = lane >> 2 & 3;
-  const int tr_dim = 4 * (lane & 3);
-
-  auto compute = [&](int step, int buf) {
+  // ---- one step's arithmetic, shared by both staging schemes ----
+  // Keys of a step all visible to every row of the wave: no per-key mask.
+  auto step_full = [&](int step) {
     const int t_base = step * kPfStep;
-    // Keys of this step all visible to every row of the wave: no per-key mask.
-    const bool full = t_base >= wave_lo && t_base + kPfStep <= wave_hi;
-    // ---- S^T for the wave's row blocks: 4 slices of 16 tokens each ----
-    mf_f32x4 sv[RB][4];
+    return t_base >= wave_lo && t_base + kPfStep <= wave_hi;
+  };
+  // S^T of a step for the wave's row blocks, slices sl0 .. sl0 + NS - 1 of 16 tokens;
+  // ka_of(sl, j) reads the K operand of slice sl, k-step j (key row 16 sl + n, dims
+  // 32 j + 8 g ..).
+  auto scores = [&](auto&& ka_of, mf_f32x4 (&sv)[RB][4], auto sl0_c, auto ns_c) {
+    constexpr int SL0 = decltype(sl0_c)::value;
+    constexpr int NS = decltype(ns_c)::value;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int sl = 0; sl < 4; ++sl) sv[rb][sl] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(1);
+      for (int sl = SL0; sl < SL0 + NS; ++sl) sv[rb][sl] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < JD; ++j) {
-      uint4 ka[4];
+      uint4 ka[NS];
+#pragma unroll
+      for (int u = 0; u < NS; ++u) ka[u] = ka_of(SL0 + u, j);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int u = 0; u < NS; ++u)
+          sv[rb][SL0 + u] = Mfma16<T>::mac(ka[u], qb[rb][j], sv[rb][SL0 + u]);
+    }
+  };
+  // Keys outside a row's range score -inf (steps that cross some row's range); slices
+  // sl0 .. sl0 + ns - 1.
+  auto mask_scores = [&](int step, mf_f32x4 (&sv)[RB][4], int sl0, int ns) {
+    const int t_base = step * kPfStep;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int sl = 0; sl < 4; ++sl)
-        ka[sl] = *reinterpret_cast<const uint4*>(&s_k[grp][buf][(16 * sl + n) * RSK + 32 * j + 8 * g]);
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int sl = 0; sl < 4; ++sl) sv[rb][sl] = Mfma16<T>::mac(ka[sl], qb[rb][j], sv[rb][sl]);
-    }
-    if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(0);
-
-    // ---- online softmax of one row block; P^T packed as the B operand ----
-    // The row max is taken on raw scores (scale_log2 > 0 keeps the order), the weights
-    // are exp2(s * scale_log2 - m). The running max m only moves when a row's max
-    // exceeds it by more than kPfRescaleSlack (base-2 units): the weights then stay
-    // below 2^kPfRescaleSlack, which fp32 sums and the bf16/fp16 P operand hold, and the
-    // accumulator rescale is skipped on most steps. The normalisation by l is exact
-    // whatever reference max the sums share.
-    uint4 pb[RB][2];
-    float alpha[RB];
-    auto softmax = [&](int rb) {
-      float sc[4][4];
-      float mt = -INFINITY;
-#pragma unroll
-      for (int sl = 0; sl < 4; ++sl) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sc[sl][r] = sv[rb][sl][r];
-        if (!full) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tok = t_base + 16 * sl + 4 * g + r;
-            sc[sl][r] = (tok >= lo_n[rb] && tok < hi_n[rb]) ? sc[sl][r] : -INFINITY;
-          }
+        for (int r = 0; r < 4; ++r) {
+          if (sl < sl0 || sl >= sl0 + ns) continue;
+          const int tok = t_base + 16 * sl + 4 * g + r;
+          sv[rb][sl][r] = (tok >= lo_n[rb] && tok < hi_n[rb]) ? sv[rb][sl][r] : -INFINITY;
         }
+  };
+  // Online softmax of one row block over one half-step (32 keys, slices 2 ks, 2 ks + 1),
+  // in two parts: softmax_max, then softmax_exp. The row max is taken on raw scores
+  // (scale_log2 > 0 keeps the order), the weights are exp2(s * scale_log2 - m). The
+  // running max m only moves when a row's max exceeds it by more than kPfRescaleSlack
+  // (base-2 units): the weights then stay below 2^kPfRescaleSlack, which fp32 sums and
+  // the bf16/fp16 P operand hold, and the accumulator rescale is skipped on most
+  // half-steps. The normalisation by l is exact whatever reference max the sums share.
+  uint4 pb[RB][2];
+  float alpha[RB];
+  // Part 1: the half-step's row max moves m (or not); alpha = exp2(m_old - m_new)
+  // (exactly 1 when m stays) rescales l.
+  auto softmax_max = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) {
+    float mt = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sc[sl][r]);
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sv[rb][2 * ks + h][r]);
+    mt = rows4_max(mt);
+    mt *= p.scale_log2;  // the row max, base-2 units
+    const float m_new = mt > m_run[rb] + kPfRescaleSlack ? mt : m_run[rb];
+    alpha[rb] = m_new != -INFINITY ? __builtin_amdgcn_exp2f(m_run[rb] - m_new) : 1.0f;
+    l_run[rb] *= alpha[rb];
+    m_run[rb] = m_new;
+  };
+  // Part 2: the weights, P^T packed as the B operand of half ks, l += their sum. A row
+  // with no key yet (m = -inf) has only -inf scores: any finite reference gives zeros.
+  auto softmax_exp = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) {
+    const float m_use = m_run[rb] != -INFINITY ? m_run[rb] : 0.0f;
+    float pr[8];
+    float psum = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = __builtin_amdgcn_exp2f(fmaf(sv[rb][2 * ks + h][r], p.scale_log2, -m_use));
+        pr[4 * h + r] = x;
+        psum += x;
       }
-      mt = rows4_max(mt);
-      mt *= p.scale_log2;  // the step's row max, base-2 units
-      const float m_new = mt > m_run[rb] + kPfRescaleSlack ? mt : m_run[rb];
-      const bool live = m_new != -INFINITY;
-      alpha[rb] = live ? __builtin_amdgcn_exp2f(m_run[rb] - m_new) : 1.0f;
-      // A row with no key yet has only -inf scores: any finite reference gives zeros.
-      const float m_use = live ? m_new : 0.0f;
-      float psum = 0.0f;
+    pb[rb][ks] = make_uint4(Pack2<T>::pack(pr[0], pr[1]), Pack2<T>::pack(pr[2], pr[3]),
+                            Pack2<T>::pack(pr[4], pr[5]), Pack2<T>::pack(pr[6], pr[7]));
+    l_run[rb] += psum;
+  };
+  // alpha is exactly 1 for rows whose reference max did not move: most steps skip this
+  auto rescale = [&](int rb) {
+    if (__builtin_expect(__any(alpha[rb] != 1.0f), 0)) {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        float pr[8];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float x = __builtin_amdgcn_exp2f(fmaf(sc[2 * ks + h][r], p.scale_log2, -m_use));
-            pr[4 * h + r] = x;
-            psum += x;
-          }
-        pb[rb][ks] = make_uint4(Pack2<T>::pack(pr[0], pr[1]), Pack2<T>::pack(pr[2], pr[3]),
-                                Pack2<T>::pack(pr[4], pr[5]), Pack2<T>::pack(pr[6], pr[7]));
-      }
-      l_run[rb] = fmaf(l_run[rb], alpha[rb], psum);
-      m_run[rb] = m_new;
-    };
-    // alpha is exactly 1 for rows whose reference max did not move: most steps skip this
-    auto rescale = [&](int rb) {
-      if (__builtin_expect(__any(alpha[rb] != 1.0f), 0)) {
-#pragma unroll
-        for (int t = 0; t < ND; ++t) acc[rb][t] *= alpha[rb];
-      }
-    };
-    // ---- O^T += V^T P^T: A = V^T via transposed LDS reads ----
-    auto v_operands = [&](int ks, uint4 (&va)[ND]) {
-      const int tok0 = 32 * ks + 4 * g + tr_tok;        // e = 0..3: slice 2ks
-      const int tok1 = 32 * ks + 16 + 4 * g + tr_tok;   // e = 4..7: slice 2ks + 1
-#pragma unroll
-      for (int t = 0; t < ND; ++t) {
-        const pf_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s4*)(&s_v[grp][buf][tok0 * RSV + 16 * t + tr_dim]));
-        const pf_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s4*)(&s_v[grp][buf][tok1 * RSV + 16 * t + tr_dim]));
-        const uint2 lo2 = __builtin_bit_cast(uint2, lo);
-        const uint2 hi2 = __builtin_bit_cast(uint2, hi);
-        va[t] = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
-      }
-    };
-#if MSATTN_PF_INTERLEAVE
-    // Row block by row block: block rb's P.V MFMAs run while block rb + 1's softmax
-    // is computed; each block reads the V operands itself.
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      softmax(rb);
-      rescale(rb);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        uint4 va[ND];
-        v_operands(ks, va);
-#pragma unroll
-        for (int t = 0; t < ND; ++t) acc[rb][t] = Mfma16<T>::mac(va[t], pb[rb][ks], acc[rb][t]);
-      }
+      for (int t = 0; t < ND; ++t) acc[rb][t] *= alpha[rb];
     }
-#else
-    // All row blocks' softmax first, then P.V with each V operand read once.
+  };
+  // O^T += V^T P^T over half-step ks; va_of(ks, t) reads the A operand V^T (dims 16 t ..,
+  // tokens 32 ks ..).
+  auto pv = [&](auto&& va_of, int ks) {
+    uint4 va[ND];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) softmax(rb);
+    for (int t = 0; t < ND; ++t) va[t] = va_of(ks, t);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) rescale(rb);
-    if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(1);
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      uint4 va[ND];
-      v_operands(ks, va);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int t = 0; t < ND; ++t) acc[rb][t] = Mfma16<T>::mac(va[t], pb[rb][ks], acc[rb][t]);
-    }
-    if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(0);
-#endif
+      for (int t = 0; t < ND; ++t) acc[rb][t] = Mfma16<T>::mac(va[t], pb[rb][ks], acc[rb][t]);
+  };
+  // Transposed reads: lane s of a 16-lane group names 4 dims of one token (tokens
+  // base + (s >> 2), dims 4 * (s & 3) ..); lane i then receives dim i of those four
+  // tokens. lo covers tokens 4 g .. 4 g + 3 of the 32-token half, hi the same 16 later.
+  const int tr_tok = lane >> 2 & 3;
+  auto tr_pair = [&](uint16_t* lo, uint16_t* hi) {
+    const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)lo));
+    const uint2 c = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)hi));
+    return make_uint4(a.x, a.y, c.x, c.y);
   };
 
-  // Group grp takes steps step_first + grp + 2i (i = 0, 1, ...) from its own pair of
-  // buffers; both groups meet at one barrier per pair of steps.
-  const int s_first = step_first + grp;
-  if (step_first < step_end) {
-    ensure_pages(step_first, min(step_first + 3, step_end - 1));
-    int ph[LPT];
-    if (s_first < step_end) {
-      plan(s_first, ph);
-      issue(s_first, ph);
+  if constexpr (DMA) {
+    // ---- K and V copied into LDS by the load unit (buffer_load ... lds) ----
+    // Wave w of a group copies token rows 16 w .. 16 w + 15 of a step, K and V, each
+    // instruction 1 KiB: lane l writes LDS bytes 16 l .. of the instruction's block. Rows
+    // are unpadded; the 16-byte chunk c of token row r sits at position c ^ pf_swz(r), so a
+    // lane reads global chunk (l % chunks per row) ^ pf_swz(row). K operand reads (16 rows,
+    // one chunk each) and the transposed V reads (8 rows, 32 bytes each) then fall on
+    // distinct banks. Tokens past hi_all, below a window's first key, or on a page the table
+    // does not map lie outside the tile's descriptor: their copies write zeros.
+    constexpr int CPRD = D / 8;        // 16-byte chunks per row
+    constexpr int RPI = kWave / CPRD;  // rows per copy instruction (4 or 8)
+    constexpr int NI = 16 / RPI;       // copy instructions per 16-row tile
+    // Lane byte offsets of the reads, as one base XORed with a constant per k-step / dim
+    // tile: K chunk (4 j + g) ^ s = 4 (j ^ (s >> 2)) + (g ^ (s & 3)) puts j in bits 6-7 of
+    // the offset, V chunk pair (2 t + h) ^ s in bits 5-7, bits the row and lane terms leave
+    // zero (slots are 256-byte aligned), so no register per j or t is held.
+    const int swz_n = pf_swz<D>(n);
+    const uint32_t kx = static_cast<uint32_t>(n * 2 * D + 16 * (g ^ (swz_n & 3)) + 64 * (swz_n >> 2));
+    const int vrow = 4 * g + tr_tok;
+    const int swz_v = pf_swz<D>(vrow);
+    const uint32_t vx = static_cast<uint32_t>(vrow * 2 * D + 16 * ((lane >> 1 & 1) ^ (swz_v & 1)) +
+                                              32 * (swz_v >> 1) + 8 * (lane & 1));
+    uint32_t dvo[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int lr = RPI * j + lane / CPRD;
+      dvo[j] = static_cast<uint32_t>(lr * row_bytes + 16 * ((lane % CPRD) ^ pf_swz<D>(lr)));
     }
-    stage(0);
-    if (s_first + 2 < step_end) {
-      plan(s_first + 2, ph);
-      issue(s_first + 2, ph);
+    // Copy this wave's 16-row tile of a step of K or V into the LDS slot dst.
+    auto dma_tile = [&](int step, const KT* src, uint16_t* dst) {
+      const int t0 = step * kPfStep + 16 * w;
+      const int pg = page_of(t0);
+      const int phys = __builtin_amdgcn_readfirstlane(s_pg[pg - pg_base]);
+      const int rows_valid = min(16, hi_all - t0);
+      const bool tile_in = phys >= 0 && rows_valid > 0 && t0 + 16 > lo_all;
+      const int skip = tile_in && t0 < lo_all ? lo_all - t0 : 0;  // rows below the window
+      const int64_t tbase = tile_in ? static_cast<int64_t>(phys) * p.blk_stride +
+                                          static_cast<int64_t>(t0 - pg * p.bs + skip) * p.slot_stride +
+                                          static_cast<int64_t>(kvh) * p.head_stride
+                                    : 0;
+      const int nbytes = tile_in ? static_cast<int>((rows_valid - 1 - skip) * row_bytes + D * EB) : 0;
+      const __amdgpu_buffer_rsrc_t r = tile_rsrc(src + tbase, nbytes);
+      const uint32_t sk = static_cast<uint32_t>(skip * row_bytes);  // rows below wrap out of range
+#pragma unroll
+      for (int j = 0; j < NI; ++j) lds_copy16(r, dst + (16 * w + RPI * j) * D, dvo[j] - sk);
+    };
+    uint16_t* const k0 = &s_k0[grp][0];
+    uint16_t* const k1 = &s_k1[grp][0];
+    uint16_t* const v0 = &s_v0[grp][0];
+    uint16_t* const v1 = &s_v1[grp][0];
+    // Reads address the slot arrays themselves (so the compiler can tell a read of one
+    // slot from a copy into another); each slot is 256-byte aligned.
+    static_assert(sizeof(s_k0[0]) % 256 == 0 && sizeof(s_v0[0]) % 256 == 0, "slot alignment");
+    auto k_from = [&](uint16_t* buf) {
+      return [&, buf](int sl, int j) {
+        const uint32_t a = (kx ^ static_cast<uint32_t>(64 * j)) + static_cast<uint32_t>(32 * sl * D);
+        return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(buf) + a);
+      };
+    };
+    auto v_from = [&](uint16_t* buf) {
+      return [&, buf](int ks, int t) {
+        const uint32_t a = (vx ^ static_cast<uint32_t>(32 * t)) + static_cast<uint32_t>(64 * ks * D);
+        char* lo = reinterpret_cast<char*>(buf) + a;
+        return tr_pair(reinterpret_cast<uint16_t*>(lo), reinterpret_cast<uint16_t*>(lo + 32 * D));
+      };
+    };
+
+    // Group grp takes steps s_first + 2 i from slots k(i & 1), v(i & 1); iteration i
+    // copies the group's next step into the other slots while it computes step i in
+    // half-steps of 32 keys, pairing independent MFMA and VALU work of the wave:
+    //   scores of keys 0-31 | scores of keys 32-63 with the softmax of keys 0-31 |
+    //   P.V of keys 0-31 with the softmax of keys 32-63 | P.V of keys 32-63.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    const int s_first = step_first + grp;
+    const int n_it = ceil_div(step_end - step_first, 2);
+    if (n_it > 0) {
+      ensure_pages(step_first, min(step_first + 3, step_end - 1));
+      if (s_first < step_end) {
+        dma_tile(s_first, kbase, k0);
+        dma_tile(s_first, vbase, v0);
+      }
     }
-  }
-  // Everything loaded before the loop (query rows, the first steps) has landed: the
-  // loop then only waits for its own staging loads, not for every load in flight.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  const int npairs = ceil_div(step_end - step_first, 2);
-  for (int i = 0; i < npairs; ++i) {
-    const int step = s_first + 2 * i;
-    const int buf = i & 1;
-    // The page ids of this iteration's prefetch (step + 4) are read before the compute.
-    const int pair_next = step_first + 2 * i + 4;  // the next prefetch, uniform over groups
-    int ph_next[LPT];
-    if (pair_next < step_end) {
-      ensure_pages(pair_next, min(pair_next + 1, step_end - 1));
-      if (step + 4 < step_end) plan(step + 4, ph_next);
+    // The copies and the query loads have landed: the compiler does not order reads of
+    // the copies' LDS after their completion itself (and without a wait here on every
+    // path into the loop, it puts one for the query into each iteration).
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    auto iteration = [&](int i, auto cur_c) {
+      constexpr int cur = decltype(cur_c)::value;
+      uint16_t* const k_cur = cur ? k1 : k0;
+      uint16_t* const v_cur = cur ? v1 : v0;
+      uint16_t* const k_nxt = cur ? k0 : k1;  // the next step's copies go here
+      uint16_t* const v_nxt = cur ? v0 : v1;
+      const int step = s_first + 2 * i;
+      const int pn = step_first + 2 * i + 2;
+      if (pn < step_end) ensure_pages(pn, min(pn + 1, step_end - 1));
+      if (step + 2 < step_end) {
+        dma_tile(step + 2, kbase, k_nxt);
+        dma_tile(step + 2, vbase, v_nxt);
+      }
+      if (step < step_end) {
+        const bool full = step_full(step);
+        mf_f32x4 sv[RB][4];
+        scores(k_from(k_cur), sv, I0{}, I2{});
+        if (!full) mask_scores(step, sv, 0, 2);
+        scores(k_from(k_cur), sv, I2{}, I2{});
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          softmax_max(sv, rb, 0);
+          softmax_exp(sv, rb, 0);
+        }
+        if constexpr (MSATTN_PF_SCHED) pf_sched_half<JD * RB * 2, 5>();
+        // The weights stay in this block (the compiler would otherwise move them past the
+        // branches below, next to their use and away from the MFMAs they overlap).
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][0]);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) rescale(rb);
+        if (!full) mask_scores(step, sv, 2, 2);
+        pv(v_from(v_cur), 0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          softmax_max(sv, rb, 1);
+          softmax_exp(sv, rb, 1);
+        }
+        if constexpr (MSATTN_PF_SCHED) pf_sched_half<RB * ND, 5>();
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][1]);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) rescale(rb);
+        pv(v_from(v_cur), 1);
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      __syncthreads();  // the next step's copies landed; this step's reads are done
+    };
+    int i = 0;
+    for (; i + 1 < n_it; i += 2) {
+      iteration(i, I0{});
+      iteration(i + 1, I1{});
     }
-    if (step < step_end) compute(step, buf);
-    if (step + 2 < step_end) stage(buf ^ 1);  // its readers finished before the last barrier
-    if (step + 4 < step_end) issue(step + 4, ph_next);
-    __syncthreads();  // buf ^ 1 is written; buf's reads are done
+    if (i < n_it) iteration(i, I0{});
+  } else {
+    // ---- register staging (caches converted on the way: fp8 e4m3, fp32) ----
+    // A group's thread gtid loads chunk st_c of token rows st_r + ROWS_PER_PASS * j of the
+    // group's steps. A pass covers ROWS_PER_PASS / 16 tiles of 16 tokens (1 for head_dim
+    // 128, 2 for 64); a wave's rows lie in one of them, tile st_tile of the pass.
+    constexpr int CPR = D * 2 / 16;  // 16-byte chunks per K/V row (as T)
+    constexpr int LPT = kPfStep * CPR / kPfGroupThreads;  // chunks per thread per tensor per step
+    static_assert(LPT * kPfGroupThreads == kPfStep * CPR, "staging split");
+    const int gtid = tid - grp * kPfGroupThreads;
+    const int st_c = gtid % CPR;
+    const int st_r = gtid / CPR;
+    constexpr int ROWS_PER_PASS = kPfGroupThreads / CPR;
+    static_assert(ROWS_PER_PASS % 16 == 0 && kWave / CPR <= 16, "a wave's rows in one tile");
+    const int st_tile = ROWS_PER_PASS > 16 ? __builtin_amdgcn_readfirstlane(st_r / 16) : 0;
+    const int st_row = st_r % 16;
+    raw_t kst[LPT], vst[LPT];
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) kst[j] = vst[j] = KV::keep_if(raw_t{}, false);
+    // A step's row j * 16 + r is row r of its 16-token tile j; block_size % 16 == 0 puts a
+    // tile in one page, so the page lookup and the tile's base offset are the same for
+    // every lane (scalar), and a lane only adds its constant in-tile offset. Each tile is
+    // read through a buffer descriptor whose size ends at the last row below hi_all (rows
+    // past it, and tiles that are holes, read as zeros).
+    const uint32_t st_off = static_cast<uint32_t>((st_row * p.slot_stride + st_c * 8) * EB);
+    // The page ids of a step's tiles are read from the window ahead of the loads (plan),
+    // so the LDS latency of the lookups is not paid in front of each tile's loads.
+    auto plan = [&](int step, int (&phys)[LPT]) {
+#pragma unroll
+      for (int j = 0; j < LPT; ++j)
+        phys[j] = s_pg[page_of(step * kPfStep + ROWS_PER_PASS * j + 16 * st_tile) - pg_base];
+    };
+    auto issue = [&](int step, const int (&phys_planned)[LPT]) {
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) {
+        const int t0 = step * kPfStep + ROWS_PER_PASS * j + 16 * st_tile;  // the wave's tile
+        const int pg = page_of(t0);
+        const int phys = __builtin_amdgcn_readfirstlane(phys_planned[j]);
+        const int rows_valid = min(16, hi_all - t0);
+        const bool tile_in = phys >= 0 && rows_valid > 0 && t0 + 16 > lo_all;
+        const int64_t tbase = tile_in ? static_cast<int64_t>(phys) * p.blk_stride +
+                                            static_cast<int64_t>(t0 - pg * p.bs) * p.slot_stride +
+                                            static_cast<int64_t>(kvh) * p.head_stride
+                                      : 0;
+        const int nbytes = tile_in ? static_cast<int>((rows_valid - 1) * row_bytes + D * EB) : 0;
+        kst[j] = KV::template load<0>(tile_rsrc(kbase + tbase, nbytes), st_off);
+        vst[j] = KV::template load<0>(tile_rsrc(vbase + tbase, nbytes), st_off);
+        if (t0 < lo_all) {  // a window's first tile: rows below it are zeros too
+          const bool keep = t0 + st_row >= lo_all;
+          kst[j] = KV::keep_if(kst[j], keep);
+          vst[j] = KV::keep_if(vst[j], keep);
+        }
+      }
+    };
+    auto stage = [&](int buf) {  // the registers loaded by issue() into LDS buffer `buf`
+      uint16_t* const kb = buf ? &s_k1[grp][0] : &s_k0[grp][0];
+      uint16_t* const vb = buf ? &s_v1[grp][0] : &s_v0[grp][0];
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) {
+        const int r = st_r + ROWS_PER_PASS * j;
+        *reinterpret_cast<uint4*>(kb + r * RSK + st_c * 8) = KV::operand(kst[j]);
+        *reinterpret_cast<uint4*>(vb + r * RSV + st_c * 8) = KV::operand(vst[j]);
+      }
+    };
+    const int tr_dim = 4 * (lane & 3);
+    auto compute = [&](int step, int buf) {
+      uint16_t* const kb = buf ? &s_k1[grp][0] : &s_k0[grp][0];
+      uint16_t* const vb = buf ? &s_v1[grp][0] : &s_v0[grp][0];
+      mf_f32x4 sv[RB][4];
+      if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(1);
+      scores([&](int sl, int j) {
+        return *reinterpret_cast<const uint4*>(kb + (16 * sl + n) * RSK + 32 * j + 8 * g);
+      }, sv, std::integral_constant<int, 0>{}, std::integral_constant<int, 4>{});
+      if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(0);
+      if (!step_full(step)) mask_scores(step, sv, 0, 4);
+      // Half-step by half-step: the same order of operations as the copy path
+      // (bit-identical results).
+      auto va_of = [&](int ks, int t) {
+        uint16_t* lo = vb + (32 * ks + 4 * g + tr_tok) * RSV + 16 * t + tr_dim;
+        return tr_pair(lo, lo + 16 * RSV);
+      };
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          softmax_max(sv, rb, ks);
+          softmax_exp(sv, rb, ks);
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) rescale(rb);
+        if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(1);
+        pv(va_of, ks);
+        if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(0);
+      }
+    };
+
+    // Group grp takes steps step_first + grp + 2i (i = 0, 1, ...) from its own pair of
+    // buffers; both groups meet at one barrier per pair of steps.
+    const int s_first = step_first + grp;
+    if (step_first < step_end) {
+      ensure_pages(step_first, min(step_first + 3, step_end - 1));
+      int ph[LPT];
+      if (s_first < step_end) {
+        plan(s_first, ph);
+        issue(s_first, ph);
+      }
+      stage(0);
+      if (s_first + 2 < step_end) {
+        plan(s_first + 2, ph);
+        issue(s_first + 2, ph);
+      }
+    }
+    // Everything loaded before the loop (query rows, the first steps) has landed: the
+    // loop then only waits for its own staging loads, not for every load in flight.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const int npairs = ceil_div(step_end - step_first, 2);
+    for (int i = 0; i < npairs; ++i) {
+      const int step = s_first + 2 * i;
+      const int buf = i & 1;
+      // The page ids of this iteration's prefetch (step + 4) are read before the compute.
+      const int pair_next = step_first + 2 * i + 4;  // the next prefetch, uniform over groups
+      int ph_next[LPT];
+      if (pair_next < step_end) {
+        ensure_pages(pair_next, min(pair_next + 1, step_end - 1));
+        if (step + 4 < step_end) plan(step + 4, ph_next);
+      }
+      if (step < step_end) compute(step, buf);
+      if (step + 2 < step_end) stage(buf ^ 1);  // its readers finished before the last barrier
+      if (step + 4 < step_end) issue(step + 4, ph_next);
+      __syncthreads();  // buf ^ 1 is written; buf's reads are done
+    }
   }
 
   // ---- combine the two key groups (same rows, same lane layout), normalise, store ----
-  // Group 1 hands its (acc, m, l) through LDS (the V buffers, free after the loop);
-  // lane (g, n) of group 0's wave w reads exactly what lane (g, n) of group 1's wave w
-  // wrote: O[row n][dims 16t + 4g + r] and the row's running m and partial l.
-  static_assert(sizeof(s_v) >= kPfWaves * RB * (ND * kWave * 16 + kWave * 8), "combine space");
-  float4* s_acc = reinterpret_cast<float4*>(&s_v[0][0][0]);
-  float2* s_ml = reinterpret_cast<float2*>(s_acc + kPfWaves * RB * ND * kWave);
+  // Group 1 hands its (acc, m, l) through LDS (the K slots hold row block 0 / 1's
+  // accumulators, the first V slot m and l; all free after the loop): lane (g, n) of group
+  // 0's wave w reads exactly what lane (g, n) of group 1's wave w wrote: O[row n][dims
+  // 16t + 4g + r] and the row's running m and partial l.
+  static_assert(sizeof(s_k0) >= kPfWaves * ND * kWave * 16, "combine space");
+  static_assert(sizeof(s_v0) >= kPfWaves * RB * kWave * 8, "combine space");
+  float4* const s_acc0 = reinterpret_cast<float4*>(&s_k0[0][0]);
+  float4* const s_acc1 = reinterpret_cast<float4*>(&s_k1[0][0]);
+  float2* const s_ml = reinterpret_cast<float2*>(&s_v0[0][0]);
   if (grp == 1) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
+      float4* const s_acc = rb == 0 ? s_acc0 : s_acc1;
 #pragma unroll
       for (int t = 0; t < ND; ++t)
-        s_acc[((w * RB + rb) * ND + t) * kWave + lane] =
+        s_acc[(w * ND + t) * kWave + lane] =
             make_float4(acc[rb][t][0], acc[rb][t][1], acc[rb][t][2], acc[rb][t][3]);
       s_ml[(w * RB + rb) * kWave + lane] = make_float2(m_run[rb], l_run[rb]);
     }
@@ -509,6 +728,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   if (grp == 0) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
+      const float4* const s_acc = rb == 0 ? s_acc0 : s_acc1;
       const float2 ml1 = s_ml[(w * RB + rb) * kWave + lane];
       const float M = fmaxf(m_run[rb], ml1.x);
       const float a0 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[rb] - M);
@@ -517,11 +737,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       l = rows4_sum(l);
       if constexpr (PX) {  // unnormalised partial of this (row, key partition)
         if (row_ok[rb]) {
-          const int64_t slot = orow[rb] * p.npart + blockIdx.y;
+          const int64_t slot = out_row(rb) * p.npart + blockIdx.y;
           if (g == 0) *reinterpret_cast<float2*>(p.pml + slot * 2) = make_float2(M, l);
 #pragma unroll
           for (int t = 0; t < ND; ++t) {
-            const float4 o1 = s_acc[((w * RB + rb) * ND + t) * kWave + lane];
+            const float4 o1 = s_acc[(w * ND + t) * kWave + lane];
             *reinterpret_cast<float4*>(p.pacc + slot * D + 16 * t + 4 * g) =
                 make_float4(acc[rb][t][0] * a0 + o1.x * a1, acc[rb][t][1] * a0 + o1.y * a1,
                             acc[rb][t][2] * a0 + o1.z * a1, acc[rb][t][3] * a0 + o1.w * a1);
@@ -531,10 +751,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       }
       if (row_ok[rb]) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        T* op = static_cast<T*>(p.out) + orow[rb] * D;
+        T* op = static_cast<T*>(p.out) + out_row(rb) * D;
 #pragma unroll
         for (int t = 0; t < ND; ++t) {
-          const float4 o1 = s_acc[((w * RB + rb) * ND + t) * kWave + lane];
+          const float4 o1 = s_acc[(w * ND + t) * kWave + lane];
           const float o0 = (acc[rb][t][0] * a0 + o1.x * a1) * inv;
           const float o1_ = (acc[rb][t][1] * a0 + o1.y * a1) * inv;
           const float o2 = (acc[rb][t][2] * a0 + o1.z * a1) * inv;
@@ -546,7 +766,6 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     }
   }
 }
-
 template <typename T, typename KT>
 hipError_t launch_prefill_mfma_impl(const PrefillParams& p, int D, hipStream_t stream,
                                     bool* supported) {
