@@ -42,9 +42,13 @@
 #ifndef MSATTN_PF_DMA
 #define MSATTN_PF_DMA 1
 #endif
-// Interleaving of MFMA and VALU work requested from the scheduler on the copy path.
+// Interleaving of MFMA and VALU work requested from the scheduler on the copy path:
+// MSATTN_PF_NV VALU instructions after each MFMA of a half-step block.
 #ifndef MSATTN_PF_SCHED
 #define MSATTN_PF_SCHED 1
+#endif
+#ifndef MSATTN_PF_NV
+#define MSATTN_PF_NV 5
 #endif
 
 namespace msattn {
@@ -93,14 +97,16 @@ __device__ __forceinline__ void keep_here(const uint4& v) {
 }
 
 // Instruction order asked of the scheduler for a half-step block of the copy path: NM
-// MFMAs, each followed by NV VALU instructions (the other half-step's softmax), the LDS
-// reads of the MFMA operands free to move. Group masks: 0x008 MFMA, 0x002 VALU.
-template <int NM, int NV>
+// MFMAs, each followed by NV VALU instructions (the other half-step's softmax), and the
+// block's NC copy instructions spread among them; the LDS reads of the MFMA operands are
+// free to move. Group masks: 0x008 MFMA, 0x002 VALU, 0x020 vector memory read.
+template <int NM, int NV, int NC>
 __device__ __forceinline__ void pf_sched_half() {
 #pragma unroll
   for (int m = 0; m < NM; ++m) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+    if (m % (NM / NC) == NM / NC - 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
   }
 }
 
@@ -171,7 +177,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   __shared__ __attribute__((aligned(256))) uint16_t s_k1[kPfGroups][kPfStep * RSK];
   __shared__ __attribute__((aligned(256))) uint16_t s_v0[kPfGroups][kPfStep * RSV];
   __shared__ __attribute__((aligned(256))) uint16_t s_v1[kPfGroups][kPfStep * RSV];
-  __shared__ int s_pg[kPfPageChunk];
+  // Page window: kPfPageChunk page ids (register staging) or 16-token tile offsets (copies).
+  __shared__ __attribute__((aligned(8))) int s_pg[2 * kPfPageChunk];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -455,23 +462,60 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       const int lr = RPI * j + lane / CPRD;
       dvo[j] = static_cast<uint32_t>(lr * row_bytes + 16 * ((lane % CPRD) ^ pf_swz<D>(lr)));
     }
-    // Copy this wave's 16-row tile of a step of K or V into the LDS slot dst.
-    auto dma_tile = [&](int step, const KT* src, uint16_t* dst) {
+    // This wave's 16-row tile of a step (token rows 16 w ..): one descriptor for its K
+    // rows and one for its V rows, and the offset that pushes rows below a window's first
+    // key out of range. ok = false gives empty descriptors (the copies then write zeros).
+    struct TileCopy {
+      __amdgpu_buffer_rsrc_t rk, rv;
+      uint32_t skip;
+    };
+    // Window of tile offsets: s_tile[i] = element offset of 16-token tile tb_base + i of
+    // this (sequence, KV head) in the caches, or -1 for a tile on an unmapped page.
+    // Reloaded (between barriers, by every thread) when a step leaves it.
+    int64_t* const s_tile = reinterpret_cast<int64_t*>(s_pg);
+    int tb_base = -(1 << 30);
+    auto ensure_tiles = [&](int s_lo, int s_hi) {
+      const int t_lo = s_lo * (kPfStep / 16);
+      const int t_hi = s_hi * (kPfStep / 16) + kPfStep / 16 - 1;
+      if (t_lo < tb_base || t_hi >= tb_base + kPfPageChunk) {
+        __syncthreads();
+        for (int j = tid; j < kPfPageChunk; j += kPfThreads) {
+          const int tok = (t_lo + j) * 16;
+          const int pg = page_of(tok);
+          int64_t off = -1;
+          if (pg < p.W) {
+            const int phys = p.table[static_cast<int64_t>(b) * p.W + pg];
+            if (phys >= 0 && phys < p.num_blocks)
+              off = static_cast<int64_t>(phys) * p.blk_stride +
+                    static_cast<int64_t>(tok - pg * p.bs) * p.slot_stride +
+                    static_cast<int64_t>(kvh) * p.head_stride;
+          }
+          s_tile[j] = off;
+        }
+        tb_base = t_lo;
+        __syncthreads();
+      }
+    };
+    auto plan_tile = [&](int step, bool ok) {
       const int t0 = step * kPfStep + 16 * w;
-      const int pg = page_of(t0);
-      const int phys = __builtin_amdgcn_readfirstlane(s_pg[pg - pg_base]);
+      const int64_t o = s_tile[ok ? t0 / 16 - tb_base : 0];
+      const uint32_t lo32 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(o));
+      const uint32_t hi32 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(o) >> 32));
+      const int64_t off = ok ? static_cast<int64_t>((static_cast<uint64_t>(hi32) << 32) | lo32) : -1;
       const int rows_valid = min(16, hi_all - t0);
-      const bool tile_in = phys >= 0 && rows_valid > 0 && t0 + 16 > lo_all;
+      const bool tile_in = off >= 0 && rows_valid > 0 && t0 + 16 > lo_all;
       const int skip = tile_in && t0 < lo_all ? lo_all - t0 : 0;  // rows below the window
-      const int64_t tbase = tile_in ? static_cast<int64_t>(phys) * p.blk_stride +
-                                          static_cast<int64_t>(t0 - pg * p.bs + skip) * p.slot_stride +
-                                          static_cast<int64_t>(kvh) * p.head_stride
-                                    : 0;
+      const int64_t tbase = tile_in ? off + static_cast<int64_t>(skip) * p.slot_stride : 0;
       const int nbytes = tile_in ? static_cast<int>((rows_valid - 1 - skip) * row_bytes + D * EB) : 0;
-      const __amdgpu_buffer_rsrc_t r = tile_rsrc(src + tbase, nbytes);
-      const uint32_t sk = static_cast<uint32_t>(skip * row_bytes);  // rows below wrap out of range
-#pragma unroll
-      for (int j = 0; j < NI; ++j) lds_copy16(r, dst + (16 * w + RPI * j) * D, dvo[j] - sk);
+      TileCopy c;
+      c.rk = tile_rsrc(kbase + tbase, nbytes);
+      c.rv = tile_rsrc(vbase + tbase, nbytes);
+      c.skip = static_cast<uint32_t>(skip * row_bytes);  // rows below wrap out of range
+      return c;
+    };
+    // Copy instruction j of the tile (RPI token rows) into the LDS slot dst.
+    auto copy_rows = [&](__amdgpu_buffer_rsrc_t r, uint32_t skip, uint16_t* dst, int j) {
+      lds_copy16(r, dst + (16 * w + RPI * j) * D, dvo[j] - skip);
     };
     uint16_t* const k0 = &s_k0[grp][0];
     uint16_t* const k1 = &s_k1[grp][0];
@@ -502,74 +546,167 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
+    // A step in four blocks (half-steps of 32 keys), each pairing independent MFMA and
+    // VALU work where it can:
+    //   r0: scores of keys 0-31;
+    //   r1: scores of keys 32-63 | softmax of keys 0-31;
+    //   r2: P.V of keys 0-31 | softmax of keys 32-63;
+    //   r3: P.V of keys 32-63.
+    // The scores sv and weights pb of a step live across blocks (and, for group 1, across
+    // an iteration's barrier). `copies` issues copy instructions among the block's MFMAs.
+    mf_f32x4 sv[RB][4];
+    auto r0 = [&](uint16_t* kc, int step, bool full, auto&& side) {
+      scores(k_from(kc), sv, I0{}, I2{});
+      side();
+      if (!full) mask_scores(step, sv, 0, 2);
+    };
+    auto r1 = [&](uint16_t* kc, int step, bool full, auto&& copies) {
+      scores(k_from(kc), sv, I2{}, I2{});
+      copies();
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        softmax_max(sv, rb, 0);
+        softmax_exp(sv, rb, 0);
+      }
+      if constexpr (MSATTN_PF_SCHED) pf_sched_half<JD * RB * 2, MSATTN_PF_NV, NI>();
+      // The weights stay in this block (the compiler would otherwise move them past the
+      // branches below, next to their use and away from the MFMAs they overlap).
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][0]);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) rescale(rb);
+      if (!full) mask_scores(step, sv, 2, 2);
+    };
+    auto r2 = [&](uint16_t* vc, auto&& copies) {
+      pv(v_from(vc), 0);
+      copies();
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        softmax_max(sv, rb, 1);
+        softmax_exp(sv, rb, 1);
+      }
+      if constexpr (MSATTN_PF_SCHED) pf_sched_half<RB * ND, MSATTN_PF_NV, NI>();
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][1]);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) rescale(rb);
+    };
+    auto r3 = [&](uint16_t* vc) { pv(v_from(vc), 1); };
+    auto no_copies = [] {};
+
+    // Group grp takes steps s_first + 2 i; the K and V of its i-th step go to slots
+    // k(i & 1) and v(i & 1). Both groups meet at one barrier per iteration, but run half a
+    // step apart so that a SIMD's two waves are in complementary blocks: iteration i of
+    // group 0 is r0 r1 r2 r3 of its step i; of group 1, r2 r3 of its step i - 1, then r0
+    // r1 of its step i. While one wave's block is MFMA-only, the other's is MFMA + VALU.
+    // The copy plans (scalar work) of an iteration are made during the one before, in its
+    // MFMA-only blocks.
     const int s_first = step_first + grp;
     const int n_it = ceil_div(step_end - step_first, 2);
+    TileCopy ck = plan_tile(0, false), cv = ck;  // this iteration's copies: K, V
     if (n_it > 0) {
-      ensure_pages(step_first, min(step_first + 3, step_end - 1));
-      if (s_first < step_end) {
-        dma_tile(s_first, kbase, k0);
-        dma_tile(s_first, vbase, v0);
+      ensure_tiles(step_first, min(step_first + 5, step_end - 1));
+      const TileCopy c = plan_tile(s_first, s_first < step_end);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        copy_rows(c.rk, c.skip, k0, j);
+        if (grp == 0) copy_rows(c.rv, c.skip, v0, j);  // group 1 copies V a step later
       }
+      // group 0 copies step i + 1 in iteration i; group 1, K of step i + 1 and V of step i
+      ck = plan_tile(s_first + 2, s_first + 2 < step_end);
+      cv = grp == 0 ? ck : c;
     }
     // The copies and the query loads have landed: the compiler does not order reads of
     // the copies' LDS after their completion itself (and without a wait here on every
     // path into the loop, it puts one for the query into each iteration).
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
-    auto iteration = [&](int i, auto cur_c) {
+    // Each group runs its own copy of the loop (the two meet at the same barriers: one
+    // per iteration and the window reloads, all at the same iterations).
+    auto iteration0 = [&](int i, auto cur_c) {
       constexpr int cur = decltype(cur_c)::value;
-      uint16_t* const k_cur = cur ? k1 : k0;
-      uint16_t* const v_cur = cur ? v1 : v0;
-      uint16_t* const k_nxt = cur ? k0 : k1;  // the next step's copies go here
-      uint16_t* const v_nxt = cur ? v0 : v1;
+      uint16_t* const k_cur = cur ? k1 : k0;  // K of the group's step i
+      uint16_t* const k_nxt = cur ? k0 : k1;  // K of step i + 1 goes here
+      uint16_t* const v_cur = cur ? v1 : v0;  // V of step i
+      uint16_t* const v_nxt = cur ? v0 : v1;  // V of step i + 1 goes here
       const int step = s_first + 2 * i;
       const int pn = step_first + 2 * i + 2;
-      if (pn < step_end) ensure_pages(pn, min(pn + 1, step_end - 1));
-      if (step + 2 < step_end) {
-        dma_tile(step + 2, kbase, k_nxt);
-        dma_tile(step + 2, vbase, v_nxt);
+      if (pn < step_end) ensure_tiles(pn, min(pn + 3, step_end - 1));
+      if (step < step_end) {
+        const bool full = step_full(step);
+        TileCopy cn;  // the next iteration's copies (step + 4)
+        r0(k_cur, step, full, [&] { cn = plan_tile(step + 4, step + 4 < step_end); });
+        r1(k_cur, step, full, [&] {
+#pragma unroll
+          for (int j = 0; j < NI; ++j) copy_rows(ck.rk, ck.skip, k_nxt, j);
+        });
+        r2(v_cur, [&] {
+#pragma unroll
+          for (int j = 0; j < NI; ++j) copy_rows(ck.rv, ck.skip, v_nxt, j);
+        });
+        r3(v_cur);
+        ck = cn;
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      __syncthreads();  // this iteration's copies landed; the reads of their slots are done
+    };
+    auto iteration1 = [&](int i, auto cur_c) {
+      constexpr int cur = decltype(cur_c)::value;
+      uint16_t* const k_cur = cur ? k1 : k0;  // K of the group's step i
+      uint16_t* const k_nxt = cur ? k0 : k1;  // K of step i + 1 goes here
+      uint16_t* const v_cur = cur ? v1 : v0;  // V of step i goes here
+      uint16_t* const v_prv = cur ? v0 : v1;  // V of step i - 1
+      const int step = s_first + 2 * i;
+      const int pn = step_first + 2 * i + 2;
+      if (pn < step_end) ensure_tiles(pn, min(pn + 3, step_end - 1));
+      if (i > 0 && step - 2 < step_end) {  // the second half of step i - 1
+        r2(v_prv, [&] {
+#pragma unroll
+          for (int j = 0; j < NI; ++j) copy_rows(ck.rk, ck.skip, k_nxt, j);
+        });
+        r3(v_prv);
+      } else {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) copy_rows(ck.rk, ck.skip, k_nxt, j);
       }
       if (step < step_end) {
         const bool full = step_full(step);
-        mf_f32x4 sv[RB][4];
-        scores(k_from(k_cur), sv, I0{}, I2{});
-        if (!full) mask_scores(step, sv, 0, 2);
-        scores(k_from(k_cur), sv, I2{}, I2{});
+        TileCopy ckn, cvn;  // the next iteration's copies: K of step + 4, V of step + 2
+        r0(k_cur, step, full, [&] {
+          ckn = plan_tile(step + 4, step + 4 < step_end);
+          cvn = plan_tile(step + 2, step + 2 < step_end);
+        });
+        r1(k_cur, step, full, [&] {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          softmax_max(sv, rb, 0);
-          softmax_exp(sv, rb, 0);
-        }
-        if constexpr (MSATTN_PF_SCHED) pf_sched_half<JD * RB * 2, 5>();
-        // The weights stay in this block (the compiler would otherwise move them past the
-        // branches below, next to their use and away from the MFMAs they overlap).
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][0]);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) rescale(rb);
-        if (!full) mask_scores(step, sv, 2, 2);
-        pv(v_from(v_cur), 0);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          softmax_max(sv, rb, 1);
-          softmax_exp(sv, rb, 1);
-        }
-        if constexpr (MSATTN_PF_SCHED) pf_sched_half<RB * ND, 5>();
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][1]);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) rescale(rb);
-        pv(v_from(v_cur), 1);
+          for (int j = 0; j < NI; ++j) copy_rows(cv.rv, cv.skip, v_cur, j);
+        });
+        ck = ckn;
+        cv = cvn;
       }
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
-      __syncthreads();  // the next step's copies landed; this step's reads are done
+      __syncthreads();  // this iteration's copies landed; the reads of their slots are done
     };
-    int i = 0;
-    for (; i + 1 < n_it; i += 2) {
-      iteration(i, I0{});
-      iteration(i + 1, I1{});
+    if (grp == 0) {
+      int i = 0;
+      for (; i + 1 < n_it; i += 2) {
+        iteration0(i, I0{});
+        iteration0(i + 1, I1{});
+      }
+      if (i < n_it) iteration0(i, I0{});
+    } else {
+      int i = 0;
+      for (; i + 1 < n_it; i += 2) {
+        iteration1(i, I0{});
+        iteration1(i + 1, I1{});
+      }
+      if (i < n_it) iteration1(i, I0{});
     }
-    if (i < n_it) iteration(i, I0{});
+    // Group 1: the second half of its last step (its V landed at the last barrier).
+    if (grp == 1 && n_it > 0 && s_first + 2 * (n_it - 1) < step_end) {
+      uint16_t* const v_last = ((n_it - 1) & 1) ? v1 : v0;
+      r2(v_last, no_copies);
+      r3(v_last);
+    }
   } else {
     // ---- register staging (caches converted on the way: fp8 e4m3, fp32) ----
     // A group's thread gtid loads chunk st_c of token rows st_r + ROWS_PER_PASS * j of the
