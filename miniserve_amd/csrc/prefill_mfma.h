@@ -50,6 +50,10 @@
 #ifndef MSATTN_PF_NV
 #define MSATTN_PF_NV 5
 #endif
+// Wave priority of key group 1 over its loop (copy path).
+#ifndef MSATTN_PF_G1PRIO
+#define MSATTN_PF_G1PRIO 1
+#endif
 
 namespace msattn {
 
@@ -694,12 +698,16 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       }
       if (i < n_it) iteration0(i, I0{});
     } else {
+      // Group 1 carries the iteration's critical path (its blocks include the plans of two
+      // copies): its waves issue first when both waves of a SIMD are ready.
+      if constexpr (MSATTN_PF_G1PRIO > 0) __builtin_amdgcn_s_setprio(MSATTN_PF_G1PRIO);
       int i = 0;
       for (; i + 1 < n_it; i += 2) {
         iteration1(i, I0{});
         iteration1(i + 1, I1{});
       }
       if (i < n_it) iteration1(i, I0{});
+      if constexpr (MSATTN_PF_G1PRIO > 0) __builtin_amdgcn_s_setprio(0);
     }
     // Group 1: the second half of its last step (its V landed at the last barrier).
     if (grp == 1 && n_it > 0 && s_first + 2 * (n_it - 1) < step_end) {
