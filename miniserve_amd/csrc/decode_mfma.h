@@ -41,6 +41,13 @@
 #ifndef MSATTN_MFMA_WAVES
 #define MSATTN_MFMA_WAVES 4
 #endif
+// Tiles in flight per wave (ring depth), head_dim 128 / head_dim 64.
+#ifndef MSATTN_MFMA_DEPTH
+#define MSATTN_MFMA_DEPTH 2
+#endif
+#ifndef MSATTN_MFMA_DEPTH_D64
+#define MSATTN_MFMA_DEPTH_D64 2
+#endif
 #ifndef MSATTN_LOAD_AUX
 #define MSATTN_LOAD_AUX 2
 #endif
@@ -663,25 +670,28 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     pv_tile<T, KT, D, RT>(acc, pr, vm, va);
   };
 
-  // Two tiles in flight. The sequence is fully unrolled (a wave owns at most
-  // kMaxTilesPerWave tiles) so every wait for a tile's loads is exact; a load for
-  // tile nt reads nothing (its descriptor has no records).
-  raw_t k0[JD], v0[NJ], k1[JD], v1[NJ];
-  int64_t base0 = tile_base(0);
-  issue(base0, k0, v0);
-#pragma unroll
-  for (int k = 0; k < kMaxTilesPerWave; k += 2) {
-    if (k >= nt) break;
-    const int64_t base1 = tile_base(k + 1);
-    issue(base1, k1, v1);
-    consume(k, k0, v0, base0);
-    if (k + 1 >= nt) break;
-    if (k + 2 < kMaxTilesPerWave) {
-      base0 = tile_base(k + 2);
-      issue(base0, k0, v0);
+  // A ring of DEPTH tiles: the loads of DEPTH - 1 tiles are in flight while one is
+  // consumed. The sequence is fully unrolled (a wave owns at most kMaxTilesPerWave
+  // tiles) so every wait for a tile's loads is exact; loads for tiles at or past nt read
+  // nothing (their descriptors have no records).
+  constexpr int DEPTH = D == 64 ? MSATTN_MFMA_DEPTH_D64 : MSATTN_MFMA_DEPTH;
+  raw_t kr[DEPTH][JD], vr[DEPTH][NJ];
+  int64_t br[DEPTH];
+  static_for<DEPTH - 1>([&](auto dc) {
+    constexpr int d = decltype(dc)::value;
+    br[d] = tile_base(d);
+    issue(br[d], kr[d], vr[d]);
+  });
+  static_for<kMaxTilesPerWave>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    if (k >= nt) return;
+    constexpr int nx = k + DEPTH - 1;  // the tile whose loads go out now
+    if constexpr (nx < kMaxTilesPerWave) {
+      br[nx % DEPTH] = tile_base(nx);
+      issue(br[nx % DEPTH], kr[nx % DEPTH], vr[nx % DEPTH]);
     }
-    consume(k + 1, k1, v1, base1);
-  }
+    consume(k, kr[k % DEPTH], vr[k % DEPTH], br[k % DEPTH]);
+  });
 
   // Wave totals: l over the 4 lane groups, acc over the V token groups (lanes of equal
   // lane % LPR), reduce-scattered so a lane keeps two dims of each row: dims
