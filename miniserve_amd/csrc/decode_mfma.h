@@ -601,13 +601,13 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
 
   // Element offset of the wave's tile k, or -1 (hole, or k >= nt).
-  auto tile_base = [&](int k) -> int64_t {
+  auto tile_base = [&](int k) -> int64_t __attribute__((always_inline)) {
     const uint32_t lo = static_cast<uint32_t>(
         __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(my_base)), k));
     const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
     return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
   };
-  auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) {
+  auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) __attribute__((always_inline)) {
     const bool ok = base >= 0;
     const int64_t b0 = ok ? base : 0;
     const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
@@ -617,7 +617,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     for (int j = 0; j < NJ; ++j) vb[j] = KV::template load<0>(rv, v_lane_off[j]);
   };
 
-  auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) {
+  auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) __attribute__((always_inline)) {
     mf_f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < JD; ++j) s = Mfma16<T>::mac(KV::operand(kb[j]), qb[j], s);

@@ -181,7 +181,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
     int b, kvh, row0, nrows, t_first, ntiles, a0, a1;
     int64_t pid, pe;
   };
-  auto locate = [&](int64_t s0) {
+  auto locate = [&](int64_t s0) __attribute__((always_inline)) {
     Piece pc;
     const int ug = static_cast<int>(s0 / sumT);
     const int o = static_cast<int>(s0 - static_cast<int64_t>(ug) * sumT);
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
   };
   // Lane k: element offset of tile t_first + run0 + k of the piece, or -1 for a hole or
   // a lane past the run.
-  auto table_run = [&](const Piece& pc, int run0) -> int64_t {
+  auto table_run = [&](const Piece& pc, int run0) -> int64_t __attribute__((always_inline)) {
     const int nt = min(kSkTableRun, pc.ntiles - run0);
     int64_t mb = -1;
     if (lane < nt) {
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
   };
   // The piece's query rows as the MFMA B operand (lane (g, n): row n, chunk j at dim
   // KV::qk_dim0(j, g), the split the K loads use).
-  auto load_q = [&](const Piece& pc, uint4 (&q)[JD]) {
+  auto load_q = [&](const Piece& pc, uint4 (&q)[JD]) __attribute__((always_inline)) {
     const T* qp = static_cast<const T*>(p.q);
     const int64_t orow_n = static_cast<int64_t>(pc.b) * p.H + pc.kvh * p.G + pc.row0 + n;
 #pragma unroll
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
     const int nt_next = has_next ? min(kSkTableRun, nxt.ntiles - run_n) : 0;
     // Ring position k: tile k of this run, nothing (k < nt_ring), or tile k - nt_ring
     // of the next run.
-    auto tile_base = [&](int k) -> int64_t {
+    auto tile_base = [&](int k) -> int64_t __attribute__((always_inline)) {
       int64_t src = my_base;
       if (k >= nt) {
         k -= nt_ring;
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
       const int hi = __builtin_amdgcn_readlane(static_cast<int>(src >> 32), k);
       return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
     };
-    auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) {
+    auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) __attribute__((always_inline)) {
       const bool ok = base >= 0;
       const int64_t b0 = ok ? base : 0;
       const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
             rv, ((static_cast<uint32_t>(TPI * j + va) * static_cast<uint32_t>(p.slot_stride)) +
                  vc * 8) * EB);
     };
-    auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) {
+    auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) __attribute__((always_inline)) {
       mf_f32x4 sv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < JD; ++j) sv = Mfma16<T>::mac(KV::operand(kb[j]), qb[j], sv);

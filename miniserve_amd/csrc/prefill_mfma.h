@@ -368,54 +368,76 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
           sv[rb][sl][r] = (tok >= lo_n[rb] && tok < hi_n[rb]) ? sv[rb][sl][r] : -INFINITY;
         }
   };
-  // Online softmax of one row block over one half-step (32 keys, slices 2 ks, 2 ks + 1),
-  // in two parts: softmax_max, then softmax_exp. The row max is taken on raw scores
-  // (scale_log2 > 0 keeps the order), the weights are exp2(s * scale_log2 - m). The
-  // running max m only moves when a row's max exceeds it by more than kPfRescaleSlack
-  // (base-2 units): the weights then stay below 2^kPfRescaleSlack, which fp32 sums and
-  // the bf16/fp16 P operand hold, and the accumulator rescale is skipped on most
-  // half-steps. The normalisation by l is exact whatever reference max the sums share.
+  // Online softmax of one row block over one half-step (32 keys, slices 2 ks, 2 ks + 1).
+  // The weights are exp2(s * scale_log2 - m) for the row's running max m (base 2; the row
+  // max is taken on raw scores, scale_log2 > 0 keeps the order). m only moves when a row's
+  // max exceeds it by more than kPfRescaleSlack: the weights then stay below
+  // 2^kPfRescaleSlack, which fp32 sums and the bf16/fp16 P operand hold, and the
+  // normalisation by l is exact whatever reference max the sums share.
+  // Fast path (almost every half-step): each lane tests its own scores against m +
+  // kPfRescaleSlack (max over lanes and the positive scale commute, so no lane over means
+  // no row over) and the weights are taken with the current m, with no cross-lane
+  // reduction. When any lane is over, softmax_redo moves m (the row max over the 4 lane
+  // groups), rescales l and acc, and takes the weights again.
   uint4 pb[RB][2];
-  float alpha[RB];
-  // Part 1: the half-step's row max moves m (or not); alpha = exp2(m_old - m_new)
-  // (exactly 1 when m stays) rescales l.
-  auto softmax_max = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) {
-    float mt = -INFINITY;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sv[rb][2 * ks + h][r]);
-    mt = rows4_max(mt);
-    mt *= p.scale_log2;  // the row max, base-2 units
-    const float m_new = mt > m_run[rb] + kPfRescaleSlack ? mt : m_run[rb];
-    alpha[rb] = m_new != -INFINITY ? __builtin_amdgcn_exp2f(m_run[rb] - m_new) : 1.0f;
-    l_run[rb] *= alpha[rb];
-    m_run[rb] = m_new;
-  };
-  // Part 2: the weights, P^T packed as the B operand of half ks, l += their sum. A row
-  // with no key yet (m = -inf) has only -inf scores: any finite reference gives zeros.
-  auto softmax_exp = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) {
+  float psum[RB];
+  float lmax[RB];
+  auto softmax_exp = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) __attribute__((always_inline)) {
     const float m_use = m_run[rb] != -INFINITY ? m_run[rb] : 0.0f;
     float pr[8];
-    float psum = 0.0f;
+    psum[rb] = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float x = __builtin_amdgcn_exp2f(fmaf(sv[rb][2 * ks + h][r], p.scale_log2, -m_use));
-        pr[4 * h + r] = x;
-        psum += x;
+        pr[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(sv[rb][2 * ks + h][r], p.scale_log2, -m_use));
+        psum[rb] += pr[4 * h + r];
       }
     pb[rb][ks] = make_uint4(Pack2<T>::pack(pr[0], pr[1]), Pack2<T>::pack(pr[2], pr[3]),
                             Pack2<T>::pack(pr[4], pr[5]), Pack2<T>::pack(pr[6], pr[7]));
-    l_run[rb] += psum;
   };
-  // alpha is exactly 1 for rows whose reference max did not move: most steps skip this
-  auto rescale = [&](int rb) {
-    if (__builtin_expect(__any(alpha[rb] != 1.0f), 0)) {
+  // The lane's max and whether it is over the bound, then the weights with the current m.
+  auto softmax_fast = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) __attribute__((always_inline)) {
+    float lm = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < ND; ++t) acc[rb][t] *= alpha[rb];
-    }
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lm = fmaxf(lm, sv[rb][2 * ks + h][r]);
+    lmax[rb] = lm;
+    softmax_exp(sv, rb, ks);
+  };
+  auto over_bound = [&]() __attribute__((always_inline)) {
+    bool over = false;
+    static_for<RB>([&](auto rc) {
+      constexpr int rb = decltype(rc)::value;
+      over |= lmax[rb] * p.scale_log2 > m_run[rb] + kPfRescaleSlack;
+    });
+    return __any(over);
+  };
+  // Slow path for the wave: move m, rescale l and acc, take the weights again.
+  auto softmax_redo = [&](const mf_f32x4 (&sv)[RB][4], int ks) __attribute__((always_inline)) {
+    // (static_for: every array index stays a constant, the arrays stay in registers)
+    static_for<RB>([&](auto rc) {
+      constexpr int rb = decltype(rc)::value;
+      const float mt = rows4_max(lmax[rb]) * p.scale_log2;  // the row max, base-2 units
+      const float m_new = mt > m_run[rb] + kPfRescaleSlack ? mt : m_run[rb];
+      const float alpha = m_new != -INFINITY ? __builtin_amdgcn_exp2f(m_run[rb] - m_new) : 1.0f;
+      l_run[rb] *= alpha;
+      m_run[rb] = m_new;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int t = 0; t < ND; ++t) acc[rb][t] *= alpha;
+      }
+      softmax_exp(sv, rb, ks);
+    });
+  };
+  // After a half-step's weights (fast, and the redo when needed): l += their sum.
+  auto softmax_end = [&](const mf_f32x4 (&sv)[RB][4], int ks) __attribute__((always_inline)) {
+    if (__builtin_expect(over_bound(), 0)) softmax_redo(sv, ks);
+    static_for<RB>([&](auto rc) {
+      constexpr int rb = decltype(rc)::value;
+      l_run[rb] += psum[rb];
+    });
   };
   // O^T += V^T P^T over half-step ks; va_of(ks, t) reads the A operand V^T (dims 16 t ..,
   // tokens 32 ks ..).
@@ -568,32 +590,24 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       scores(k_from(kc), sv, I2{}, I2{});
       copies();
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        softmax_max(sv, rb, 0);
-        softmax_exp(sv, rb, 0);
-      }
+      for (int rb = 0; rb < RB; ++rb) softmax_fast(sv, rb, 0);
       if constexpr (MSATTN_PF_SCHED) pf_sched_half<JD * RB * 2, MSATTN_PF_NV, NI>();
       // The weights stay in this block (the compiler would otherwise move them past the
       // branches below, next to their use and away from the MFMAs they overlap).
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][0]);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) rescale(rb);
+      softmax_end(sv, 0);
       if (!full) mask_scores(step, sv, 2, 2);
     };
     auto r2 = [&](uint16_t* vc, auto&& copies) {
       pv(v_from(vc), 0);
       copies();
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        softmax_max(sv, rb, 1);
-        softmax_exp(sv, rb, 1);
-      }
+      for (int rb = 0; rb < RB; ++rb) softmax_fast(sv, rb, 1);
       if constexpr (MSATTN_PF_SCHED) pf_sched_half<RB * ND, MSATTN_PF_NV, NI>();
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][1]);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) rescale(rb);
+      softmax_end(sv, 1);
     };
     auto r3 = [&](uint16_t* vc) { pv(v_from(vc), 1); };
     auto no_copies = [] {};
@@ -798,12 +812,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          softmax_max(sv, rb, ks);
-          softmax_exp(sv, rb, ks);
-        }
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) rescale(rb);
+        for (int rb = 0; rb < RB; ++rb) softmax_fast(sv, rb, ks);
+        softmax_end(sv, ks);
         if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(1);
         pv(va_of, ks);
         if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(0);
