@@ -64,6 +64,15 @@ constexpr int kSkTableRun = 64;     // tile page ids fetched per table load
 #ifndef MSATTN_SK_ROUNDS
 #define MSATTN_SK_ROUNDS 1
 #endif
+// Two waves on a SIMD (workgroups of more than 4 waves): the hardware issues the older
+// wave's loads first whenever both are ready, so the younger one streams its chunk
+// behind it and ends well after it (C3 fp8: waves 0-3 at 55 us, waves 4-7 at 67 us),
+// with the SIMD half-used meanwhile. With MSATTN_SK_BALANCE, each wave posts the tiles
+// it has consumed in LDS and runs at raised priority while it is not ahead of its SIMD
+// partner (wave w ^ waves/2), so the two keep pace and end together.
+#ifndef MSATTN_SK_BALANCE
+#define MSATTN_SK_BALANCE 1
+#endif
 
 // Pieces a launch can produce: one per chunk plus one per segment boundary.
 __host__ __device__ constexpr int64_t streamk_pieces(int64_t n_chunks, int64_t n_segments) {
@@ -90,10 +99,13 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
   __shared__ int s_pre[kSkMaxBatch + 1];  // exclusive prefix of T_b
   __shared__ int s_ctx[kSkMaxBatch];      // context length of b, clamped to max_ctx
   __shared__ int s_wsum[2][kSkWaves];
+  constexpr bool kBalance = MSATTN_SK_BALANCE && kSkWaves > 4;
+  __shared__ int s_prog[kSkWaves];        // tiles consumed per wave (kBalance)
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  if (kBalance && tid < kSkWaves) s_prog[tid] = 0;  // ordered by the scan's barriers
   const int g = lane >> 4;
   const int n = lane & 15;
   const int va = lane / LPR;
@@ -266,6 +278,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
   raw_t kq[DEPTH][JD], vq[DEPTH][NJ];
   int64_t bq[DEPTH];
   bool primed = false;  // the ring holds the run's first DEPTH - 1 tiles
+  int prog = 0;         // ring positions consumed (kBalance)
   while (true) {
     const bool more_here = run0 + kSkTableRun < cur.ntiles;
     const bool next_piece = !more_here && cur.pe < s_end;
@@ -380,6 +393,19 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
           issue(bq[nx], kq[nx], vq[nx]);
           consume(k + d, kq[cu], vq[cu], bq[cu]);
         });
+        if constexpr (kBalance) {
+          // Post this wave's progress; take priority while not ahead of the partner.
+          // Both walk the same chunk, ring positions included, so counts compare.
+          prog += STEP;
+          if (lane == 0)
+            __hip_atomic_store(&s_prog[w], prog, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          const int other = __hip_atomic_load(&s_prog[w ^ (kSkWaves / 2)], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (prog <= __builtin_amdgcn_readfirstlane(other))
+            __builtin_amdgcn_s_setprio(1);
+          else
+            __builtin_amdgcn_s_setprio(0);
+        }
       }
       primed = has_next;
     }
