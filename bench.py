@@ -54,6 +54,10 @@ def parse():
                          "config dtype; the query stays in the config dtype and the cache is "
                          "cast to it as it is read. Bytes follow the cache's element size.")
     ap.add_argument("--kv-fp8", action="store_true", help="same as --kv-dtype fp8")
+    ap.add_argument("--q-dtype", choices=["same", "fp32"], default="same",
+                    help="the query (and output) in fp32 instead of the config dtype; with "
+                         "--kv-dtype fp32 this is the reference runner's default pair "
+                         "(model_runner.py:122-123), which takes the generic kernel")
     ap.add_argument("--no-cascade", action="store_true",
                     help="decode a shared-prefix workload (config 4) in one pass per sequence "
                          "instead of the cascade entry point")
@@ -179,6 +183,9 @@ def main():
     if kv_torch is not None:  # the same values stored as kv_torch; bytes follow the dtype
         w.k_caches = [c.to(kv_torch) for c in w.k_caches]
         w.v_caches = [c.to(kv_torch) for c in w.v_caches]
+    if args.q_dtype == "fp32":  # the query's values in fp32; q/out bytes follow
+        w.query = w.query.float()
+        w.dtype = torch.float32
 
     B, H, KVH, D, bs = w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
     table = w.table.to(device=dev, dtype=torch.int32).contiguous()
@@ -260,12 +267,17 @@ def main():
             e[2].record()
     torch.cuda.synchronize()
     # Which partials kernel ran: the workspace header's first word is the layout kind
-    # (1 = stream-K); otherwise the partition kernel, on MFMA for bf16/fp16 with head_dim
-    # 64 or 128, else the generic kernel.
+    # (1 = stream-K); otherwise the partition kernel, on MFMA with head_dim 64 or 128 for a
+    # bf16/fp16 query over its own type, fp8 or fp32 and for an fp32 query over fp32, else
+    # the generic kernel.
     kind = int(ws[:4].view(torch.int32).item())
+    kv_t = w.k_caches[0].dtype
+    mfma_pair = ((w.dtype in (torch.bfloat16, torch.float16)
+                  and kv_t in (w.dtype, torch.float8_e4m3fn, torch.float32))
+                 or (w.dtype == torch.float32 and kv_t == torch.float32))
     if kind == 1:
         kernel_name = "msattn::decode_streamk_kernel (stream-K split-K partials)"
-    elif w.dtype in (torch.bfloat16, torch.float16) and D in (64, 128):
+    elif mfma_pair and D in (64, 128):
         kernel_name = "msattn::decode_mfma_kernel (partition split-K partials)"
     else:
         kernel_name = "msattn::split_kernel (generic partition split-K partials)"
@@ -285,7 +297,8 @@ def main():
     # (FETCH_SIZE, WRITE_SIZE) recorded in profiles/; it is reported only when that record
     # was taken on the library this run loaded (same sha256), else null with the reason.
     traffic, traffic_note = None, None
-    tname = f"traffic_{w.name}{'' if args.kv_dtype == 'same' else '-' + args.kv_dtype}.json"
+    tname = (f"traffic_{w.name}{'' if args.kv_dtype == 'same' else '-' + args.kv_dtype}"
+             f"{'' if args.q_dtype == 'same' else '-q' + args.q_dtype}.json")
     tfile = PROFILES / tname
     lib_sha = library_sha256()
     if tfile.exists():
@@ -346,7 +359,7 @@ def main():
         },
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline and args.kv_dtype == "same":  # the config dtype's baseline
+    if not args.no_cpu_baseline and args.kv_dtype == "same" and args.q_dtype == "same":
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

@@ -106,7 +106,8 @@ Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, i
   L.rows = static_cast<int64_t>(batch) * q_len * num_heads;
   L.slots = L.rows * L.max_parts;
   if (q_len == 1 && batch <= kSkMaxBatch) {
-    // Either stream-K shape (2-byte or fp8 cache: the size does not depend on the dtype).
+    // Either stream-K shape (2- or 4-byte or fp8 cache: the size does not depend on the
+    // dtype).
     const int RT = mfma_rows_per_tile(num_heads / num_kv_heads);
     const int units = num_kv_heads * ceil_div(num_heads / num_kv_heads, RT);
     for (const int waves : {sk_waves(2), sk_waves(1)}) {
@@ -250,6 +251,24 @@ hipError_t with_mfma_types(int q_dtype, int kv_dtype, F&& f) {
   return with_kv_type<_Float16>(kv_dtype, f);
 }
 
+// The decode kernels (partition and stream-K) also take an fp32 query over an fp32 cache,
+// the reference runner's default types (miniserve/model_runner.py:122-123): scores on
+// fp32 MFMAs, P.V on fp32 FMAs. Chunked prefill and the cascade's prefix pass keep the
+// generic kernel for it.
+bool mfma_decode_route_ok(const void* query, int q_dtype, int kv_dtype, int head_dim,
+                          int block_size, int64_t slot_stride) {
+  if (q_dtype == MSATTN_F32 && kv_dtype == MSATTN_F32)
+    return (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 &&
+           tile_span_ok(slot_stride, head_dim, kv_dtype) && aligned(query, 16);
+  return mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, slot_stride);
+}
+template <typename F>
+hipError_t with_mfma_decode_types(int q_dtype, int kv_dtype, F&& f) {
+  if (q_dtype != MSATTN_F32) return with_mfma_types(q_dtype, kv_dtype, f);
+  if (kv_dtype != MSATTN_F32) return hipErrorNotSupported;  // fp32 query: fp32 cache only
+  return f(float{}, float{});
+}
+
 int check_cache_args(const void* k_cache, const void* v_cache, int64_t blk, int64_t slot,
                      int64_t head, int kv_dtype, int block_size, int num_blocks, int table_width) {
   if (!k_cache || !v_cache) return MSATTN_ERR_INVALID_ARG;
@@ -327,10 +346,10 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
 
   const int G = num_heads / num_kv_heads;
   const int rows = q_len * G;
-  // MFMA path where mfma_route_ok allows it; everything else takes the generic kernel.
+  // MFMA path where mfma_decode_route_ok allows it; everything else takes the generic kernel.
   const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
-  const bool use_mfma = mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size,
-                                      cache_slot_stride);
+  const bool use_mfma = mfma_decode_route_ok(query, q_dtype, kv_dtype, head_dim, block_size,
+                                             cache_slot_stride);
   const int RT = use_mfma ? mfma_rows_per_tile(rows) : rows_per_tile(rows);
   char* ws = static_cast<char*>(workspace);
   SplitParams p;
@@ -386,7 +405,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
     p.sk_group = largest_pow2_divisor_upto(units, sk_waves(kv_fp8 ? 1 : 2));
     p.sk_unit_groups = units / p.sk_group;
     const int grid = device_cus() < 256 ? kSkGrid * device_cus() / 256 : kSkGrid;
-    e = with_mfma_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
+    e = with_mfma_decode_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
       return launch_decode_streamk<decltype(t), decltype(kt)>(p, head_dim, RT, grid, st, &sup);
     });
     if (!sup) return MSATTN_ERR_UNSUPPORTED;
@@ -394,7 +413,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   }
   *kind = 0;  // the partition kernels below
   if (use_mfma) {
-    e = with_mfma_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
+    e = with_mfma_decode_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
       return launch_decode_mfma<decltype(t), decltype(kt)>(p, head_dim, RT, st, &sup);
     });
   } else {

@@ -75,6 +75,58 @@ template <> struct Mfma16<_Float16> {
   }
 };
 
+// Eight fp32 values in two 16-byte halves: an fp32 cache's K/V chunk, and an fp32 query's.
+struct F8 {
+  uint4 lo, hi;
+};
+__device__ __forceinline__ void f8_unpack(const F8& x, float* o) {
+  const uint32_t w[8] = {x.lo.x, x.lo.y, x.lo.z, x.lo.w, x.hi.x, x.hi.y, x.hi.z, x.hi.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = __uint_as_float(w[e]);
+}
+__device__ __forceinline__ F8 f8_pack(const float* f) {
+  return F8{make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                       __float_as_uint(f[3])),
+            make_uint4(__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]),
+                       __float_as_uint(f[7]))};
+}
+
+// An fp32 query over an fp32 cache: a chunk's eight dims are eight k-steps of
+// v_mfma_f32_16x16x4_f32, lane group g supplying k-index g of each (A[n][g] =
+// K[token n][dim d0 + e], B[g][n] = Q[row n][dim d0 + e] with d0 the lane group's first
+// dim). Summed over the eight steps this is the same 16 x 16 tile of dot products, with
+// the layout of the 16x16x32 form, in fp32 products and sums (the reference computes
+// in fp32 there: attention.py:240-249 with an fp32 query).
+template <> struct Mfma16<float> {
+  __device__ static mf_f32x4 mac(const F8& a, const F8& b, mf_f32x4 c) {
+    float av[8], bv[8];
+    f8_unpack(a, av);
+    f8_unpack(b, bv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[e], c, 0, 0, 0);
+    return c;
+  }
+};
+
+// The query's MFMA B-operand chunk (eight dims of one row) for a query type: one 16-byte
+// load of bf16/fp16, two of fp32.
+template <typename T> struct QChunk {
+  typedef uint4 type;
+  __device__ static type zero() { return make_uint4(0u, 0u, 0u, 0u); }
+  __device__ static type load(const T* p) { return *reinterpret_cast<const uint4*>(p); }
+  __device__ static void unpack(const type& x, float* o) { Chunk<T>::unpack(x, o); }
+  __device__ static type pack(const float* f) { return Chunk<T>::pack(f); }
+};
+template <> struct QChunk<float> {
+  typedef F8 type;
+  __device__ static type zero() { return F8{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)}; }
+  __device__ static type load(const float* p) {
+    return F8{reinterpret_cast<const uint4*>(p)[0], reinterpret_cast<const uint4*>(p)[1]};
+  }
+  __device__ static void unpack(const type& x, float* o) { f8_unpack(x, o); }
+  __device__ static type pack(const float* f) { return f8_pack(f); }
+};
+
 // Value of `v` in lane 16 * (lane / 16) + N (DPP row_newbcast).
 template <int N>
 __device__ __forceinline__ float row_bcast(float v) {
@@ -269,9 +321,7 @@ template <typename T> struct Kv8<T, fp8_t> {
 // of T (dims 8 (4j + g)): the four lane groups of a row read 128 contiguous bytes per
 // chunk index.
 template <typename T> struct Kv8<T, float> {
-  struct raw_t {
-    uint4 lo, hi;
-  };
+  typedef F8 raw_t;
   __host__ __device__ static constexpr int qk_dim0(int j, int g, int /*JD*/) {
     return 8 * (4 * j + g);
   }
@@ -306,6 +356,32 @@ template <typename T> struct Kv8<T, float> {
   }
 };
 
+// An fp32 cache read by an fp32 query: the loads of Kv8<T, float>, kept in fp32 (the
+// reference's .to(query.dtype) is the identity there). The MFMA operand is the raw chunk
+// (Mfma16<float>), and P.V runs on fp32 FMAs.
+template <> struct Kv8<float, float> {
+  typedef F8 raw_t;
+  __host__ __device__ static constexpr int qk_dim0(int j, int g, int /*JD*/) {
+    return 8 * (4 * j + g);
+  }
+  template <int AUX>
+  __device__ static raw_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return raw_t{buffer_load16<AUX>(r, off), buffer_load16<AUX>(r, off + 16u)};
+  }
+  template <int AUX, int JD>
+  __device__ static void load_k(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int g,
+                                raw_t (&kb)[JD]) {
+#pragma unroll
+    for (int j = 0; j < JD; ++j)
+      kb[j] = load<AUX>(r, row_off + static_cast<uint32_t>(qk_dim0(j, g, JD)) * 4u);
+  }
+  __device__ static const F8& operand(const raw_t& x) { return x; }
+  __device__ static void unpack(const raw_t& x, float* o) { f8_unpack(x, o); }
+  __device__ static raw_t keep_if(const raw_t& x, bool keep) {
+    return keep ? x : raw_t{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+  }
+};
+
 #ifndef MSATTN_PV_DOT2
 #define MSATTN_PV_DOT2 1
 #endif
@@ -327,7 +403,9 @@ __device__ __forceinline__ void pv_tile(float (&acc)[RT][8], const float (&pr)[4
   constexpr int NJ = 16 / TPI;
   constexpr int APR = 16 / LPR;
   static_assert(NJ == D / 32, "V loads per tile");
-#if MSATTN_PV_DOT2
+  // An fp32 query keeps P and V in fp32: scalar FMAs.
+  constexpr bool kDot2 = MSATTN_PV_DOT2 && !std::is_same<T, float>::value;
+  if constexpr (kDot2) {
   static_assert(NJ % 2 == 0, "V loads pair up");
 #pragma unroll
   for (int i = 0; i < NJ / 2; ++i) {
@@ -351,7 +429,7 @@ __device__ __forceinline__ void pv_tile(float (&acc)[RT][8], const float (&pr)[4
       for (int e = 0; e < 8; ++e) acc[rn][e] = Dot2<T>::dot(pb, vp[e], acc[rn][e]);
     });
   }
-#else
+  } else {
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     float vf[8];
@@ -370,7 +448,7 @@ __device__ __forceinline__ void pv_tile(float (&acc)[RT][8], const float (&pr)[4
       for (int e = 0; e < 8; ++e) acc[rn][e] = fmaf(pb, vf[e], acc[rn][e]);
     });
   }
-#endif
+  }
 }
 
 // Workgroups of the partition kernel a CU may hold (0: as registers allow). Two on a CU
@@ -409,14 +487,14 @@ __host__ __device__ constexpr int tile_token(int i) {
 // the query (relative 2^-9 for bf16) is the only difference. Lanes l and l ^ 32 (the same
 // query row) are both active or both not.
 template <typename T, typename KT, int D>
-__device__ __forceinline__ void rope_chunks(uint4 (&qb)[D / 32], const float* cs, const float* sn,
-                                            int g) {
+__device__ __forceinline__ void rope_chunks(typename QChunk<T>::type (&qb)[D / 32], const float* cs,
+                                            const float* sn, int g) {
   constexpr int JD = D / 32;
   constexpr bool kCross = sizeof(KT) == 1 && D == 64;  // the partner is in the other half-wave
   float q[JD][8];
   float qp[JD][8];
 #pragma unroll
-  for (int j = 0; j < JD; ++j) Chunk<T>::unpack(qb[j], q[j]);
+  for (int j = 0; j < JD; ++j) QChunk<T>::unpack(qb[j], q[j]);
   if constexpr (kCross) {
     const bool lo = g < 2;
 #pragma unroll
@@ -450,7 +528,7 @@ __device__ __forceinline__ void rope_chunks(uint4 (&qb)[D / 32], const float* cs
         r = j < JD / 2 ? -q[j + JD / 2][e] : q[j - JD / 2][e];
       o[e] = rope_mix(q[j][e], r, c[e], sv[e]);
     }
-    qb[j] = Chunk<T>::pack(o);
+    qb[j] = QChunk<T>::pack(o);
   }
 }
 
@@ -566,13 +644,13 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   }
 
   // Query rows as the MFMA B operand: lane (g, n) holds Q[row n][dims 8*(4j+g) .. +8].
-  uint4 qb[JD];
+  typename QChunk<T>::type qb[JD];
   {
     const T* qp = static_cast<const T*>(p.q);
 #pragma unroll
     for (int j = 0; j < JD; ++j) {
-      qb[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (n < nrows) qb[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + KV::qk_dim0(j, g, JD));
+      qb[j] = QChunk<T>::zero();
+      if (n < nrows) qb[j] = QChunk<T>::load(qp + orow_n * D + KV::qk_dim0(j, g, JD));
     }
     if (p.rope_cos != nullptr && n < nrows) {
       const int64_t po = static_cast<int64_t>(rope_position(p, b)) * D;
@@ -788,6 +866,7 @@ MSATTN_DECLARE_MFMA_LAUNCHER(bf16_t, fp8_t)
 MSATTN_DECLARE_MFMA_LAUNCHER(_Float16, fp8_t)
 MSATTN_DECLARE_MFMA_LAUNCHER(bf16_t, float)
 MSATTN_DECLARE_MFMA_LAUNCHER(_Float16, float)
+MSATTN_DECLARE_MFMA_LAUNCHER(float, float)
 #undef MSATTN_DECLARE_MFMA_LAUNCHER
 
 }  // namespace msattn

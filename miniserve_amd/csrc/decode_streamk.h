@@ -240,13 +240,14 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
   };
   // The piece's query rows as the MFMA B operand (lane (g, n): row n, chunk j at dim
   // KV::qk_dim0(j, g), the split the K loads use).
-  auto load_q = [&](const Piece& pc, uint4 (&q)[JD]) __attribute__((always_inline)) {
+  typedef typename QChunk<T>::type qchunk_t;
+  auto load_q = [&](const Piece& pc, qchunk_t (&q)[JD]) __attribute__((always_inline)) {
     const T* qp = static_cast<const T*>(p.q);
     const int64_t orow_n = static_cast<int64_t>(pc.b) * p.H + pc.kvh * p.G + pc.row0 + n;
 #pragma unroll
     for (int j = 0; j < JD; ++j) {
-      q[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (n < pc.nrows) q[j] = *reinterpret_cast<const uint4*>(qp + orow_n * D + KV::qk_dim0(j, g, JD));
+      q[j] = QChunk<T>::zero();
+      if (n < pc.nrows) q[j] = QChunk<T>::load(qp + orow_n * D + KV::qk_dim0(j, g, JD));
     }
     if (p.rope_cos != nullptr && n < pc.nrows) {
       const int64_t po = static_cast<int64_t>(rope_position(p, pc.b)) * D;
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
   Piece cur = locate(s);
   int run0 = 0;
   int64_t my_base = table_run(cur, 0);
-  uint4 qb[JD];
+  qchunk_t qb[JD];
   load_q(cur, qb);
 
   float m_run = -INFINITY;
@@ -284,7 +285,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
     const bool next_piece = !more_here && cur.pe < s_end;
     Piece nxt = cur;
     int run_n = run0 + kSkTableRun;
-    uint4 qn[JD];
+    qchunk_t qn[JD];
     if (next_piece) {
       nxt = locate(cur.pe);
       run_n = 0;
@@ -471,6 +472,7 @@ MSATTN_DECLARE_SK_LAUNCHER(bf16_t, fp8_t)
 MSATTN_DECLARE_SK_LAUNCHER(_Float16, fp8_t)
 MSATTN_DECLARE_SK_LAUNCHER(bf16_t, float)
 MSATTN_DECLARE_SK_LAUNCHER(_Float16, float)
+MSATTN_DECLARE_SK_LAUNCHER(float, float)
 #undef MSATTN_DECLARE_SK_LAUNCHER
 
 #define MSATTN_SK_RT(T, KT, D)                                                      \

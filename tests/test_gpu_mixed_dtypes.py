@@ -72,7 +72,7 @@ def check(out: torch.Tensor, ref: np.ndarray, q_dtype) -> float:
 @pytest.mark.parametrize("q_dtype,kv_dtype", PAIRS)
 def test_decode_every_pair(device, q_dtype, kv_dtype, D):
     """Decode (partition kernels: MFMA for a bf16/fp16 query over its own type, fp8 or
-    fp32, the generic kernel for the rest) against the oracle with the cast; a row of
+    fp32 and for an fp32 query over fp32, the generic kernel for the rest) against the oracle with the cast; a row of
     context 1 returns exactly V[0] as the query type holds it."""
     H, KVH = 8, 2
     lens = [1, 17, 300, 1000, 0, 64]

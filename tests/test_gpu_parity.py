@@ -285,7 +285,9 @@ def rope_unfused(q, cos, sin, pos):
     (32, 8, 128, torch.bfloat16, torch.bfloat16, True),    # stream-K MFMA kernel
     (14, 2, 64, torch.bfloat16, torch.bfloat16, False),    # partition MFMA kernel
     (28, 4, 128, torch.float16, torch.float16, False),     # partition MFMA kernel, fp16
-    (4, 2, 64, torch.float32, torch.float32, False),       # generic kernel, fp32
+    (4, 2, 64, torch.float32, torch.float32, False),       # partition MFMA kernel, fp32
+    (32, 8, 128, torch.float32, torch.float32, True),      # stream-K MFMA kernel, fp32
+    (4, 2, 96, torch.float32, torch.float32, False),       # generic kernel, fp32
     (8, 2, 96, torch.bfloat16, torch.float8_e4m3fn, False),  # generic kernel, fp8 KV
     # fp8 KV on the MFMA kernels: the query's chunks follow the fp8 split of the head dims,
     # so the rotate-half partner comes from the other half-wave
@@ -424,6 +426,51 @@ def test_mfma_routes_fuzz(device):
         assert err < BF16_REL, f"fuzz #{i}: max-rel {err}"
 
 
+def test_mfma_fp32_routes_fuzz(device):
+    """Seeded shapes for an fp32 query over an fp32 cache (the reference runner's types,
+    miniserve/model_runner.py:120-123): partition and stream-K decode and short q_len on
+    the fp32 MFMA decode kernels, chunked prefill and cascade decode on the generic kernel;
+    head_dim 64/128, pages of 16..64 tokens, windows; each within max-abs 1e-4 of the
+    float64 oracle."""
+    for i in range(24):
+        gen = torch.Generator().manual_seed(7000 + i)
+        pick = lambda seq: seq[int(torch.randint(0, len(seq), (1,), generator=gen))]
+        D = pick((64, 128))
+        KVH = pick((1, 2, 4, 8))
+        G = pick((1, 2, 4, 5, 7, 8, 16))
+        H = KVH * G
+        bs = pick((16, 32, 48, 64))
+        B = int(torch.randint(1, 5, (1,), generator=gen))
+        route = pick(("decode", "decode", "wide", "wide", "short", "prefill", "cascade"))
+        q_len = {"short": int(torch.randint(2, 4, (1,), generator=gen)),
+                 "prefill": int(torch.randint(8, 41, (1,), generator=gen))}.get(route, 1)
+        lens = [int(torch.randint(1, 1500, (1,), generator=gen)) for _ in range(B)]
+        window = pick((None, None, 64, 300)) if route != "cascade" else None
+        pages = max((L + bs - 1) // bs for L in lens)
+        width = pages + 2
+        if route == "wide":
+            width = max(width, -(-65536 * 16 // (B * KVH * bs)))
+        prefix = 0
+        if route == "cascade":
+            prefix = int(torch.randint(1, max(2, min(lens) // bs + 2), (1,), generator=gen))
+            width = max(width, prefix + 1)
+        note(f"fp32 fuzz #{i} {route} B={B} H={H} KVH={KVH} D={D} q_len={q_len} bs={bs} "
+             f"width={width} window={window} prefix={prefix} lens={lens}")
+        if prefix:
+            q, kc, vc, table = shared_prefix_case(H, KVH, D, lens, torch.float32, bs, prefix,
+                                                  width, seed=i)
+        else:
+            q, kc, vc, table = paged_case(H, KVH, D, lens, torch.float32, bs, width, seed=i,
+                                          q_len=q_len)
+        kw = dict(window=window, max_context=width * bs)
+        if prefix:
+            kw["prefix_pages"] = prefix
+        out = run_hip(device, q, kc, vc, table, lens, **kw)
+        ref = dense.paged_attention_f64(q, kc, vc, table, lens, window=window)
+        err = abs_err(out, ref)
+        assert err < FP32_ATOL, f"fp32 fuzz #{i}: max-abs {err}"
+
+
 # ------------------------------------------------------------------ edge cases
 
 def test_ragged_zero_and_one(device):
@@ -545,6 +592,8 @@ def wide_table_case(H, KVH, D, lens, dtype, width_pages, seed):
     (32, 8, 128, torch.bfloat16, 100),     # windowed decode
     (8, 8, 64, torch.bfloat16, None),      # MHA, G = 1
     (32, 1, 128, torch.bfloat16, None),    # MQA, G = 32: two row tiles per KV head
+    (32, 8, 128, torch.float32, None),     # fp32 query over an fp32 cache
+    (14, 2, 64, torch.float32, 100),       # fp32, head_dim 64, windowed
 ])
 def test_streamk_decode(device, H, KVH, D, dtype, window):
     lens = [0, 1, 16, 17, 300, 1234, 77, 4096, 5, 2048, 999, 33]
@@ -553,9 +602,14 @@ def test_streamk_decode(device, H, KVH, D, dtype, window):
     q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=H + D)
     out = run_hip(device, q, kc, vc, table, lens, window=window, max_context=width * 16)
     ref = dense.paged_attention_f64(q, kc, vc, table, lens, window=window)
-    err = rel_err(out, ref)
-    note(f"stream-K max-rel {err:.3e}")
-    assert err < BF16_REL
+    if dtype == torch.float32:
+        err = abs_err(out, ref)
+        note(f"stream-K max-abs {err:.3e}")
+        assert err < FP32_ATOL
+    else:
+        err = rel_err(out, ref)
+        note(f"stream-K max-rel {err:.3e}")
+        assert err < BF16_REL
     assert not out[0].any()  # context 0 -> zeros
     for h in range(H):      # context 1 -> V[0] of the row's KV head (rounded to dtype)
         assert torch.equal(out[1, 0, h].cpu(), vc[table[1, 0], 0, h // (H // KVH)])

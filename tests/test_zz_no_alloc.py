@@ -3,7 +3,8 @@
 Called through the C ABI (ctypes) and compared with the workspace entry point on the
 same inputs: two calls in a row, the second with a smaller batch and shorter contexts
 (so the scratch still holds the first call's partials), on the stream-K decode, the
-partition decode, the generic kernel (fp32) and the direct prefill route; the results
+partition decode (bf16 and fp32), the generic kernel (fp32, head_dim 96) and the direct
+prefill route; the results
 must be bit-identical (the same kernels run) and within the float64 oracle's bar. A
 geometry whose workspace exceeds the scratch is refused before any work.
 """
@@ -82,7 +83,8 @@ CASES = {  # name -> (H, KVH, D, dtype, q_len, first lens, second lens, width in
                  [900, 33, 4000], 1024),
     "partition": (14, 2, 64, torch.bfloat16, 1, [1500, 300, 2048, 77, 1024, 640],
                   [100, 1800], 128),
-    "generic fp32": (14, 2, 64, torch.float32, 1, [400, 130, 512, 9], [200, 35], 32),
+    "partition fp32": (14, 2, 64, torch.float32, 1, [400, 130, 512, 9], [200, 35], 32),
+    "generic fp32": (14, 2, 96, torch.float32, 1, [400, 130, 512, 9], [200, 35], 32),
     "prefill": (28, 4, 128, torch.bfloat16, 64, [512, 700], [64], 48),
 }
 
