@@ -4,7 +4,8 @@
                     [--kv-fp8] [--no-cascade] [--prefill] [--graph-steps G]
 
 A step is one layer's paged-attention decode over the whole batch (split-K
-partials kernel + merge kernel), replayed from a captured hipGraph with the
+partials kernel + merge kernel; one launch where the partition kernel merges
+in-kernel), replayed from a captured hipGraph with the
 block tables, context lengths, workspace and output in static device buffers.
 The default workload is BASELINE.json's headline config C3 (Llama-3-8B
 attention geometry, bf16, batch 64, context log-uniform in [1024, 8192]); C2
@@ -57,7 +58,7 @@ def parse():
     ap.add_argument("--q-dtype", choices=["same", "fp32"], default="same",
                     help="the query (and output) in fp32 instead of the config dtype; with "
                          "--kv-dtype fp32 this is the reference runner's default pair "
-                         "(model_runner.py:122-123), which takes the generic kernel")
+                         "(model_runner.py:122-123), on the fp32 MFMA decode kernels")
     ap.add_argument("--no-cascade", action="store_true",
                     help="decode a shared-prefix workload (config 4) in one pass per sequence "
                          "instead of the cascade entry point")
@@ -200,7 +201,7 @@ def main():
     if cascade:
         ws_bytes = lib.msattn_prefix_workspace_bytes(B, H, KVH, D, bs, max_ctx, cascade)
     part_tokens = lib.msattn_partition_tokens(B, 1, H, KVH, D, max_ctx)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # merge tickets start at zero
     outs = [torch.empty_like(q) for _ in range(w.layers)]
     qcode, kvcode = nat.dtype_code(w.dtype), nat.dtype_code(w.k_caches[0].dtype)
 
@@ -243,9 +244,12 @@ def main():
           file=sys.stderr, flush=True)
 
     # Dominant kernel: the partials kernel, bracketed by HIP events on the stream it
-    # is launched on (torch's current stream), over its own timed loop.
+    # is launched on (torch's current stream), over its own timed loop. A decode that
+    # merges in-kernel (workspace kind 2 after the step) is one launch: the whole
+    # msattn_paged_attention call is timed instead, and the merge column is 0.
     stream = nat.stream_handle(dev)
     kc, vc = w.k_caches[0], w.v_caches[0]
+    fused = not cascade and int(ws[:4].view(torch.int32).item()) == 2
     n_k = max(10, min(args.steps, 200))
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
             torch.cuda.Event(enable_timing=True)) for _ in range(n_k)]
@@ -253,6 +257,17 @@ def main():
         e = evs[i - 5] if i >= 5 else None
         if e:
             e[0].record()
+        if fused:
+            st = lib.msattn_paged_attention(
+                q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
+                kc.stride(2), table.data_ptr(), lens.data_ptr(), outs[0].data_ptr(),
+                ws.data_ptr(), ws_bytes, B, 1, H, KVH, D, bs, w.num_blocks, W, max_ctx, 1, 0,
+                w.scale, qcode, kvcode, stream)
+            nat.check("fused decode", st)
+            if e:
+                e[1].record()
+                e[2].record()
+            continue
         st = lib.msattn_paged_attention_partials(
             q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
             table.data_ptr(), lens.data_ptr(), ws.data_ptr(), ws_bytes, B, 1, H, KVH, D, bs,
@@ -275,7 +290,9 @@ def main():
     mfma_pair = ((w.dtype in (torch.bfloat16, torch.float16)
                   and kv_t in (w.dtype, torch.float8_e4m3fn, torch.float32))
                  or (w.dtype == torch.float32 and kv_t == torch.float32))
-    if kind == 1:
+    if fused:
+        kernel_name = "msattn::decode_mfma_kernel (partition split-K, merged in-kernel)"
+    elif kind == 1:
         kernel_name = "msattn::decode_streamk_kernel (stream-K split-K partials)"
     elif mfma_pair and D in (64, 128):
         kernel_name = "msattn::decode_mfma_kernel (partition split-K partials)"
@@ -284,7 +301,7 @@ def main():
     split_ms = sorted(a.elapsed_time(b) for a, b, _ in evs)
     merge_ms = sorted(b.elapsed_time(c) for _, b, c in evs)
     split_avg = sum(split_ms) / len(split_ms)
-    merge_avg = sum(merge_ms) / len(merge_ms)
+    merge_avg = 0.0 if fused else sum(merge_ms) / len(merge_ms)
 
     per_layer_bytes = w.algorithmic_bytes(unique=True)
     layer_us = ms_per_step * 1e3 / w.layers

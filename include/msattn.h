@@ -69,7 +69,11 @@ int msattn_partition_tokens(int batch, int q_len, int num_heads, int num_kv_head
 /*
  * Bytes of caller-owned device workspace msattn_paged_attention needs (a size
  * that depends on the geometry only). Replaces the per-call torch.empty partial buffers of
- * kernels/paged_attn_triton.py:320-323.
+ * kernels/paged_attn_triton.py:320-323. A workspace must be all zeros when it is first
+ * used (allocate it zeroed once): its header holds the arrival counters of the in-kernel
+ * merge at a fixed offset, and every call leaves them zero, so one workspace serves any
+ * sequence of calls and geometries that fit it. Calls that share a workspace must not
+ * overlap in time.
  */
 size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_heads,
                               int head_dim, int max_context);
@@ -93,11 +97,15 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
  * head) runs on the MFMA kernels for a bf16/fp16 query over a cache of its type, fp8 e4m3
  * or fp32, and for an fp32 query over an fp32 cache (head_dim 64 or 128, 16-byte aligned
  * query, block_size a multiple of 16); other pairs and shapes take the generic kernel.
- * Runs msattn_paged_attention_partials followed by
- * msattn_merge_partials, except for chunked prefill on the MFMA kernel (bf16/fp16 query
- * 16-byte aligned, output 8-byte aligned, cache of the query's type, fp8 e4m3 or fp32,
- * head_dim 64 or 128, more than 16 query rows per KV head), which writes the output
- * directly.
+ * Runs msattn_paged_attention_partials followed by msattn_merge_partials, except:
+ * chunked prefill on the MFMA kernel (bf16/fp16 query 16-byte aligned, output 8-byte
+ * aligned, cache of the query's type, fp8 e4m3 or fp32, head_dim 64 or 128, more than 16
+ * query rows per KV head), which writes the output directly; and decodes on the MFMA
+ * partition kernel (those below the stream-K threshold, with batch x num_kv_heads x row
+ * tiles <= 4096), which merge in-kernel in one launch: the last partition of each
+ * (sequence, KV head, row tile) to finish folds the others' partials into `out`, and a
+ * sequence of one partition writes `out` directly. The partials kernel's rounding and
+ * the fold are those of the two-launch path, with the fold's sums in another order.
  */
 int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
                            int64_t cache_block_stride, int64_t cache_slot_stride,

@@ -269,7 +269,8 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     ``max_context`` bounds context_lens; when context_lens is a device tensor
     and it is None, the table capacity (width * block_size) is used so that no
     device->host read happens (the call is then safe to capture in a graph).
-    ``workspace``/``out`` let a caller pass preallocated buffers.
+    ``workspace``/``out`` let a caller pass preallocated buffers; a workspace must be
+    zero when first used (``torch.zeros``), and every call leaves it reusable.
     ``rope`` = (cos, sin, position) applies rotate-half RoPE to a decode query inside
     the attention kernels (cos/sin [max_pos, head_dim], position [batch] or a scalar;
     kernels/paged_attn_triton.py:211-220).
@@ -327,7 +328,8 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     if ws_bytes == 0:
         raise ValueError("unsupported attention geometry")
     if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        # zeroed: the in-kernel merge's tickets must start at zero (calls leave them so)
+        workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
     if out is None:
         out = torch.empty((B, q_len, H, D), dtype=query.dtype, device=dev)
     args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),

@@ -32,6 +32,11 @@ constexpr int64_t kTargetSlots = MSATTN_TARGET_SLOTS;  // workgroup slots wanted
 #endif
 // Decode launches whose (batch x KV heads x table tiles) reach this use stream-K.
 constexpr int64_t kStreamKMinTiles = MSATTN_STREAMK_MIN_TILES;
+#ifndef MSATTN_FUSED_MERGE
+#define MSATTN_FUSED_MERGE 1
+#endif
+// 1: msattn_paged_attention's partition-kernel decodes merge in-kernel (no merge launch).
+constexpr bool kFusedMerge = MSATTN_FUSED_MERGE != 0;
 
 bool dtype_ok(int d) { return d >= MSATTN_F32 && d <= MSATTN_FP8_E4M3; }
 int dtype_bytes(int d) { return d == MSATTN_F32 ? 4 : (d == MSATTN_FP8_E4M3 ? 1 : 2); }
@@ -329,7 +334,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
                   int q_len, int num_heads, int num_kv_heads, int head_dim, int block_size,
                   int num_blocks, int table_width, int max_context, int causal, int window,
                   float scale, int q_dtype, int kv_dtype, const RopeArgs& rope, int key_lo,
-                  int* kind, void* stream) {
+                  int* kind, void* stream, void* fused_out = nullptr) {
   *kind = -1;
   if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
@@ -388,6 +393,8 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   p.rope_sin = rope.sin;
   p.rope_pos = rope.pos;
   p.rope_max_pos = rope.max_pos;
+  p.out = nullptr;
+  p.tickets = nullptr;
   const int64_t gx = static_cast<int64_t>(p.max_parts) * num_kv_heads * p.rtiles;
   if (gx >= (int64_t(1) << 31) || batch > 65535) return MSATTN_ERR_UNSUPPORTED;
 
@@ -412,6 +419,15 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
     return hip_status(e);
   }
   *kind = 0;  // the partition kernels below
+  // With an output to write, the MFMA partition kernel merges in-kernel (the last
+  // partition of each (sequence, KV head, row tile) to finish folds the others in), so
+  // no merge launch follows; it needs one header ticket per such triple.
+  if (use_mfma && fused_out != nullptr && key_lo == 0 && kFusedMerge &&
+      static_cast<int64_t>(batch) * num_kv_heads * p.rtiles <= kMaxTickets) {
+    *kind = 2;
+    p.out = fused_out;
+    p.tickets = p.hdr + kHdrTickets;
+  }
   if (use_mfma) {
     e = with_mfma_decode_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
       return launch_decode_mfma<decltype(t), decltype(kt)>(p, head_dim, RT, st, &sup);
@@ -578,8 +594,9 @@ int attention_impl(const void* query, const void* k_cache, const void* v_cache,
       query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
       block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
       num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
-      scale, q_dtype, kv_dtype, RopeArgs{nullptr, nullptr, nullptr, 0}, 0, &kind, stream);
+      scale, q_dtype, kv_dtype, RopeArgs{nullptr, nullptr, nullptr, 0}, 0, &kind, stream, out);
   if (rc != MSATTN_OK) return rc;
+  if (kind == 2) return MSATTN_OK;  // merged in-kernel
   return merge_impl(workspace, workspace_bytes, context_lens, out, batch, q_len, num_heads,
                     num_kv_heads, head_dim, max_context, q_dtype, nullptr, nullptr, 0, kind, stream);
 }
@@ -682,8 +699,9 @@ int msattn_paged_attention_rope(const void* query, const void* k_cache, const vo
       block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
       num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
       scale, q_dtype, kv_dtype, RopeArgs{rope_cos, rope_sin, position, max_position}, 0, &kind,
-      stream);
+      stream, out);
   if (rc != MSATTN_OK) return rc;
+  if (kind == 2) return MSATTN_OK;  // merged in-kernel
   return merge_impl(workspace, workspace_bytes, context_lens, out, batch, q_len, num_heads,
                     num_kv_heads, head_dim, max_context, q_dtype, nullptr, nullptr, 0, kind, stream);
 }

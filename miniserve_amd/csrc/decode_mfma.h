@@ -200,6 +200,27 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Device-scope coherent accesses: agent-scope atomic loads and stores, vector memory
+// instructions with cache policy SC1. A store is written through to the memory every XCD
+// reads, and a load does not take a line that another XCD may have changed from this
+// XCD's L2 (each XCD has its own L2, not coherent with the others). Partials exchanged
+// between workgroups inside one launch go through these, so publishing them needs only
+// their completion (s_waitcnt vmcnt(0)), not a writeback of the whole L2.
+constexpr int kWaitVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt and lgkmcnt not waited
+
+__device__ __forceinline__ void store2_device(float* p, float a, float b) {  // p: 8-byte aligned
+  const uint64_t v = static_cast<uint64_t>(__float_as_uint(a)) |
+                     (static_cast<uint64_t>(__float_as_uint(b)) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load2_device(const float* p) {  // p: 8-byte aligned
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float(static_cast<uint32_t>(v)),
+                     __uint_as_float(static_cast<uint32_t>(v >> 32)));
+}
+
 typedef float mf_f32x2 __attribute__((ext_vector_type(2)));
 
 // Eight consecutive K/V elements per lane. A cache of the compute type T loads 16
@@ -546,6 +567,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
 
   __shared__ float s_red[kMfmaWaves][RT][D];
   __shared__ float s_ml[kMfmaWaves][RT][2];
+  __shared__ int s_last;  // in-kernel merge: this workgroup arrived last
   // LDS reserved beyond s_red / s_ml so that at most kMfmaWgPerCu workgroups share a
   // CU (the store below never runs; it keeps the array allocated).
   constexpr int kLdsUsed = static_cast<int>(sizeof(s_red) + sizeof(s_ml));
@@ -563,7 +585,11 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   const int va = lane / LPR; // V token group
   const int vc = lane % LPR; // V 16-byte chunk
 
-  if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) p.hdr[kHdrKind] = 0;
+  // In-kernel merge: the partition workgroups of a (sequence, KV head, row tile) count
+  // themselves in on a header ticket; the last one folds every partial into the output.
+  // A sequence of one partition writes its output directly.
+  const bool fused = p.out != nullptr;
+  if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) p.hdr[kHdrKind] = fused ? 2 : 0;
   // blockIdx.x = kvh + KVH * (part + max_parts * rtile); blockIdx.z = b.
   const unsigned bx = blockIdx.x;
   const int kvh = static_cast<int>(bx % static_cast<unsigned>(p.KVH));
@@ -612,7 +638,99 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     orow_n = (static_cast<int64_t>(b) * p.q_len + i) * p.H + (kvh * p.G + (gr - i * p.G));
   }
 
+  const bool direct = fused && nparts == 1;
+  constexpr int D4 = D / 4;
+  auto out_row = [&](int r) -> int64_t __attribute__((always_inline)) {
+    const int gr = row0 + r;
+    const int i = gr / p.G;
+    return (static_cast<int64_t>(b) * p.q_len + i) * p.H + (kvh * p.G + (gr - i * p.G));
+  };
+  auto store_out4 = [&](int64_t orow, int d, float4 a, float inv) __attribute__((always_inline)) {
+    T* o = static_cast<T*>(p.out) + orow * D + d;
+    Elt<T>::store(o + 0, a.x * inv);
+    Elt<T>::store(o + 1, a.y * inv);
+    Elt<T>::store(o + 2, a.z * inv);
+    Elt<T>::store(o + 3, a.w * inv);
+  };
+  // The in-kernel merge's second half: wait for this workgroup's device-scope partial
+  // stores, take the ticket, and if every other partition of the row tile is in, fold
+  // the nparts partials (slots 0 .. nparts - 1 of each row) into the output and leave the
+  // ticket at zero for the next call. The fold is the merge kernel's: running max M,
+  // weights 2^(m_j - M), out = sum w_j acc_j / sum w_j l_j; partials with m = -inf
+  // (no key) carry no weight and their acc is not read into the sum.
+  auto fused_merge = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    if (tid == 0) {
+      int* t = p.tickets + ((static_cast<int64_t>(b) * p.KVH + kvh) * p.rtiles + rtile);
+      const int old = __hip_atomic_fetch_add(t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = old == nparts - 1;
+      if (last) __hip_atomic_store(t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    for (int idx = tid; idx < nrows * D4; idx += kMfmaThreads) {
+      const int r = idx / D4;
+      const int d = (idx - r * D4) * 4;
+      const int64_t orow = out_row(r);
+      const float* mlr = p.ml + orow * p.max_parts * 2;
+      const float* ar = p.acc + orow * p.max_parts * D + d;
+      float M = -INFINITY, L = 0.0f;
+      float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      constexpr int kBatch = 8;
+      for (int j0 = 0; j0 < nparts; j0 += kBatch) {
+        float2 xlo[kBatch], xhi[kBatch];
+        float mv[kBatch], lv[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {  // slots past nparts repeat the last one, unused
+          const int j = j0 + u < nparts ? j0 + u : nparts - 1;
+          const float2 ml = load2_device(mlr + 2 * j);
+          mv[u] = j0 + u < nparts ? ml.x : -INFINITY;
+          lv[u] = ml.y;
+          xlo[u] = load2_device(ar + static_cast<int64_t>(j) * D);
+          xhi[u] = load2_device(ar + static_cast<int64_t>(j) * D + 2);
+        }
+        float mb = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) mb = fmaxf(mb, mv[u]);
+        if (mb == -INFINITY) continue;
+        const float Mn = fmaxf(M, mb);
+        const float alpha = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M = -inf
+        L *= alpha;
+        a.x *= alpha;
+        a.y *= alpha;
+        a.z *= alpha;
+        a.w *= alpha;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          if (mv[u] == -INFINITY) continue;
+          const float wj = __builtin_amdgcn_exp2f(mv[u] - Mn);
+          L = fmaf(wj, lv[u], L);
+          a.x = fmaf(wj, xlo[u].x, a.x);
+          a.y = fmaf(wj, xlo[u].y, a.y);
+          a.z = fmaf(wj, xhi[u].x, a.z);
+          a.w = fmaf(wj, xhi[u].y, a.w);
+        }
+        M = Mn;
+      }
+      store_out4(orow, d, a, L > 0.0f ? 1.0f / L : 0.0f);
+    }
+  };
+
   if (a1 <= a0) {
+    if (direct) {  // no key in the only partition: zeros
+      for (int idx = tid; idx < nrows * D4; idx += kMfmaThreads) {
+        const int r = idx / D4;
+        store_out4(out_row(r), (idx - r * D4) * 4, make_float4(0.0f, 0.0f, 0.0f, 0.0f), 0.0f);
+      }
+      return;
+    }
+    if (fused) {
+      if (tid < nrows) store2_device(p.ml + (orow_n * p.max_parts + part) * 2, -INFINITY, 0.0f);
+      fused_merge();
+      return;
+    }
     if (tid < nrows) {
       float* ml = p.ml + (orow_n * p.max_parts + part) * 2;
       ml[0] = -INFINITY;
@@ -790,7 +908,6 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   __syncthreads();
 
   // Combine the waves, four dims a thread: rescale each wave to the common max.
-  constexpr int D4 = D / 4;
   for (int idx = tid; idx < nrows * D4; idx += kMfmaThreads) {
     const int r = idx / D4;
     const int d = (idx - r * D4) * 4;
@@ -814,11 +931,24 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
         a.w = fmaf(v.w, f, a.w);
       }
     }
-    const int gr = row0 + r;
-    const int i = gr / p.G;
-    const int64_t orow = (static_cast<int64_t>(b) * p.q_len + i) * p.H + (kvh * p.G + (gr - i * p.G));
-    *reinterpret_cast<float4*>(p.acc + (orow * p.max_parts + part) * D + d) = a;
+    const int64_t orow = out_row(r);
+    if (direct) {  // the only partition: normalise and write the output
+      float L = 0.0f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int ww = 0; ww < kMfmaWaves; ++ww)
+          if (mw[ww] != -INFINITY) L = fmaf(s_ml[ww][r][1], __builtin_amdgcn_exp2f(mw[ww] - M), L);
+      }
+      store_out4(orow, d, a, L > 0.0f ? 1.0f / L : 0.0f);
+    } else if (fused) {
+      float* slot = p.acc + (orow * p.max_parts + part) * D + d;
+      store2_device(slot, a.x, a.y);
+      store2_device(slot + 2, a.z, a.w);
+    } else {
+      *reinterpret_cast<float4*>(p.acc + (orow * p.max_parts + part) * D + d) = a;
+    }
   }
+  if (direct) return;
   if (tid < nrows) {
     float M = -INFINITY;
 #pragma unroll
@@ -832,13 +962,18 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
       }
     }
     float* ml = p.ml + (orow_n * p.max_parts + part) * 2;
-    ml[0] = M;
-    ml[1] = L;
-    if (part + 1 == nparts && nparts < p.max_parts) {  // end marker
-      ml[2] = -INFINITY;
-      ml[3] = -1.0f;
+    if (fused) {
+      store2_device(ml, M, L);
+    } else {
+      ml[0] = M;
+      ml[1] = L;
+      if (part + 1 == nparts && nparts < p.max_parts) {  // end marker
+        ml[2] = -INFINITY;
+        ml[3] = -1.0f;
+      }
     }
   }
+  if (fused) fused_merge();
 }
 
 template <typename T, typename KT, int D, int RT>

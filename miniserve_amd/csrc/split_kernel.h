@@ -49,10 +49,16 @@ constexpr int kPartMax = MSATTN_PART_MAX;
 // Workspace header (first bytes of every workspace): which partial layout the
 // partials kernel used, so the merge can read it back.
 //   hdr[0] kind: 0 = per-row slots closed by end markers (partition kernels);
-//                1 = stream-K pieces (decode_streamk.h)
+//                1 = stream-K pieces (decode_streamk.h);
+//                2 = partition kernel that merged in-kernel and wrote the output
 //   kind 1 also: hdr[1] sumT, [2] chunk c, [3] sub-ranges, [4] UG, [5] NUG, [6] B,
 //   [7] RT, and hdr[kHdrPrefix + b] = tiles of sequences before b (b = 0..B).
-constexpr int kHdrPrefix = 64;
+//   hdr[kHdrTickets + t], t < kMaxTickets: arrival counters of the in-kernel merge, one
+//   per (sequence, KV head, row tile). They sit at the same offset for every geometry,
+//   must be zero when a workspace is first used, and every call leaves them zero.
+constexpr int kHdrTickets = 64;
+constexpr int kMaxTickets = 4096;
+constexpr int kHdrPrefix = kHdrTickets + kMaxTickets;
 constexpr int kHdrKind = 0, kHdrSumT = 1, kHdrChunk = 2, kHdrNsub = 3, kHdrUG = 4,
               kHdrNUG = 5, kHdrB = 6, kHdrRT = 7;
 
@@ -84,6 +90,11 @@ struct SplitParams {
   const float* rope_sin;
   const int32_t* rope_pos;
   int rope_max_pos;
+  // In-kernel merge (partition MFMA kernel only): non-null `out` [rows][D] of the query
+  // type makes the last partition of each (sequence, KV head, row tile) to arrive merge
+  // its partials and write the output; `tickets` are the header's arrival counters.
+  void* out;
+  int* tickets;
 };
 
 // Position of row b's query for RoPE, clamped into the tables.

@@ -45,7 +45,8 @@ def test_abi_version_and_status_strings():
 def test_partition_policy(B, q_len, H, KVH, D, ctx, part):
     lib = nat.lib()
     assert lib.msattn_partition_tokens(B, q_len, H, KVH, D, ctx) == part
-    # header: 64 ints + B + 1 prefix sums; slots: rows x (partitions + end marker),
+    # header: 64 ints, 4096 merge tickets, B + 1 prefix sums; slots: rows x (partitions
+    # + end marker),
     # or stream-K pieces x UG x RT if larger: pieces = chunks + NUG x B, chunks at
     # most 256 workgroups x waves / UG and at most tiles / 4, for the larger of the
     # two stream-K shapes (4 waves for a 2-byte cache, 8 for fp8)
@@ -61,7 +62,7 @@ def test_partition_policy(B, q_len, H, KVH, D, ctx, part):
             segments = units // UG * B
             chunks = min(256 * waves // UG, -(-(segments * -(-ctx // 16)) // 4))
             slots = max(slots, (chunks + segments) * UG * RT)
-    expect = r256(4 * (64 + B + 1)) + r256(slots * 2 * 4) + slots * D * 4
+    expect = r256(4 * (64 + 4096 + B + 1)) + r256(slots * 2 * 4) + slots * D * 4
     assert lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) == expect
 
 

@@ -1,0 +1,178 @@
+"""GPU parity of the in-kernel merge of the partition decode kernel.
+
+msattn_paged_attention runs small decodes (the partition MFMA kernel) as one launch: the
+last partition workgroup of each (sequence, KV head, row tile) to arrive folds the
+others' partials into the output, and a sequence of one partition writes its output
+directly. The partials travel between workgroups (and XCDs) through device-coherent
+stores and loads, and the arrival counters live in the workspace header.
+
+Checked here, over several consecutive calls on one workspace (so stale partials and
+counters of an earlier call would show): the output against the float64 oracle (fp32
+max-abs 1e-4, bf16/fp16 max-rel 2e-2) and against the two-launch path of the same
+partials (msattn_paged_attention_partials + msattn_merge_partials; the fold's summation
+order differs, so fp32 within 1e-5 relative and bf16/fp16 within two units of the last
+place of the output type), that the workspace's counters are all zero after each call,
+and that the workspace header names the in-kernel route (kind 2).
+"""
+import numpy as np
+import pytest
+import torch
+
+from miniserve_amd import _native as nat
+from oracle import dense
+
+pytestmark = pytest.mark.gpu
+
+FP32_ATOL = 1e-4
+BF16_REL = 2e-2
+HDR_TICKETS, MAX_TICKETS = 64, 4096
+
+
+def note(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+
+
+def make(H, KVH, D, lens, dtype, width, seed, q_len=1):
+    g = torch.Generator().manual_seed(seed)
+    pool = sum((L + 15) // 16 for L in lens) + 3
+    q = torch.randn(len(lens), q_len, H, D, generator=g).to(dtype)
+    kc = torch.randn(pool, 16, KVH, D, generator=g).to(dtype)
+    vc = torch.randn(pool, 16, KVH, D, generator=g).to(dtype)
+    perm = torch.randperm(pool, generator=g)
+    table = torch.zeros(len(lens), width, dtype=torch.int32)
+    cur = 0
+    for b, L in enumerate(lens):
+        n = (L + 15) // 16
+        table[b, :n] = perm[cur:cur + n].to(torch.int32)
+        cur += n
+    return q, kc, vc, table
+
+
+class Caller:
+    """One workspace reused by every call (zeroed once), and a separate one for the
+    two-launch path."""
+
+    def __init__(self, device, nbytes):
+        self.device = device
+        self.ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        self.ws2 = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+    def run(self, q, kc, vc, table, lens, window=0):
+        lib = nat.lib()
+        dev = self.device
+        B, q_len, H, D = q.shape
+        nb, bs, KVH, _ = kc.shape
+        max_ctx = table.shape[1] * bs
+        ws_bytes = lib.msattn_workspace_bytes(B, q_len, H, KVH, D, max_ctx)
+        assert 0 < ws_bytes <= self.ws.numel()
+        qd, kcd, vcd = q.to(dev), kc.to(dev), vc.to(dev)
+        td, ld = table.to(dev), torch.tensor(lens, dtype=torch.int32, device=dev)
+        common = (qd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), kcd.stride(0), kcd.stride(1),
+                  kcd.stride(2), td.data_ptr(), ld.data_ptr())
+        qc, kvc = nat.dtype_code(q.dtype), nat.dtype_code(kc.dtype)
+        tail = (B, q_len, H, KVH, D, bs, nb, table.shape[1], max_ctx, 1, window,
+                1.0 / D ** 0.5, qc, kvc)
+        stream = nat.stream_handle(dev)
+        fused = torch.full_like(qd, float("nan"))
+        st = lib.msattn_paged_attention(*common, fused.data_ptr(), self.ws.data_ptr(),
+                                        ws_bytes, *tail, stream)
+        assert st == nat.OK, st
+        two = torch.full_like(qd, float("nan"))
+        st = lib.msattn_paged_attention_partials(*common, self.ws2.data_ptr(), ws_bytes, *tail,
+                                                 stream)
+        assert st == nat.OK, st
+        st = lib.msattn_merge_partials(self.ws2.data_ptr(), ws_bytes, ld.data_ptr(),
+                                       two.data_ptr(), B, q_len, H, KVH, D, max_ctx, qc, stream)
+        assert st == nat.OK, st
+        torch.cuda.synchronize()
+        hdr = self.ws[: 4 * (HDR_TICKETS + MAX_TICKETS)].view(torch.int32).cpu()
+        return fused, two, hdr
+
+
+def check(fused, two, hdr, q, kc, vc, table, lens, window=None):
+    assert int(hdr[0]) == 2, f"workspace kind {int(hdr[0])}: not the in-kernel merge"
+    assert not hdr[HDR_TICKETS:].any(), "merge counters not left at zero"
+    assert not torch.isnan(fused).any()
+    ref = dense.paged_attention_f64(q, kc, vc, table.long(), lens, window=window)
+    f = fused.double().cpu().numpy()
+    t = two.double().cpu().numpy()
+    if q.dtype == torch.float32:
+        err = float(np.abs(f - ref).max())
+        assert err < FP32_ATOL, err
+        diff = float(np.abs(f - t).max() / max(np.abs(t).max(), 1e-30))
+        assert diff < 1e-5, diff
+    else:
+        err = float(np.abs(f - ref).max() / max(np.abs(ref).max(), 1e-30))
+        assert err < BF16_REL, err
+        ulp = 2.0 ** (-7 if q.dtype == torch.bfloat16 else -10)
+        assert np.all(np.abs(f - t) <= 2 * ulp * np.maximum(np.abs(t), 2.0 ** -14)), \
+            float(np.abs(f - t).max())
+    note(f"oracle err {err:.3e}")
+
+
+CASES = {  # name -> (H, KVH, D, dtype, width in pages)
+    "C2 geometry bf16": (14, 2, 64, torch.bfloat16, 128),
+    "C5 geometry bf16": (28, 4, 128, torch.bfloat16, 240),
+    "fp32 (runner default)": (14, 2, 64, torch.float32, 64),
+    "fp16 MHA": (8, 8, 128, torch.float16, 64),
+    "MQA two row tiles": (32, 1, 128, torch.bfloat16, 64),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_fused_merge_consecutive_calls(device, name):
+    """Five calls on one workspace with new data and lengths each time: empty, one-token
+    and one-partition sequences (direct output) beside many-partition ones."""
+    H, KVH, D, dtype, width = CASES[name]
+    caller = Caller(device, 64 << 20)
+    for i in range(5):
+        g = torch.Generator().manual_seed(100 * i + H)
+        B = int(torch.randint(3, 33, (1,), generator=g))
+        cap = width * 16
+        lens = [int(x) for x in torch.randint(0, cap + 1, (B,), generator=g)]
+        lens[0], lens[1] = 0, 1
+        lens[2] = int(torch.randint(2, 60, (1,), generator=g))  # one partition
+        note(f"fused {name} call {i}: B={B} lens={lens}")
+        q, kc, vc, table = make(H, KVH, D, lens, dtype, width, seed=i + 7 * H)
+        fused, two, hdr = caller.run(q, kc, vc, table, lens)
+        check(fused, two, hdr, q, kc, vc, table, lens)
+        assert not fused[0].cpu().any()  # context 0 -> zeros
+
+
+def test_fused_merge_window_and_short_q(device):
+    """Windowed decode (partitions below the window hold no key and carry no weight) and
+    q_len 2 (speculative rows, causal) through the in-kernel merge."""
+    caller = Caller(device, 64 << 20)
+    H, KVH, D, width = 14, 2, 64, 128
+    lens = [2000, 700, 1, 1500, 33, 0, 1999]
+    for window, q_len in ((100, 1), (600, 1), (0, 2)):
+        note(f"fused window={window} q_len={q_len}")
+        q, kc, vc, table = make(H, KVH, D, lens, torch.bfloat16, width, seed=window + q_len,
+                                q_len=q_len)
+        if q_len > 1:
+            lens_q = [max(L, q_len) for L in lens]
+            q, kc, vc, table = make(H, KVH, D, lens_q, torch.bfloat16, width, seed=5,
+                                    q_len=q_len)
+        else:
+            lens_q = lens
+        fused, two, hdr = caller.run(q, kc, vc, table, lens_q, window=window)
+        check(fused, two, hdr, q, kc, vc, table, lens_q, window=window or None)
+
+
+def test_stream_k_leaves_counters_alone(device):
+    """A stream-K decode (wide table) on the same workspace neither uses nor disturbs the
+    merge counters, and a partition decode after it still merges correctly."""
+    lib = nat.lib()
+    caller = Caller(device, 256 << 20)
+    H, KVH, D = 32, 8, 128
+    lens = [3000, 17, 5000, 0, 800, 4096, 1, 2500]
+    q, kc, vc, table = make(H, KVH, D, lens, torch.bfloat16, 1024, seed=3)
+    fused, two, hdr = caller.run(q, kc, vc, table, lens)
+    assert int(hdr[0]) == 1  # stream-K: the merge kernel ran
+    assert not hdr[HDR_TICKETS:].any()
+    assert torch.equal(fused, two)
+    lens = [300, 1200, 0, 64]
+    q, kc, vc, table = make(14, 2, 64, lens, torch.bfloat16, 80, seed=4)
+    fused, two, hdr = caller.run(q, kc, vc, table, lens)
+    check(fused, two, hdr, q, kc, vc, table, lens)
+    assert lib is nat.lib()

@@ -653,7 +653,7 @@ def test_streamk_graph_replays(device):
     sq = q.to(device)
     stable = table.to(device=device, dtype=torch.int32)
     slens = torch.tensor(lens, dtype=torch.int32, device=device)
-    ws = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+    ws = torch.zeros(256 << 20, dtype=torch.uint8, device=device)
     out = torch.empty_like(sq)
     cap = width * 16
 
@@ -875,7 +875,7 @@ def test_cascade_graph_replays(device):
     sq = q.to(device)
     stable = table.to(device=device, dtype=torch.int32)
     slens = torch.tensor(lens, dtype=torch.int32, device=device)
-    ws = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+    ws = torch.zeros(256 << 20, dtype=torch.uint8, device=device)
     out = torch.empty_like(sq)
     cap = width * bs
 
@@ -990,7 +990,7 @@ def test_graph_capture_replay(device):
     static_lens = torch.tensor(lens, dtype=torch.int32, device=device)
     cap = table.shape[1] * bs
     ws_bytes = 64 << 20
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=device)
     out = torch.empty_like(static_q)
 
     def step():

@@ -68,7 +68,7 @@ def test_c2_all_layers_in_one_graph(device):
     cap = table.shape[1] * bs
     q = w.query.contiguous()
     from miniserve_amd import _native as nat
-    ws = torch.empty(nat.lib().msattn_workspace_bytes(B, 1, H, KVH, D, cap), dtype=torch.uint8,
+    ws = torch.zeros(nat.lib().msattn_workspace_bytes(B, 1, H, KVH, D, cap), dtype=torch.uint8,
                      device=dev)
     outs = [torch.empty_like(q) for _ in range(w.layers)]
 

@@ -51,7 +51,7 @@ def call_both(device, q, kc, vc, table, lens, max_ctx):
     td = table.to(device)
     ld = torch.tensor(lens, dtype=torch.int32, device=device)
     ws_bytes = lib.msattn_workspace_bytes(B, q_len, H, KVH, D, max_ctx)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=device)
     out_ws = torch.full_like(qd, float("nan"))
     out_na = torch.full_like(qd, float("nan"))
     scale = 1.0 / D ** 0.5
