@@ -64,7 +64,8 @@ def parse():
                          "instead of the cascade entry point")
     ap.add_argument("--prefill", action="store_true",
                     help="C5's chunked-prefill part (2 x 512 query tokens onto 4096 cached): "
-                         "MFMA-bound, reported in TFLOP/s")
+                         "MFMA-bound, reported in TFLOP/s; with --q-dtype fp32 --kv-dtype fp32 "
+                         "the reference runner's types, priced against the fp32 matrix peak")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--stream-probe", action="store_true",
@@ -385,17 +386,25 @@ def prefill_bench(args):
     """C5 prefill: one forward over 2 x 512 query rows, captured in a hipGraph."""
     import torch
 
+    from miniserve_amd import _native as nat
     from miniserve_amd.attention import paged_attention
     from miniserve_amd.workloads import make_workload
 
     dev = torch.device("cuda:0")
     w = make_workload(5, device=dev, values_device=dev, part="prefill")
+    if args.q_dtype == "fp32":
+        w.query = w.query.float()
+    kv_torch = {"fp8": torch.float8_e4m3fn, "fp32": torch.float32}.get(args.kv_dtype)
+    if kv_torch is not None:
+        w.k_caches = [c.to(kv_torch) for c in w.k_caches]
+        w.v_caches = [c.to(kv_torch) for c in w.v_caches]
     B, T, H, D = w.query.shape
     table = w.table.to(device=dev, dtype=torch.int32).contiguous()
     lens = torch.tensor(w.lens, dtype=torch.int32, device=dev)
     cap = table.shape[1] * w.block_size
     out = torch.empty_like(w.query)
-    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    ws_bytes = nat.lib().msattn_workspace_bytes(B, T, H, w.num_kv_heads, D, cap)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
 
     def step():
         paged_attention(w.query, w.k_caches[0], w.v_caches[0], table, lens, max_context=cap,
@@ -429,18 +438,69 @@ def prefill_bench(args):
     # causal: row i of a sequence with context L sees L - T + i + 1 keys
     flops = sum(4 * D * H * (L - T + i + 1) for L in w.lens for i in range(T) if L - T + i + 1 > 0)
     tflops = flops / (ms * 1e-3) / 1e12
+    fp32 = w.query.dtype == torch.float32
+    # MI355X dense matrix peaks: bf16 2.5 PFLOP/s, fp32 157.3 TFLOP/s.
+    peak = 157.3 if fp32 else 2500.0
+    kernel = ("msattn::decode_mfma_kernel (fp32, 16-row tiles, P.V on the matrix core, "
+              "merged in-kernel)" if fp32 and w.k_caches[0].dtype == torch.float32
+              else "msattn::prefill_mfma_kernel")
     print(json.dumps({
         "metric": "C5 chunked-prefill attention (2 x 512 tokens onto 4096 cached)",
         "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
-        "dtype": "bf16", "data": "synthetic: seeded N(0,1) q/K/V, scattered block tables",
+        "dtype": "f32" if fp32 else "bf16",
+        "data": "synthetic: seeded N(0,1) q/K/V, scattered block tables",
         "config": {"workload": "C5-prefill", "batch": B, "q_len": T, "num_heads": H,
                    "num_kv_heads": w.num_kv_heads, "head_dim": D, "flops": flops,
+                   "kv_dtype": str(w.k_caches[0].dtype).replace("torch.", ""),
                    "steps_per_graph": gsteps, "us_per_step_one_per_graph": round(ms_single * 1e3, 2)},
-        "roofline": {"kernel": "msattn::prefill_mfma_kernel", "bound": "mfma",
-                     "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": round(tflops / 2500.0, 4), "traffic": None},
+        "roofline": {"kernel": kernel, "bound": "mfma",
+                     "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4), "traffic": None},
+        "reference_gpu": reference_prefill_us(w, table, lens, T),
     }), flush=True)
+
+
+def reference_prefill_us(w, table, lens, T) -> dict:
+    """The reference's own forward for this call, restated in torch on the same GPU and
+    timed with events: gather every row's K/V up to the longest context through the block
+    table, expand the KV heads to the query heads, causal mask over the context, and
+    scaled_dot_product_attention in the query dtype (miniserve/attention.py:155-171,
+    :235-250). Eager, as the reference runs it."""
+    import torch
+    import torch.nn.functional as F
+
+    dev = w.query.device
+    B, _, H, D = w.query.shape
+    KVH = w.num_kv_heads
+    max_l = max(w.lens)
+    tl = table.long()
+    pos = torch.arange(max_l, device=dev)
+    L = lens.long()
+    q_pos = L[:, None] - T + torch.arange(T, device=dev)[None, :]
+    mask = ((pos[None, None, :] <= q_pos[:, :, None]) & (pos[None, None, :] < L[:, None, None]))[:, None]
+    kc, vc = w.k_caches[0], w.v_caches[0]
+
+    def forward():
+        pages = tl[:, pos // w.block_size]
+        slots = (pos % w.block_size)[None, :]
+        k = kc[pages, slots].to(w.query.dtype).repeat_interleave(H // KVH, dim=2).transpose(1, 2)
+        v = vc[pages, slots].to(w.query.dtype).repeat_interleave(H // KVH, dim=2).transpose(1, 2)
+        return F.scaled_dot_product_attention(w.query.transpose(1, 2), k, v, attn_mask=mask)
+
+    for _ in range(3):
+        forward()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    n = 10
+    for _ in range(n):
+        forward()
+    stop.record()
+    torch.cuda.synchronize()
+    return {"us": round(start.elapsed_time(stop) / n * 1e3, 1),
+            "what": "the reference's forward (block-table gather, GQA expand, masked SDPA) "
+                    "restated in torch, eager, on this GPU"}
 
 
 def library_sha256() -> str:

@@ -427,6 +427,20 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
     *kind = 2;
     p.out = fused_out;
     p.tickets = p.hdr + kHdrTickets;
+    // The fp32 16-row route (P.V on the matrix core; its kernel unrolls kPartLongF32
+    // tokens per workgroup) takes partitions of up to kPartLongF32 tokens when the grid
+    // still reaches kTargetSlots: chunked prefill. Only the in-kernel merge reads these
+    // slots, so their count may shrink to the partitions launched.
+    if (MSATTN_PV_MFMA32 && q_dtype == MSATTN_F32 && kv_dtype == MSATTN_F32 && RT == 16) {
+      const int np = ceil_div(max_context, kPartLongF32);
+      const int step = 16 * kMfmaWaves;
+      const int part_l = ceil_div(ceil_div(max_context, np), step) * step;
+      if (part_l > p.part &&
+          static_cast<int64_t>(np) * num_kv_heads * p.rtiles * batch >= kTargetSlots) {
+        p.part = part_l;
+        p.max_parts = np;
+      }
+    }
   }
   if (use_mfma) {
     e = with_mfma_decode_types(q_dtype, kv_dtype, [&](auto t, auto kt) {

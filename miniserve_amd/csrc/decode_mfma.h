@@ -406,6 +406,11 @@ template <> struct Kv8<float, float> {
 #ifndef MSATTN_PV_DOT2
 #define MSATTN_PV_DOT2 1
 #endif
+// P.V of an fp32 query over an fp32 cache at 16 query rows per tile on the matrix core
+// (v_mfma_f32_16x16x4_f32) instead of fp32 FMAs: chunked prefill and G >= 16 decodes.
+#ifndef MSATTN_PV_MFMA32
+#define MSATTN_PV_MFMA32 1
+#endif
 
 // P.V of one 16-token tile on the VALU, for the decode kernels. Lane (g, n) holds the
 // weights pr[r] of query row n for tokens tile_token(4g + r); V lane (va, vc) holds, for
@@ -484,6 +489,15 @@ constexpr int kCuLdsBytes = 160 * 1024;  // gfx950 LDS per CU
 constexpr int kMfmaWaves = MSATTN_MFMA_WAVES;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
 constexpr int kMaxTilesPerWave = kPartMax / 16 / kMfmaWaves;  // partitions are <= kPartMax tokens
+// Partition of the fp32 16-row route (MFMA P.V) when it merges in-kernel over a large grid
+// (chunked prefill): longer partitions spread each workgroup's start, epilogue and merge
+// over more tiles. Its kernel unrolls this many tiles per wave.
+#ifndef MSATTN_PART_LONG_F32
+#define MSATTN_PART_LONG_F32 2048
+#endif
+constexpr int kPartLongF32 = MSATTN_PART_LONG_F32;
+static_assert(kPartLongF32 % (16 * kMfmaWaves) == 0 && kPartLongF32 / (16 * kMfmaWaves) <= 64,
+              "whole tiles per wave, page ids in one lane each");
 
 // Token (within a 16-token tile) whose score lands in MFMA row i = 4g + r.
 template <int D>
@@ -788,11 +802,42 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   const KT* kbase = static_cast<const KT*>(p.k);
   const KT* vbase = static_cast<const KT*>(p.v);
 
+  // P.V on the matrix core (fp32 query and cache, a full 16-row tile): O = P V as
+  // v_mfma_f32_16x16x4_f32 steps. Step r takes, in lane (g, n), A = P[row n][token
+  // tile_token(4g + r)] (the lane's own weight pr[r], where the scores landed) and
+  // B = V[that token][dim]; lane (g, n) loads 16 bytes of that token's row, dims
+  // 64 h + 4 n .. + 3, and element e of them feeds output block (h, e), whose column n
+  // is dim 64 h + 4 n + e. Output lane (g', n') then holds rows 4 g' .. 4 g' + 3 of dims
+  // 64 h + 4 n' + e: a float4 of consecutive dims per (row, h).
+  constexpr bool kPvMfma = MSATTN_PV_MFMA32 && std::is_same<T, float>::value &&
+                           std::is_same<KT, float>::value && RT == 16;
+  constexpr int NH = D / 64;         // 16-byte V loads per token step
+  constexpr int NVQ = 4 * NH;        // V loads per tile (MFMA P.V)
+  constexpr int NOB = 4 * NH;        // 16x16 output blocks (MFMA P.V)
+  uint32_t v_mfma_off[kPvMfma ? NVQ : 1];
+  if constexpr (kPvMfma) {
+    static_assert(NVQ == 2 * NJ, "the V ring holds the MFMA P.V loads");
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+        v_mfma_off[r * NH + h] = static_cast<uint32_t>(
+            (tile_token<D>(4 * g + r) * p.slot_stride + 64 * h + 4 * n) * EB);
+  }
+  // Tiles a wave may own: partitions of the fp32 16-row route reach kPartLongF32 tokens.
+  constexpr int kMaxT = kPvMfma ? kPartLongF32 / 16 / kMfmaWaves : kMaxTilesPerWave;
+  mf_f32x4 acc_o[kPvMfma ? NOB : 1];
+  if constexpr (kPvMfma) {
+#pragma unroll
+    for (int q = 0; q < NOB; ++q) acc_o[q] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
   float m_run = -INFINITY;
   float l_run = 0.0f;
-  float acc[RT][8];
+  constexpr int RTA = kPvMfma ? 1 : RT;  // rows of the FMA accumulator
+  float acc[RTA][8];
 #pragma unroll
-  for (int r = 0; r < RT; ++r)
+  for (int r = 0; r < RTA; ++r)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
 
@@ -809,8 +854,17 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
     const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
     KV::template load_k<0, JD>(rk, k_row_off, g, kb);
+    if constexpr (kPvMfma) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) vb[j] = KV::template load<0>(rv, v_lane_off[j]);
+      for (int q = 0; q < NVQ; ++q) {
+        const uint4 x = buffer_load16<0>(rv, v_mfma_off[q]);
+        if (q % 2 == 0) vb[q / 2].lo = x;
+        else vb[q / 2].hi = x;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) vb[j] = KV::template load<0>(rv, v_lane_off[j]);
+    }
   };
 
   auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) __attribute__((always_inline)) {
@@ -842,18 +896,50 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     l_run = fmaf(l_run, alpha, psum);
     m_run = m_new;
 
+    // Rows outside the tile's key range (partial tiles) may hold anything, even
+    // NaN: their values are replaced by zeros before the weights meet them.
+    const bool partial = t0 < a0 || t0 + 16 > a1;
+    if constexpr (kPvMfma) {
+      // alpha of output rows 4g .. 4g + 3 (row rr's alpha sits in lane rr).
+      if (!MSATTN_LAZY_RESCALE || __any(alpha != 1.0f)) {
+        float al[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          al[i] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), __float_as_int(alpha)));
+#pragma unroll
+        for (int q = 0; q < NOB; ++q)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc_o[q][i] *= al[i];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bool keep = true;
+        if (partial) {
+          const int vtok = t0 + tile_token<D>(4 * g + r);
+          keep = vtok >= a0 && vtok < a1;
+        }
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+          const int q = r * NH + h;
+          const uint4 x = q % 2 == 0 ? vb[q / 2].lo : vb[q / 2].hi;
+          const float xv[4] = {keep ? __uint_as_float(x.x) : 0.0f, keep ? __uint_as_float(x.y) : 0.0f,
+                               keep ? __uint_as_float(x.z) : 0.0f, keep ? __uint_as_float(x.w) : 0.0f};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc_o[4 * h + e] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], xv[e], acc_o[4 * h + e], 0, 0, 0);
+        }
+      }
+      return;
+    }
     // alpha is exactly 1 for every row whose running max did not move.
     if (!MSATTN_LAZY_RESCALE || __any(alpha != 1.0f)) {
-      static_for<RT>([&](auto nc) {
+      static_for<RTA>([&](auto nc) {
         constexpr int rn = decltype(nc)::value;
         const float al = row_bcast<rn>(alpha);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[rn][e] *= al;
       });
     }
-    // Rows outside the tile's key range (partial tiles) may hold anything, even
-    // NaN: their values are replaced by zeros before the weights meet them.
-    const bool partial = t0 < a0 || t0 + 16 > a1;
     raw_t vm[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -863,12 +949,12 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
         vm[j] = KV::keep_if(vm[j], vtok >= a0 && vtok < a1);
       }
     }
-    pv_tile<T, KT, D, RT>(acc, pr, vm, va);
+    pv_tile<T, KT, D, RTA>(acc, pr, vm, va);
   };
 
   // A ring of DEPTH tiles: the loads of DEPTH - 1 tiles are in flight while one is
-  // consumed. The sequence is fully unrolled (a wave owns at most kMaxTilesPerWave
-  // tiles) so every wait for a tile's loads is exact; loads for tiles at or past nt read
+  // consumed. The sequence is fully unrolled (a wave owns at most kMaxT tiles) so
+  // every wait for a tile's loads is exact; loads for tiles at or past nt read
   // nothing (their descriptors have no records).
   constexpr int DEPTH = D == 64 ? MSATTN_MFMA_DEPTH_D64 : MSATTN_MFMA_DEPTH;
   raw_t kr[DEPTH][JD], vr[DEPTH][NJ];
@@ -878,11 +964,11 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     br[d] = tile_base(d);
     issue(br[d], kr[d], vr[d]);
   });
-  static_for<kMaxTilesPerWave>([&](auto kc) {
+  static_for<kMaxT>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
     if (k >= nt) return;
     constexpr int nx = k + DEPTH - 1;  // the tile whose loads go out now
-    if constexpr (nx < kMaxTilesPerWave) {
+    if constexpr (nx < kMaxT) {
       br[nx % DEPTH] = tile_base(nx);
       issue(br[nx % DEPTH], kr[nx % DEPTH], vr[nx % DEPTH]);
     }
@@ -893,17 +979,26 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   // lane % LPR), reduce-scattered so a lane keeps two dims of each row: dims
   // vc * 8 + 2 * share + {0, 1}.
   l_run = rows4_sum(l_run);
-  float red[RT * 2];
-  reduce_scatter<LPR>(acc, red);
   if (lane < RT) {
     s_ml[w][lane][0] = m_run;
     s_ml[w][lane][1] = l_run;
   }
-  if (rs_owner<LPR>(lane)) {
-    const int d0 = vc * 8 + 2 * rs_share<LPR>(lane);
+  if constexpr (kPvMfma) {  // the matrix core summed the wave's tokens already
 #pragma unroll
-    for (int r = 0; r < RT; ++r)
-      *reinterpret_cast<float2*>(&s_red[w][r][d0]) = make_float2(red[2 * r], red[2 * r + 1]);
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(&s_red[w][4 * g + i][64 * h + 4 * n]) =
+            make_float4(acc_o[4 * h][i], acc_o[4 * h + 1][i], acc_o[4 * h + 2][i], acc_o[4 * h + 3][i]);
+  } else {
+    float red[RTA * 2];
+    reduce_scatter<LPR>(acc, red);
+    if (rs_owner<LPR>(lane)) {
+      const int d0 = vc * 8 + 2 * rs_share<LPR>(lane);
+#pragma unroll
+      for (int r = 0; r < RTA; ++r)
+        *reinterpret_cast<float2*>(&s_red[w][r][d0]) = make_float2(red[2 * r], red[2 * r + 1]);
+    }
   }
   __syncthreads();
 

@@ -176,3 +176,19 @@ def test_stream_k_leaves_counters_alone(device):
     fused, two, hdr = caller.run(q, kc, vc, table, lens)
     check(fused, two, hdr, q, kc, vc, table, lens)
     assert lib is nat.lib()
+
+
+@pytest.mark.parametrize("D,window", [(128, 0), (64, 0), (128, 700)])
+def test_fp32_prefill_long_partitions(device, D, window):
+    """fp32 chunked prefill large enough (grid of >= 512 workgroups) for the fp32 16-row
+    route's long partitions (up to 2048 tokens a workgroup, P.V on the matrix core, merged
+    in-kernel): against the float64 oracle and the two-launch path, whose partitions are
+    512 tokens, on two consecutive calls."""
+    caller = Caller(device, 64 << 20)
+    H, KVH, q_len, width = 16, 4, 200, 256  # 800 rows per KV head: 50 row tiles
+    for i, lens in enumerate(([2500, 3100], [4096, 333])):
+        note(f"fp32 long prefill D={D} window={window} call {i}: lens={lens}")
+        q, kc, vc, table = make(H, KVH, D, lens, torch.float32, width, seed=D + i,
+                                q_len=q_len)
+        fused, two, hdr = caller.run(q, kc, vc, table, lens, window=window)
+        check(fused, two, hdr, q, kc, vc, table, lens, window=window or None)
