@@ -376,7 +376,11 @@ def main():
             "frac_of_stream_read": round(achieved / read_ceiling, 4),
         },
         "cpu_baseline": None,
+        "reference_gpu": None,
     }
+    ref = reference_forward_us(w, table, lens, 1)
+    ref["speedup"] = round(ref["us"] / layer_us, 1)
+    result["reference_gpu"] = ref
     if not args.no_cpu_baseline and args.kv_dtype == "same" and args.q_dtype == "same":
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -457,16 +461,16 @@ def prefill_bench(args):
         "roofline": {"kernel": kernel, "bound": "mfma",
                      "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(tflops / peak, 4), "traffic": None},
-        "reference_gpu": reference_prefill_us(w, table, lens, T),
+        "reference_gpu": reference_forward_us(w, table, lens, T),
     }), flush=True)
 
 
-def reference_prefill_us(w, table, lens, T) -> dict:
+def reference_forward_us(w, table, lens, T) -> dict:
     """The reference's own forward for this call, restated in torch on the same GPU and
     timed with events: gather every row's K/V up to the longest context through the block
     table, expand the KV heads to the query heads, causal mask over the context, and
     scaled_dot_product_attention in the query dtype (miniserve/attention.py:155-171,
-    :235-250). Eager, as the reference runs it."""
+    :235-250), over the first layer's caches. Eager, as the reference runs it."""
     import torch
     import torch.nn.functional as F
 
