@@ -95,9 +95,9 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
  * narrowing), as the reference casts the gathered K/V to query.dtype
  * (miniserve/attention.py:240-241). Decode (q_len 1, or at most 16 query rows per KV
  * head) runs on the MFMA kernels for a bf16/fp16 query over a cache of its type, fp8 e4m3
- * or fp32, and for an fp32 query over an fp32 cache (head_dim 64 or 128, 16-byte aligned
- * query, block_size a multiple of 16), whose chunked prefill (more than 16 query rows per
- * KV head) also runs there; other pairs and shapes take the generic kernel.
+ * or fp32, and for an fp32 query over any cache (head_dim 64 or 128, 16-byte aligned
+ * query, block_size a multiple of 16); an fp32 query's chunked prefill (more than 16 query
+ * rows per KV head) also runs there. Other pairs and shapes take the generic kernel.
  * Runs msattn_paged_attention_partials followed by msattn_merge_partials, except:
  * chunked prefill on the MFMA kernel (bf16/fp16 query 16-byte aligned, output 8-byte
  * aligned, cache of the query's type, fp8 e4m3 or fp32, head_dim 64 or 128, more than 16

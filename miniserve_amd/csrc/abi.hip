@@ -256,13 +256,15 @@ hipError_t with_mfma_types(int q_dtype, int kv_dtype, F&& f) {
   return with_kv_type<_Float16>(kv_dtype, f);
 }
 
-// The decode kernels (partition and stream-K) also take an fp32 query over an fp32 cache,
-// the reference runner's default types (miniserve/model_runner.py:122-123): scores on
-// fp32 MFMAs, P.V on fp32 FMAs. Chunked prefill and the cascade's prefix pass keep the
-// generic kernel for it.
+// The decode kernels (partition and stream-K) also take an fp32 query over any cache:
+// an fp32 cache is the reference runner's default (miniserve/model_runner.py:122-123), and
+// its fp8 kv_dtype (miniserve/attention.py:151-152) under the runner's fp32 model gives an
+// fp32 query over fp8. Scores on fp32 MFMAs over the cache widened exactly to fp32; P.V on
+// fp32 FMAs, or fp32 MFMAs at 16 rows per tile over an fp32 cache. The cascade's prefix
+// pass keeps the generic kernel for an fp32 query.
 bool mfma_decode_route_ok(const void* query, int q_dtype, int kv_dtype, int head_dim,
                           int block_size, int64_t slot_stride) {
-  if (q_dtype == MSATTN_F32 && kv_dtype == MSATTN_F32)
+  if (q_dtype == MSATTN_F32)
     return (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 &&
            tile_span_ok(slot_stride, head_dim, kv_dtype) && aligned(query, 16);
   return mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, slot_stride);
@@ -270,8 +272,13 @@ bool mfma_decode_route_ok(const void* query, int q_dtype, int kv_dtype, int head
 template <typename F>
 hipError_t with_mfma_decode_types(int q_dtype, int kv_dtype, F&& f) {
   if (q_dtype != MSATTN_F32) return with_mfma_types(q_dtype, kv_dtype, f);
-  if (kv_dtype != MSATTN_F32) return hipErrorNotSupported;  // fp32 query: fp32 cache only
-  return f(float{}, float{});
+  switch (kv_dtype) {
+    case MSATTN_F32: return f(float{}, float{});
+    case MSATTN_BF16: return f(float{}, bf16_t{});
+    case MSATTN_F16: return f(float{}, _Float16{});
+    case MSATTN_FP8_E4M3: return f(float{}, fp8_t{});
+    default: return hipErrorNotSupported;
+  }
 }
 
 int check_cache_args(const void* k_cache, const void* v_cache, int64_t blk, int64_t slot,
@@ -409,7 +416,8 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   if (use_mfma && q_len == 1 && batch <= kSkMaxBatch && tile_capacity >= kStreamKMinTiles) {
     *kind = 1;
     const int units = num_kv_heads * p.rtiles;
-    p.sk_group = largest_pow2_divisor_upto(units, sk_waves(kv_fp8 ? 1 : 2));
+    p.sk_group = largest_pow2_divisor_upto(
+        units, sk_waves(kv_fp8 ? 1 : 2, q_dtype == MSATTN_F32 ? 4 : 2));
     p.sk_unit_groups = units / p.sk_group;
     const int grid = device_cus() < 256 ? kSkGrid * device_cus() / 256 : kSkGrid;
     e = with_mfma_decode_types(q_dtype, kv_dtype, [&](auto t, auto kt) {

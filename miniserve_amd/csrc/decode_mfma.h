@@ -112,19 +112,34 @@ template <> struct Mfma16<float> {
 // load of bf16/fp16, two of fp32.
 template <typename T> struct QChunk {
   typedef uint4 type;
+  static constexpr int kWords = 4;
   __device__ static type zero() { return make_uint4(0u, 0u, 0u, 0u); }
   __device__ static type load(const T* p) { return *reinterpret_cast<const uint4*>(p); }
   __device__ static void unpack(const type& x, float* o) { Chunk<T>::unpack(x, o); }
   __device__ static type pack(const float* f) { return Chunk<T>::pack(f); }
+  __device__ static void words(const type& x, uint32_t (&w)[kWords]) {
+    w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+  }
+  __device__ static type from_words(const uint32_t (&w)[kWords]) {
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
 };
 template <> struct QChunk<float> {
   typedef F8 type;
+  static constexpr int kWords = 8;
   __device__ static type zero() { return F8{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)}; }
   __device__ static type load(const float* p) {
     return F8{reinterpret_cast<const uint4*>(p)[0], reinterpret_cast<const uint4*>(p)[1]};
   }
   __device__ static void unpack(const type& x, float* o) { f8_unpack(x, o); }
   __device__ static type pack(const float* f) { return f8_pack(f); }
+  __device__ static void words(const type& x, uint32_t (&w)[kWords]) {
+    w[0] = x.lo.x; w[1] = x.lo.y; w[2] = x.lo.z; w[3] = x.lo.w;
+    w[4] = x.hi.x; w[5] = x.hi.y; w[6] = x.hi.z; w[7] = x.hi.w;
+  }
+  __device__ static type from_words(const uint32_t (&w)[kWords]) {
+    return F8{make_uint4(w[0], w[1], w[2], w[3]), make_uint4(w[4], w[5], w[6], w[7])};
+  }
 };
 
 // Value of `v` in lane 16 * (lane / 16) + N (DPP row_newbcast).
@@ -377,6 +392,25 @@ template <typename T> struct Kv8<T, float> {
   }
 };
 
+// A bf16/fp16 or fp8 cache read by an fp32 query: the loads and head-dim split of the
+// cache's own kernels (Kv8<KT, KT>, Kv8<bf16_t, fp8_t>), widened exactly to fp32 once
+// they arrive: the reference's .to(query.dtype) of the gathered rows
+// (miniserve/attention.py:240-241), so the scores run on fp32 MFMAs (Mfma16<float>) and
+// P.V on fp32 FMAs over the cache's own values.
+template <typename KT> struct Kv8Widened
+    : Kv8<typename std::conditional<std::is_same<KT, fp8_t>::value, bf16_t, KT>::type, KT> {
+  typedef Kv8<typename std::conditional<std::is_same<KT, fp8_t>::value, bf16_t, KT>::type, KT> Base;
+  typedef typename Base::raw_t raw_t;
+  __device__ static F8 operand(const raw_t& x) {
+    float o[8];
+    Base::unpack(x, o);  // exact: every bf16, fp16 and e4m3 value is an fp32 value
+    return f8_pack(o);
+  }
+};
+template <> struct Kv8<float, bf16_t> : Kv8Widened<bf16_t> {};
+template <> struct Kv8<float, _Float16> : Kv8Widened<_Float16> {};
+template <> struct Kv8<float, fp8_t> : Kv8Widened<fp8_t> {};
+
 // An fp32 cache read by an fp32 query: the loads of Kv8<T, float>, kept in fp32 (the
 // reference's .to(query.dtype) is the identity there). The MFMA operand is the raw chunk
 // (Mfma16<float>), and P.V runs on fp32 FMAs.
@@ -534,14 +568,15 @@ __device__ __forceinline__ void rope_chunks(typename QChunk<T>::type (&qb)[D / 3
     const bool lo = g < 2;
 #pragma unroll
     for (int j = 0; j < JD; ++j) {
-      const uint32_t w[4] = {qb[j].x, qb[j].y, qb[j].z, qb[j].w};
-      uint32_t o[4];
+      constexpr int NW = QChunk<T>::kWords;
+      uint32_t w[NW], o[NW];
+      QChunk<T>::words(qb[j], w);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < NW; ++k) {
         const auto t = __builtin_amdgcn_permlane32_swap(w[k], w[k], false, false);
         o[k] = lo ? t[1] : t[0];
       }
-      Chunk<T>::unpack(make_uint4(o[0], o[1], o[2], o[3]), qp[j]);
+      QChunk<T>::unpack(QChunk<T>::from_words(o), qp[j]);
     }
   }
 #pragma unroll
@@ -1097,6 +1132,9 @@ MSATTN_DECLARE_MFMA_LAUNCHER(_Float16, fp8_t)
 MSATTN_DECLARE_MFMA_LAUNCHER(bf16_t, float)
 MSATTN_DECLARE_MFMA_LAUNCHER(_Float16, float)
 MSATTN_DECLARE_MFMA_LAUNCHER(float, float)
+MSATTN_DECLARE_MFMA_LAUNCHER(float, bf16_t)
+MSATTN_DECLARE_MFMA_LAUNCHER(float, _Float16)
+MSATTN_DECLARE_MFMA_LAUNCHER(float, fp8_t)
 #undef MSATTN_DECLARE_MFMA_LAUNCHER
 
 }  // namespace msattn

@@ -47,9 +47,11 @@ namespace msattn {
 #ifndef MSATTN_SK_WAVES_FP8
 #define MSATTN_SK_WAVES_FP8 8
 #endif
-// Waves per workgroup for a cache of kv_bytes-byte elements.
-__host__ __device__ constexpr int sk_waves(int kv_bytes) {
-  return kv_bytes == 1 ? MSATTN_SK_WAVES_FP8 : MSATTN_SK_WAVES;
+// Waves per workgroup for a cache of kv_bytes-byte elements under a query of q_bytes-byte
+// elements. An fp32 query keeps one wave per SIMD: its query chunks take twice the
+// registers, and two waves on a SIMD would spill.
+__host__ __device__ constexpr int sk_waves(int kv_bytes, int q_bytes = 2) {
+  return kv_bytes == 1 && q_bytes < 4 ? MSATTN_SK_WAVES_FP8 : MSATTN_SK_WAVES;
 }
 constexpr int kSkMaxBatch = 4096;   // sequences per launch on this path
 constexpr int kSkTableRun = 64;     // tile page ids fetched per table load
@@ -80,9 +82,9 @@ __host__ __device__ constexpr int64_t streamk_pieces(int64_t n_chunks, int64_t n
 }
 
 template <typename T, typename KT, int D, int RT>
-__global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_kernel(
+__global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decode_streamk_kernel(
     const SplitParams p) {
-  constexpr int kSkWaves = sk_waves(sizeof(KT));
+  constexpr int kSkWaves = sk_waves(sizeof(KT), sizeof(T));
   constexpr int kSkThreads = kSkWaves * kWave;
   typedef Kv8<T, KT> KV;
   typedef typename KV::raw_t raw_t;
@@ -452,7 +454,7 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT)) * kWave) void decode_streamk_k
 template <typename T, typename KT, int D, int RT>
 hipError_t launch_decode_streamk_one(const SplitParams& p, int grid, hipStream_t stream) {
   hipLaunchKernelGGL((decode_streamk_kernel<T, KT, D, RT>), dim3(static_cast<unsigned>(grid)),
-                     dim3(sk_waves(sizeof(KT)) * kWave), 0, stream, p);
+                     dim3(sk_waves(sizeof(KT), sizeof(T)) * kWave), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -473,6 +475,9 @@ MSATTN_DECLARE_SK_LAUNCHER(_Float16, fp8_t)
 MSATTN_DECLARE_SK_LAUNCHER(bf16_t, float)
 MSATTN_DECLARE_SK_LAUNCHER(_Float16, float)
 MSATTN_DECLARE_SK_LAUNCHER(float, float)
+MSATTN_DECLARE_SK_LAUNCHER(float, bf16_t)
+MSATTN_DECLARE_SK_LAUNCHER(float, _Float16)
+MSATTN_DECLARE_SK_LAUNCHER(float, fp8_t)
 #undef MSATTN_DECLARE_SK_LAUNCHER
 
 #define MSATTN_SK_RT(T, KT, D)                                                      \

@@ -72,7 +72,8 @@ def check(out: torch.Tensor, ref: np.ndarray, q_dtype) -> float:
 @pytest.mark.parametrize("q_dtype,kv_dtype", PAIRS)
 def test_decode_every_pair(device, q_dtype, kv_dtype, D):
     """Decode (partition kernels: MFMA for a bf16/fp16 query over its own type, fp8 or
-    fp32 and for an fp32 query over fp32, the generic kernel for the rest) against the oracle with the cast; a row of
+    fp32 and for an fp32 query over any cache, the generic kernel for fp16 over bf16 and
+    bf16 over fp16) against the oracle with the cast; a row of
     context 1 returns exactly V[0] as the query type holds it."""
     H, KVH = 8, 2
     lens = [1, 17, 300, 1000, 0, 64]
@@ -209,3 +210,33 @@ def test_model_runner_attention_lines(device, q_dtype, kv_dtype):
                                         [s + 1 for s in row_starts], kv_cast=True)
         check(out.view(4, 1, H, D), ref, q_dtype)
         row_starts = [s + 1 for s in row_starts]
+
+
+@pytest.mark.parametrize("route", ["partition", "stream-K"])
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn])
+def test_fp32_query_narrow_cache_equals_widened(device, route, kv_dtype):
+    """An fp32 query over a bf16/fp16/fp8 cache runs the fp32 MFMA decode kernels on the
+    cache's rows widened exactly in registers (the reference's .to(query.dtype),
+    miniserve/attention.py:240-241). The same call over the cache converted to fp32
+    beforehand gives the same result: bit for bit for a 2-byte cache, whose head-dim split
+    across the MFMA steps is the fp32 cache's; within 1e-6 relative for fp8, whose split
+    differs (so the fp32 sums run in another order). Both are within max-abs 1e-4 of the
+    float64 oracle."""
+    H, KVH, D, lens, q_len, width, _ = ROUTES[route]
+    note(f"fp32 query over {name(kv_dtype)}, {route}")
+    q, kc, vc, table = case(H, KVH, D, lens, torch.float32, kv_dtype, q_len=q_len,
+                            width=width, seed=13)
+    cap = table.shape[1] * 16
+    qd = q.to(device)
+    out_n = paged_attention(qd, kc.to(device), vc.to(device), table, lens, max_context=cap)
+    out_w = paged_attention(qd, kc.float().to(device), vc.float().to(device), table, lens,
+                            max_context=cap)
+    torch.cuda.synchronize()
+    if kv_dtype == torch.float8_e4m3fn:
+        diff = float((out_n - out_w).abs().max() / out_w.abs().max())
+        note(f"fp8 against widened: {diff:.3e}")
+        assert diff < 1e-6
+    else:
+        assert torch.equal(out_n, out_w)
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens, kv_cast=True)
+    check(out_n, ref, torch.float32)

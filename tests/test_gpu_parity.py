@@ -294,6 +294,8 @@ def rope_unfused(q, cos, sin, pos):
     (32, 8, 128, torch.bfloat16, torch.float8_e4m3fn, True),   # stream-K
     (14, 2, 64, torch.bfloat16, torch.float8_e4m3fn, False),   # partition, head_dim 64
     (28, 4, 128, torch.float16, torch.float8_e4m3fn, False),   # partition, fp16 query
+    (14, 2, 64, torch.float32, torch.float8_e4m3fn, False),    # fp32 query over fp8
+    (32, 8, 128, torch.float32, torch.bfloat16, True),         # stream-K, fp32 over bf16
 ])
 def test_rope_in_kernel_matches_unfused(device, H, KVH, D, dtype, kv_dtype, wide):
     """RoPE applied inside the decode kernels equals attention over the query rotated
