@@ -66,6 +66,11 @@ constexpr int kSkTableRun = 64;     // tile page ids fetched per table load
 #ifndef MSATTN_SK_ROUNDS
 #define MSATTN_SK_ROUNDS 1
 #endif
+// 1: a run's page ids are decoded in the previous run's last ring turn, a run after
+// their request, so the wave does not wait for the table at each run's start.
+#ifndef MSATTN_SK_LATE_IDS
+#define MSATTN_SK_LATE_IDS 1
+#endif
 // Two waves on a SIMD (workgroups of more than 4 waves): the hardware issues the older
 // wave's loads first whenever both are ready, so the younger one streams its chunk
 // behind it and ends well after it (C3 fp8: waves 0-3 at 55 us, waves 4-7 at 67 us),
@@ -240,6 +245,31 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decod
     }
     return mb;
   };
+  // The same in two halves, so that the page id's load and its use are a run apart:
+  // table_issue requests lane k's page id (-1 past the run or the table) and the
+  // id-independent part of the offset; table_decode turns them into table_run's value.
+  struct RunIds {
+    int phys;
+    int64_t rest;
+  };
+  auto table_issue = [&](const Piece& pc, int run0) -> RunIds __attribute__((always_inline)) {
+    const int nt = min(kSkTableRun, pc.ntiles - run0);
+    RunIds r{-1, 0};
+    if (lane < nt) {
+      const int t = pc.t_first + run0 + lane;
+      const int pg = (t * 16) / p.bs;
+      const int slot0 = t * 16 - pg * p.bs;
+      r.rest = static_cast<int64_t>(slot0) * p.slot_stride +
+               static_cast<int64_t>(pc.kvh) * p.head_stride;
+      if (pg < p.W) r.phys = p.table[static_cast<int64_t>(pc.b) * p.W + pg];
+    }
+    return r;
+  };
+  auto table_decode = [&](const RunIds& r) -> int64_t __attribute__((always_inline)) {
+    return r.phys >= 0 && r.phys < p.num_blocks
+               ? static_cast<int64_t>(r.phys) * p.blk_stride + r.rest
+               : int64_t(-1);
+  };
   // The piece's query rows as the MFMA B operand (lane (g, n): row n, chunk j at dim
   // KV::qk_dim0(j, g), the split the K loads use).
   typedef typename QChunk<T>::type qchunk_t;
@@ -294,7 +324,17 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decod
       load_q(nxt, qn);
     }
     const bool has_next = more_here || next_piece;
-    const int64_t base_n = has_next ? table_run(nxt, run_n) : -1;
+    // The next run's page ids are requested now and decoded in this run's last ring turn,
+    // where its first tiles are issued: the wait for them then falls a run after the
+    // request (MSATTN_SK_LATE_IDS; decoding at once makes the wave wait here for the
+    // table's round trip and for the tile in flight).
+    RunIds ids_n{-1, 0};
+    int64_t base_n = -1;
+    if constexpr (MSATTN_SK_LATE_IDS) {
+      if (has_next) ids_n = table_issue(nxt, run_n);
+    } else {
+      base_n = has_next ? table_run(nxt, run_n) : -1;
+    }
 
     const int nt = min(kSkTableRun, cur.ntiles - run0);
     const int nt_ring = (nt + STEP - 1) / STEP * STEP;  // positions the ring walks
@@ -387,6 +427,18 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decod
           issue(bq[d], kq[d], vq[d]);
         });
       }
+      // The next run's ids are decoded after the issues of the turn before the last (the
+      // last turn issues the next run's first tiles): those issues are younger than the
+      // id's load on every path, so the wait for it holds back no tile in flight. (An
+      // empty asm that rewrites the id keeps the decode, and that wait, here rather than
+      // hoisted to the request.) A run of one turn decodes before it.
+      auto decode_next = [&]() __attribute__((always_inline)) {
+        asm volatile("" : "+v"(ids_n.phys));
+        base_n = table_decode(ids_n);
+      };
+      if constexpr (MSATTN_SK_LATE_IDS) {
+        if (nt <= STEP) decode_next();
+      }
       for (int k = 0; k < nt; k += STEP) {
         static_for<STEP>([&](auto dc) {
           constexpr int d = decltype(dc)::value;
@@ -396,6 +448,9 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decod
           issue(bq[nx], kq[nx], vq[nx]);
           consume(k + d, kq[cu], vq[cu], bq[cu]);
         });
+        if constexpr (MSATTN_SK_LATE_IDS) {
+          if (k + STEP < nt && k + 2 * STEP >= nt) decode_next();
+        }
         if constexpr (kBalance) {
           // Post this wave's progress; take priority while not ahead of the partner.
           // Both walk the same chunk, ring positions included, so counts compare.
