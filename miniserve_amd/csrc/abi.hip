@@ -3,6 +3,7 @@
 #include <cmath>
 #include <cstdint>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -37,6 +38,16 @@ constexpr int64_t kStreamKMinTiles = MSATTN_STREAMK_MIN_TILES;
 #endif
 // 1: msattn_paged_attention's partition-kernel decodes merge in-kernel (no merge launch).
 constexpr bool kFusedMerge = MSATTN_FUSED_MERGE != 0;
+#ifndef MSATTN_WIDE_ROUTE
+#define MSATTN_WIDE_ROUTE 1
+#endif
+#ifndef MSATTN_WIDE_SLOTS_PCT
+#define MSATTN_WIDE_SLOTS_PCT 100
+#endif
+// 1: long-context decodes with few (sequence, KV head) pairs take the wide partition
+// shape; its partitions are sized for kWideSlotsPct percent of a workgroup per CU.
+constexpr bool kWideRoute = MSATTN_WIDE_ROUTE != 0;
+constexpr int kWideSlotsPct = MSATTN_WIDE_SLOTS_PCT;
 
 bool dtype_ok(int d) { return d >= MSATTN_F32 && d <= MSATTN_FP8_E4M3; }
 int dtype_bytes(int d) { return d == MSATTN_F32 ? 4 : (d == MSATTN_FP8_E4M3 ? 1 : 2); }
@@ -395,6 +406,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   p.sk_group = 1;
   p.sk_unit_groups = 0;
   p.sk_min_chunk = kSkMinChunk;
+  p.mfma_waves = kMfmaWaves;
   p.key_lo = key_lo;
   p.rope_cos = rope.cos;
   p.rope_sin = rope.sin;
@@ -447,6 +459,25 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
           static_cast<int64_t>(np) * num_kv_heads * p.rtiles * batch >= kTargetSlots) {
         p.part = part_l;
         p.max_parts = np;
+      }
+    }
+    // Few (sequence, KV head, row tile) triples over long contexts: when partitions that
+    // give about one workgroup per CU would hold kPartWide tokens or more, and the launch
+    // stays within 1.5 workgroups per CU, the partition kernel's wide shape (8 waves, two
+    // per SIMD) over kPartWide-token partitions. Its
+    // two waves per SIMD fill each other's waits (C5-decode: 24.1 -> 22.6 us); shorter
+    // wide partitions, and wide workgroups two to a CU, measured slower than the regular
+    // shape.
+    if (kWideRoute && q_len == 1 && (RT == 4 || RT == 8) && q_dtype != MSATTN_F32 &&
+        kv_dtype != MSATTN_F32) {
+      const int64_t triples = static_cast<int64_t>(batch) * num_kv_heads * p.rtiles;
+      const int64_t want = static_cast<int64_t>(device_cus()) * kWideSlotsPct / 100;
+      const int64_t np = std::max<int64_t>(1, want / triples);
+      const int64_t launched = triples * ceil_div(max_context, kPartWide);
+      if (static_cast<int64_t>(max_context) >= np * kPartWide && 2 * launched <= 3 * want) {
+        p.part = kPartWide;
+        p.max_parts = ceil_div(max_context, kPartWide);
+        p.mfma_waves = kWideWaves;
       }
     }
   }

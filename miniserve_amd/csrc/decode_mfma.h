@@ -523,6 +523,12 @@ constexpr int kCuLdsBytes = 160 * 1024;  // gfx950 LDS per CU
 constexpr int kMfmaWaves = MSATTN_MFMA_WAVES;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
 constexpr int kMaxTilesPerWave = kPartMax / 16 / kMfmaWaves;  // partitions are <= kPartMax tokens
+// The wide shape of the partition kernel: kWideWaves waves (two per SIMD) over partitions
+// of up to kPartWide tokens, the same tiles per wave as the regular shape's longest
+// partition. It serves decodes with few (sequence, KV head) pairs over long contexts,
+// where partitions of that length still fill the chip with one workgroup per CU.
+constexpr int kWideWaves = 8;
+constexpr int kPartWide = kMaxTilesPerWave * 16 * kWideWaves;
 // Partition of the fp32 16-row route (MFMA P.V) when it merges in-kernel over a large grid
 // (chunked prefill): longer partitions spread each workgroup's start, epilogue and merge
 // over more tiles. Its kernel unrolls this many tiles per wave.
@@ -602,8 +608,10 @@ __device__ __forceinline__ void rope_chunks(typename QChunk<T>::type (&qb)[D / 3
   }
 }
 
-template <typename T, typename KT, int D, int RT>
-__global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitParams p) {
+template <typename T, typename KT, int D, int RT, int W = kMfmaWaves>
+__global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParams p) {
+  constexpr int kWaves = W;               // waves per workgroup
+  constexpr int kThreads = W * kWave;
   typedef Kv8<T, KT> KV;
   typedef typename KV::raw_t raw_t;
   static_assert(D == 64 || D == 128, "MFMA decode handles head_dim 64 and 128");
@@ -614,8 +622,8 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   constexpr int NJ = 16 / TPI;      // V load instructions per tile
   constexpr int APR = 16 / LPR;     // token groups per 16-lane row
 
-  __shared__ float s_red[kMfmaWaves][RT][D];
-  __shared__ float s_ml[kMfmaWaves][RT][2];
+  __shared__ float s_red[kWaves][RT][D];
+  __shared__ float s_ml[kWaves][RT][2];
   __shared__ int s_last;  // in-kernel merge: this workgroup arrived last
   // LDS reserved beyond s_red / s_ml so that at most kMfmaWgPerCu workgroups share a
   // CU (the store below never runs; it keeps the array allocated).
@@ -638,7 +646,11 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   // themselves in on a header ticket; the last one folds every partial into the output.
   // A sequence of one partition writes its output directly.
   const bool fused = p.out != nullptr;
-  if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) p.hdr[kHdrKind] = fused ? 2 : 0;
+  if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) {
+    p.hdr[kHdrKind] = fused ? 2 : 0;
+    p.hdr[kHdrPart] = p.part;
+    p.hdr[kHdrWaves] = W;
+  }
   // blockIdx.x = kvh + KVH * (part + max_parts * rtile); blockIdx.z = b.
   const unsigned bx = blockIdx.x;
   const int kvh = static_cast<int>(bx % static_cast<unsigned>(p.KVH));
@@ -649,7 +661,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
 
   // Wave w owns a fixed run of the partition's tiles, so their page ids can be
   // requested together with the context length instead of after it.
-  const int per_wave = p.part / (16 * kMfmaWaves);
+  const int per_wave = p.part / (16 * kWaves);
   const int tw0 = part * (p.part / 16) + w * per_wave;
   int phys_pre = -1;
   if (lane < per_wave) {
@@ -719,7 +731,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
     }
     __syncthreads();
     if (!s_last) return;
-    for (int idx = tid; idx < nrows * D4; idx += kMfmaThreads) {
+    for (int idx = tid; idx < nrows * D4; idx += kThreads) {
       const int r = idx / D4;
       const int d = (idx - r * D4) * 4;
       const int64_t orow = out_row(r);
@@ -769,7 +781,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
 
   if (a1 <= a0) {
     if (direct) {  // no key in the only partition: zeros
-      for (int idx = tid; idx < nrows * D4; idx += kMfmaThreads) {
+      for (int idx = tid; idx < nrows * D4; idx += kThreads) {
         const int r = idx / D4;
         store_out4(out_row(r), (idx - r * D4) * 4, make_float4(0.0f, 0.0f, 0.0f, 0.0f), 0.0f);
       }
@@ -860,7 +872,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
             (tile_token<D>(4 * g + r) * p.slot_stride + 64 * h + 4 * n) * EB);
   }
   // Tiles a wave may own: partitions of the fp32 16-row route reach kPartLongF32 tokens.
-  constexpr int kMaxT = kPvMfma ? kPartLongF32 / 16 / kMfmaWaves : kMaxTilesPerWave;
+  constexpr int kMaxT = kPvMfma ? kPartLongF32 / 16 / kWaves : kMaxTilesPerWave;
   mf_f32x4 acc_o[kPvMfma ? NOB : 1];
   if constexpr (kPvMfma) {
 #pragma unroll
@@ -1038,20 +1050,20 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   __syncthreads();
 
   // Combine the waves, four dims a thread: rescale each wave to the common max.
-  for (int idx = tid; idx < nrows * D4; idx += kMfmaThreads) {
+  for (int idx = tid; idx < nrows * D4; idx += kThreads) {
     const int r = idx / D4;
     const int d = (idx - r * D4) * 4;
-    float mw[kMfmaWaves];
+    float mw[kWaves];
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < kMfmaWaves; ++ww) {
+    for (int ww = 0; ww < kWaves; ++ww) {
       mw[ww] = s_ml[ww][r][0];
       M = fmaxf(M, mw[ww]);
     }
     float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (M != -INFINITY) {
 #pragma unroll
-      for (int ww = 0; ww < kMfmaWaves; ++ww) {
+      for (int ww = 0; ww < kWaves; ++ww) {
         if (mw[ww] == -INFINITY) continue;
         const float f = __builtin_amdgcn_exp2f(mw[ww] - M);
         const float4 v = *reinterpret_cast<const float4*>(&s_red[ww][r][d]);
@@ -1066,7 +1078,7 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
       float L = 0.0f;
       if (M != -INFINITY) {
 #pragma unroll
-        for (int ww = 0; ww < kMfmaWaves; ++ww)
+        for (int ww = 0; ww < kWaves; ++ww)
           if (mw[ww] != -INFINITY) L = fmaf(s_ml[ww][r][1], __builtin_amdgcn_exp2f(mw[ww] - M), L);
       }
       store_out4(orow, d, a, L > 0.0f ? 1.0f / L : 0.0f);
@@ -1082,11 +1094,11 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   if (tid < nrows) {
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < kMfmaWaves; ++ww) M = fmaxf(M, s_ml[ww][tid][0]);
+    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, s_ml[ww][tid][0]);
     float L = 0.0f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int ww = 0; ww < kMfmaWaves; ++ww) {
+      for (int ww = 0; ww < kWaves; ++ww) {
         const float mw = s_ml[ww][tid][0];
         if (mw != -INFINITY) L = fmaf(s_ml[ww][tid][1], __builtin_amdgcn_exp2f(mw - M), L);
       }
@@ -1106,12 +1118,12 @@ __global__ __launch_bounds__(kMfmaThreads) void decode_mfma_kernel(const SplitPa
   if (fused) fused_merge();
 }
 
-template <typename T, typename KT, int D, int RT>
+template <typename T, typename KT, int D, int RT, int W = kMfmaWaves>
 hipError_t launch_decode_mfma_one(const SplitParams& p, hipStream_t stream) {
   const unsigned gx = static_cast<unsigned>(p.max_parts) * static_cast<unsigned>(p.KVH) *
                       static_cast<unsigned>(p.rtiles);
-  hipLaunchKernelGGL((decode_mfma_kernel<T, KT, D, RT>),
-                     dim3(gx, 1, static_cast<unsigned>(p.batch)), dim3(kMfmaThreads), 0, stream, p);
+  hipLaunchKernelGGL((decode_mfma_kernel<T, KT, D, RT, W>),
+                     dim3(gx, 1, static_cast<unsigned>(p.batch)), dim3(W * kWave), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -4,14 +4,27 @@
 
 #include "decode_mfma.h"
 
-#define MSATTN_MFMA_RT(T, KT, D)                                              \
-  switch (RT) {                                                               \
-    case 1: return launch_decode_mfma_one<T, KT, D, 1>(p, stream);            \
-    case 2: return launch_decode_mfma_one<T, KT, D, 2>(p, stream);            \
-    case 4: return launch_decode_mfma_one<T, KT, D, 4>(p, stream);            \
-    case 8: return launch_decode_mfma_one<T, KT, D, 8>(p, stream);            \
-    case 16: return launch_decode_mfma_one<T, KT, D, 16>(p, stream);          \
-    default: break;                                                           \
+namespace msattn {
+template <typename T, typename KT>
+constexpr bool kWideOk = sizeof(T) == 2 && sizeof(KT) <= 2;
+}  // namespace msattn
+
+// The wide (8-wave) shape is compiled for 4 and 8 rows per tile under a 2-byte query
+// (a 16-bit or fp8 cache); p.mfma_waves selects it.
+#define MSATTN_MFMA_RT(T, KT, D)                                                          \
+  switch (RT) {                                                                           \
+    case 1: return launch_decode_mfma_one<T, KT, D, 1>(p, stream);                        \
+    case 2: return launch_decode_mfma_one<T, KT, D, 2>(p, stream);                        \
+    case 4:                                                                               \
+      if constexpr (kWideOk<T, KT>)                                                       \
+        if (p.mfma_waves == kWideWaves) return launch_decode_mfma_one<T, KT, D, 4, kWideWaves>(p, stream); \
+      return launch_decode_mfma_one<T, KT, D, 4>(p, stream);                              \
+    case 8:                                                                               \
+      if constexpr (kWideOk<T, KT>)                                                       \
+        if (p.mfma_waves == kWideWaves) return launch_decode_mfma_one<T, KT, D, 8, kWideWaves>(p, stream); \
+      return launch_decode_mfma_one<T, KT, D, 8>(p, stream);                              \
+    case 16: return launch_decode_mfma_one<T, KT, D, 16>(p, stream);                      \
+    default: break;                                                                       \
   }
 
 #define MSATTN_MFMA_LAUNCHER(T, KT)                                                          \

@@ -53,6 +53,8 @@ constexpr int kPartMax = MSATTN_PART_MAX;
 //                2 = partition kernel that merged in-kernel and wrote the output
 //   kind 1 also: hdr[1] sumT, [2] chunk c, [3] sub-ranges, [4] UG, [5] NUG, [6] B,
 //   [7] RT, and hdr[kHdrPrefix + b] = tiles of sequences before b (b = 0..B).
+//   kinds 0 and 2 (partition kernels) also: hdr[8] partition tokens, [9] waves per
+//   workgroup (the launch's shape, for tests and measurements; the merge does not read them).
 //   hdr[kHdrTickets + t], t < kMaxTickets: arrival counters of the in-kernel merge, one
 //   per (sequence, KV head, row tile). They sit at the same offset for every geometry,
 //   must be zero when a workspace is first used, and every call leaves them zero.
@@ -60,7 +62,7 @@ constexpr int kHdrTickets = 64;
 constexpr int kMaxTickets = 4096;
 constexpr int kHdrPrefix = kHdrTickets + kMaxTickets;
 constexpr int kHdrKind = 0, kHdrSumT = 1, kHdrChunk = 2, kHdrNsub = 3, kHdrUG = 4,
-              kHdrNUG = 5, kHdrB = 6, kHdrRT = 7;
+              kHdrNUG = 5, kHdrB = 6, kHdrRT = 7, kHdrPart = 8, kHdrWaves = 9;
 
 struct SplitParams {
   int* hdr;
@@ -95,6 +97,7 @@ struct SplitParams {
   // its partials and write the output; `tickets` are the header's arrival counters.
   void* out;
   int* tickets;
+  int mfma_waves;  // partition MFMA kernel: waves per workgroup (4, or 8 for long partitions)
 };
 
 // Position of row b's query for RoPE, clamped into the tables.
@@ -136,7 +139,11 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int w = tid / kWave;
-  if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) p.hdr[kHdrKind] = 0;
+  if (tid == 0 && blockIdx.x == 0 && blockIdx.z == 0) {
+    p.hdr[kHdrKind] = 0;
+    p.hdr[kHdrPart] = p.part;
+    p.hdr[kHdrWaves] = kSplitWaves;
+  }
 
   // blockIdx.x = part + max_parts * (kvh + KVH * rtile); blockIdx.z = b.
   const int part = static_cast<int>(blockIdx.x % static_cast<unsigned>(p.max_parts));

@@ -86,11 +86,16 @@ class Caller:
         assert st == nat.OK, st
         torch.cuda.synchronize()
         hdr = self.ws[: 4 * (HDR_TICKETS + MAX_TICKETS)].view(torch.int32).cpu()
-        return fused, two, hdr
+        hdr2 = self.ws2[: 4 * HDR_TICKETS].view(torch.int32).cpu()
+        return fused, two, hdr, hdr2
 
 
-def check(fused, two, hdr, q, kc, vc, table, lens, window=None):
+def check(fused, two, hdr, q, kc, vc, table, lens, window=None, hdr2=None):
     assert int(hdr[0]) == 2, f"workspace kind {int(hdr[0])}: not the in-kernel merge"
+    # The same partitions on both paths unless the fused call took the wide shape (longer
+    # partitions): then the weights meet other running maxima before their rounding to
+    # the cache type for v_dot2, and only the oracle's bar applies between the two.
+    same_split = hdr2 is None or (int(hdr[8]), int(hdr[9])) == (int(hdr2[8]), int(hdr2[9]))
     assert not hdr[HDR_TICKETS:].any(), "merge counters not left at zero"
     assert not torch.isnan(fused).any()
     ref = dense.paged_attention_f64(q, kc, vc, table.long(), lens, window=window)
@@ -105,8 +110,12 @@ def check(fused, two, hdr, q, kc, vc, table, lens, window=None):
         err = float(np.abs(f - ref).max() / max(np.abs(ref).max(), 1e-30))
         assert err < BF16_REL, err
         ulp = 2.0 ** (-7 if q.dtype == torch.bfloat16 else -10)
-        assert np.all(np.abs(f - t) <= 2 * ulp * np.maximum(np.abs(t), 2.0 ** -14)), \
-            float(np.abs(f - t).max())
+        if same_split:
+            assert np.all(np.abs(f - t) <= 2 * ulp * np.maximum(np.abs(t), 2.0 ** -14)), \
+                float(np.abs(f - t).max())
+        else:
+            terr = float(np.abs(t - ref).max() / max(np.abs(ref).max(), 1e-30))
+            assert terr < BF16_REL, terr
     note(f"oracle err {err:.3e}")
 
 
@@ -134,8 +143,8 @@ def test_fused_merge_consecutive_calls(device, name):
         lens[2] = int(torch.randint(2, 60, (1,), generator=g))  # one partition
         note(f"fused {name} call {i}: B={B} lens={lens}")
         q, kc, vc, table = make(H, KVH, D, lens, dtype, width, seed=i + 7 * H)
-        fused, two, hdr = caller.run(q, kc, vc, table, lens)
-        check(fused, two, hdr, q, kc, vc, table, lens)
+        fused, two, hdr, hdr2 = caller.run(q, kc, vc, table, lens)
+        check(fused, two, hdr, q, kc, vc, table, lens, hdr2=hdr2)
         assert not fused[0].cpu().any()  # context 0 -> zeros
 
 
@@ -155,8 +164,8 @@ def test_fused_merge_window_and_short_q(device):
                                     q_len=q_len)
         else:
             lens_q = lens
-        fused, two, hdr = caller.run(q, kc, vc, table, lens_q, window=window)
-        check(fused, two, hdr, q, kc, vc, table, lens_q, window=window or None)
+        fused, two, hdr, hdr2 = caller.run(q, kc, vc, table, lens_q, window=window)
+        check(fused, two, hdr, q, kc, vc, table, lens_q, window=window or None, hdr2=hdr2)
 
 
 def test_stream_k_leaves_counters_alone(device):
@@ -167,14 +176,14 @@ def test_stream_k_leaves_counters_alone(device):
     H, KVH, D = 32, 8, 128
     lens = [3000, 17, 5000, 0, 800, 4096, 1, 2500]
     q, kc, vc, table = make(H, KVH, D, lens, torch.bfloat16, 1024, seed=3)
-    fused, two, hdr = caller.run(q, kc, vc, table, lens)
+    fused, two, hdr, hdr2 = caller.run(q, kc, vc, table, lens)
     assert int(hdr[0]) == 1  # stream-K: the merge kernel ran
     assert not hdr[HDR_TICKETS:].any()
     assert torch.equal(fused, two)
     lens = [300, 1200, 0, 64]
     q, kc, vc, table = make(14, 2, 64, lens, torch.bfloat16, 80, seed=4)
-    fused, two, hdr = caller.run(q, kc, vc, table, lens)
-    check(fused, two, hdr, q, kc, vc, table, lens)
+    fused, two, hdr, hdr2 = caller.run(q, kc, vc, table, lens)
+    check(fused, two, hdr, q, kc, vc, table, lens, hdr2=hdr2)
     assert lib is nat.lib()
 
 
@@ -190,5 +199,45 @@ def test_fp32_prefill_long_partitions(device, D, window):
         note(f"fp32 long prefill D={D} window={window} call {i}: lens={lens}")
         q, kc, vc, table = make(H, KVH, D, lens, torch.float32, width, seed=D + i,
                                 q_len=q_len)
-        fused, two, hdr = caller.run(q, kc, vc, table, lens, window=window)
-        check(fused, two, hdr, q, kc, vc, table, lens, window=window or None)
+        fused, two, hdr, hdr2 = caller.run(q, kc, vc, table, lens, window=window)
+        check(fused, two, hdr, q, kc, vc, table, lens, window=window or None, hdr2=hdr2)
+
+
+WIDE_CASES = {  # name -> (H, KVH, D, q dtype, cache dtype, batch, window)
+    "C5 geometry bf16": (28, 4, 128, torch.bfloat16, torch.bfloat16, 16, 0),
+    "C5 geometry fp8 cache": (28, 4, 128, torch.bfloat16, torch.float8_e4m3fn, 16, 0),
+    "fp16 D64 G4": (16, 4, 64, torch.float16, torch.float16, 16, 0),
+    "bf16 window 1500": (28, 4, 128, torch.bfloat16, torch.bfloat16, 16, 1500),
+}
+
+
+@pytest.mark.parametrize("name", list(WIDE_CASES))
+def test_wide_shape_long_contexts(device, name):
+    """Few (sequence, KV head) pairs over long contexts take the wide partition shape (8
+    waves, partitions of more than 512 tokens, about one workgroup per CU): the header
+    must name it, and the output must meet the float64 oracle's bar (K/V cast to the
+    query type) on three consecutive calls, with empty, one-token, one-partition and
+    full-table sequences among them."""
+    H, KVH, D, q_dtype, kv_dtype, B, window = WIDE_CASES[name]
+    width = 256  # 4096 tokens: a 1024-token partition for 64 (sequence, KV head) pairs
+    caller = Caller(device, 64 << 20)
+    for i in range(3):
+        g = torch.Generator().manual_seed(300 + 10 * i + H)
+        lens = [int(x) for x in torch.randint(1024, width * 16 + 1, (B,), generator=g)]
+        lens[0], lens[1], lens[2], lens[3] = 0, 1, 700, width * 16
+        note(f"wide {name} call {i}: lens={lens}")
+        q, kc, vc, table = make(H, KVH, D, lens, q_dtype, width, seed=i + 11 * H)
+        kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+        fused, two, hdr, hdr2 = caller.run(q, kc, vc, table, lens, window=window)
+        assert (int(hdr[0]), int(hdr[9])) == (2, 8), f"kind {int(hdr[0])}, waves {int(hdr[9])}"
+        assert int(hdr[8]) > 512, int(hdr[8])
+        assert not hdr[HDR_TICKETS:].any(), "merge counters not left at zero"
+        assert not torch.isnan(fused).any()
+        assert not fused[0].cpu().any()  # context 0 -> zeros
+        ref = dense.paged_attention_f64(q, kc, vc, table.long(), lens, window=window or None,
+                                        kv_cast=True)
+        for out in (fused, two):
+            f = out.double().cpu().numpy()
+            err = float(np.abs(f - ref).max() / max(np.abs(ref).max(), 1e-30))
+            assert err < BF16_REL, err
+        note(f"oracle err {err:.3e}, partition {int(hdr[8])}")
