@@ -125,13 +125,22 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decod
   // waves through LDS (two buffers, so one barrier a slice), carrying the running total.
   constexpr int kSlices = (kSkMaxBatch + kSkThreads - 1) / kSkThreads;
   const int nslices = (B + kSkThreads - 1) / kSkThreads;
+  // Every live slice's length load goes out before any is used (lanes past the batch
+  // read sequence 0's and drop it): one memory round trip for the whole batch.
+  int lraw[kSlices];
+#pragma unroll
+  for (int k = 0; k < kSlices; ++k)
+    if (k < nslices) {
+      const int b = k * kSkThreads + tid;
+      lraw[k] = p.lens[b < B ? b : 0];
+    }
   int tb[kSlices];
 #pragma unroll
   for (int k = 0; k < kSlices; ++k) {
     const int b = k * kSkThreads + tid;
     int t = 0;
-    if (b < B) {
-      int ctx = p.lens[b];
+    if (k < nslices && b < B) {
+      int ctx = lraw[k];
       ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
       s_ctx[b] = ctx;
       const int lo = max(p.key_lo, p.window > 0 ? max(0, ctx - p.window) : 0);
@@ -287,12 +296,45 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decod
     }
   };
 
+  // The first piece's query rows and first run's page ids, requested together and with
+  // no branch around either load, so that the wave waits once for both (a load under a
+  // lane condition whose result must merge with a default value makes the compiler wait
+  // for it on the spot: four query chunks and the page id were five round trips).
+  auto load_q_first = [&](const Piece& pc, qchunk_t (&q)[JD]) __attribute__((always_inline)) {
+    const T* qp = static_cast<const T*>(p.q);
+    // Lanes past the piece's rows load row 0 again: their MFMA columns' scores are
+    // replaced by -inf before use (the masking in the tile loop tests n < nrows), and no
+    // output or partial row is stored for them.
+    const bool live = n < pc.nrows;
+    const int64_t orow_n =
+        static_cast<int64_t>(pc.b) * p.H + pc.kvh * p.G + pc.row0 + (live ? n : 0);
+#pragma unroll
+    for (int j = 0; j < JD; ++j) q[j] = QChunk<T>::load(qp + orow_n * D + KV::qk_dim0(j, g, JD));
+    if (p.rope_cos != nullptr && live) {
+      const int64_t po = static_cast<int64_t>(rope_position(p, pc.b)) * D;
+      rope_chunks<T, KT, D>(q, p.rope_cos + po, p.rope_sin + po, g);
+    }
+  };
+  auto table_first = [&](const Piece& pc) -> int64_t __attribute__((always_inline)) {
+    const int nt = min(kSkTableRun, pc.ntiles);
+    const int t = pc.t_first + lane;
+    const int pg = (t * 16) / p.bs;
+    const int slot0 = t * 16 - pg * p.bs;
+    const bool ok = lane < nt && pg < p.W;  // other lanes read entry 0 and drop it
+    const int phys = p.table[static_cast<int64_t>(pc.b) * p.W + (ok ? pg : 0)];
+    const int64_t rest = static_cast<int64_t>(slot0) * p.slot_stride +
+                         static_cast<int64_t>(pc.kvh) * p.head_stride;
+    return ok && phys >= 0 && phys < p.num_blocks
+               ? static_cast<int64_t>(phys) * p.blk_stride + rest
+               : int64_t(-1);
+  };
+
   if (s >= s_end) return;
   Piece cur = locate(s);
   int run0 = 0;
-  int64_t my_base = table_run(cur, 0);
   qchunk_t qb[JD];
-  load_q(cur, qb);
+  load_q_first(cur, qb);
+  int64_t my_base = table_first(cur);
 
   float m_run = -INFINITY;
   float l_run = 0.0f;
