@@ -320,6 +320,35 @@ def test_rope_in_kernel_matches_unfused(device, H, KVH, D, dtype, kv_dtype, wide
     assert rel_err(fused, ref) < (1e-4 if dtype == torch.float32 else BF16_REL)
 
 
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_rope_in_kernel_wide_partition_shape(device, kv_dtype):
+    """Fused RoPE on the partition kernel's wide shape (8 waves over 1024-token partitions:
+    few (sequence, KV head) pairs over a long table), bit-exact against the query rotated
+    beforehand, and the workspace header naming that shape."""
+    H, KVH, D, dtype = 28, 4, 128, torch.bfloat16
+    lens = [1, 3000, 77, 9000, 1025, 10240]
+    width = 640  # 10240 tokens: 24 (sequence, KV head) pairs, ten 1024-token partitions
+    note(f"rope wide partition shape kv={kv_dtype}")
+    q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=77)
+    kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+    cos, sin = rope_tables(max(lens) + 8, D)
+    pos = torch.tensor([L - 1 for L in lens])
+    cap = width * 16
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=device)
+    fused = paged_attention(q.to(device), kc.to(device), vc.to(device), table, lens,
+                            max_context=cap, workspace=ws,
+                            rope=(cos.to(device), sin.to(device), pos.to(device)))
+    torch.cuda.synchronize()
+    hdr = ws[:64].view(torch.int32).cpu()
+    assert (int(hdr[0]), int(hdr[8]), int(hdr[9])) == (2, 1024, 8), hdr[:10].tolist()
+    qr = rope_unfused(q, cos, sin, pos)
+    unfused = paged_attention(qr.to(device), kc.to(device), vc.to(device), table, lens,
+                              max_context=cap)
+    assert torch.equal(fused, unfused)
+    ref = dense.paged_attention_f64(qr, kc, vc, table, lens)
+    assert rel_err(fused, ref) < BF16_REL
+
+
 @pytest.mark.parametrize("H,KVH,D,dtype,wide", [
     (32, 8, 128, torch.bfloat16, True),     # stream-K MFMA kernel
     (14, 2, 64, torch.bfloat16, False),     # partition MFMA kernel
