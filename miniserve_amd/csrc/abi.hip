@@ -29,9 +29,11 @@ static_assert(kPartMax / 8 >= 16 * kMfmaWaves && (kPartMax / 8) % (16 * kMfmaWav
 #endif
 constexpr int64_t kTargetSlots = MSATTN_TARGET_SLOTS;  // workgroup slots wanted in a launch
 #ifndef MSATTN_STREAMK_MIN_TILES
-#define MSATTN_STREAMK_MIN_TILES 65536
+#define MSATTN_STREAMK_MIN_TILES 262144
 #endif
-// Decode launches whose (batch x KV heads x table tiles) reach this use stream-K.
+// Decode launches whose (batch x KV heads x table tiles) reach this use stream-K; below it
+// the partition kernel was measured as fast or faster (3-12 % at 65,536 tiles, even at
+// 131,072 with long contexts), above it stream-K (11 % at 64 sequences of 1-8k tokens).
 constexpr int64_t kStreamKMinTiles = MSATTN_STREAMK_MIN_TILES;
 #ifndef MSATTN_FUSED_MERGE
 #define MSATTN_FUSED_MERGE 1

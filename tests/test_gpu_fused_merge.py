@@ -175,7 +175,7 @@ def test_stream_k_leaves_counters_alone(device):
     caller = Caller(device, 256 << 20)
     H, KVH, D = 32, 8, 128
     lens = [3000, 17, 5000, 0, 800, 4096, 1, 2500]
-    q, kc, vc, table = make(H, KVH, D, lens, torch.bfloat16, 1024, seed=3)
+    q, kc, vc, table = make(H, KVH, D, lens, torch.bfloat16, 4096, seed=3)
     fused, two, hdr, hdr2 = caller.run(q, kc, vc, table, lens)
     assert int(hdr[0]) == 1  # stream-K: the merge kernel ran
     assert not hdr[HDR_TICKETS:].any()

@@ -104,7 +104,7 @@ def test_prefill_every_pair(device, q_dtype, kv_dtype):
 
 ROUTES = {  # name -> (H, KVH, D, lens, q_len, width in pages, prefix pages)
     "partition": (14, 2, 64, [5, 100, 1000, 333], 1, None, 0),
-    "stream-K": (32, 8, 128, [3000, 17, 5000, 0, 800, 4096, 1, 2500], 1, 1024, 0),
+    "stream-K": (32, 8, 128, [3000, 17, 5000, 0, 800, 4096, 1, 2500], 1, 4096, 0),
     "prefill": (28, 4, 128, [512, 700], 64, None, 0),
     "cascade": (32, 8, 128, [5, 100, 1000, 333, 2000, 160, 161, 0], 1, 130, 10),
 }

@@ -18,6 +18,11 @@ from miniserve_amd import PagedAttention, gather_kv, paged_attention
 from miniserve_amd.workloads import make_workload
 from oracle import dense, paged_sdpa, split_k
 
+# Decodes whose table capacity (batch x KV heads x table tiles) reaches this run on the
+# stream-K kernel (MSATTN_STREAMK_MIN_TILES in csrc/abi.hip); smaller ones on the partition
+# kernel. Tests that mean to reach stream-K size their tables from it.
+SK_MIN_TILES = 1 << 18
+
 pytestmark = pytest.mark.gpu
 
 FP32_ATOL = 1e-4
@@ -206,7 +211,7 @@ def test_fp8_kv_mfma_equals_dequantized(device, H, KVH, D, dtype, wide, window):
     kernel, test_fp8_kv_prefill_equals_dequantized, which shares it.)"""
     note(f"fp8 MFMA H={H} KVH={KVH} D={D} {dtype} wide={wide} window={window}")
     lens = [0, 1, 17, 300, 1234, 77, 4096, 999]
-    width = 65536 // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
+    width = SK_MIN_TILES // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
     q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=D + KVH)
     kc8, vc8 = kc.to(torch.float8_e4m3fn), vc.to(torch.float8_e4m3fn)
     kd, vd = kc8.to(dtype), vc8.to(dtype)
@@ -303,7 +308,7 @@ def test_rope_in_kernel_matches_unfused(device, H, KVH, D, dtype, kv_dtype, wide
     float64 oracle over the rotated query."""
     note(f"rope H={H} KVH={KVH} D={D} {dtype} kv={kv_dtype} wide={wide}")
     lens = [1, 300, 77, 1234, 16, 999]
-    width = 65536 // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
+    width = SK_MIN_TILES // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
     q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=D + H)
     if kv_dtype != dtype:
         kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
@@ -363,7 +368,7 @@ def test_rope_low_precision_against_fp32_rotation(device, H, KVH, D, dtype, wide
     2e-2 max-rel bar."""
     note(f"rope vs fp32 rotation H={H} KVH={KVH} D={D} {dtype} wide={wide}")
     lens = [1, 300, 77, 1234, 16, 999]
-    width = 65536 // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
+    width = SK_MIN_TILES // (len(lens) * KVH) + 1 if wide else (max(lens) + 15) // 16
     q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=D + H + 1)
     cos, sin = rope_tables(max(lens) + 8, D)
     pos = torch.tensor([L - 1 for L in lens])
@@ -434,7 +439,7 @@ def test_mfma_routes_fuzz(device):
         pages = max((L + bs - 1) // bs for L in lens)
         width = pages + 2
         if route == "wide":
-            width = max(width, -(-65536 * 16 // (B * KVH * bs)))
+            width = max(width, -(-SK_MIN_TILES * 16 // (B * KVH * bs)))
         prefix = 0
         if route == "cascade":
             prefix = int(torch.randint(1, max(2, min(lens) // bs + 2), (1,), generator=gen))
@@ -480,7 +485,7 @@ def test_mfma_fp32_routes_fuzz(device):
         pages = max((L + bs - 1) // bs for L in lens)
         width = pages + 2
         if route == "wide":
-            width = max(width, -(-65536 * 16 // (B * KVH * bs)))
+            width = max(width, -(-SK_MIN_TILES * 16 // (B * KVH * bs)))
         prefix = 0
         if route == "cascade":
             prefix = int(torch.randint(1, max(2, min(lens) // bs + 2), (1,), generator=gen))
@@ -628,7 +633,7 @@ def wide_table_case(H, KVH, D, lens, dtype, width_pages, seed):
 ])
 def test_streamk_decode(device, H, KVH, D, dtype, window):
     lens = [0, 1, 16, 17, 300, 1234, 77, 4096, 5, 2048, 999, 33]
-    width = 65536 // (len(lens) * KVH) + 1  # capacity past the stream-K threshold
+    width = SK_MIN_TILES // (len(lens) * KVH) + 1  # capacity past the stream-K threshold
     note(f"stream-K H={H} KVH={KVH} D={D} {dtype} window={window}")
     q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=H + D)
     out = run_hip(device, q, kc, vc, table, lens, window=window, max_context=width * 16)
@@ -647,20 +652,20 @@ def test_streamk_decode(device, H, KVH, D, dtype, window):
 
 
 @pytest.mark.parametrize("batch,max_ctx,width", [
-    (257, 300, 128),    # two slices of the in-kernel context-length scan
-    (700, 300, 48),     # three slices
-    (4096, 128, 8),     # the path's largest batch: sixteen slices
+    (257, 300, 512),    # two slices of the in-kernel context-length scan
+    (700, 300, 192),    # three slices
+    (4096, 128, 32),    # the path's largest batch: sixteen slices
 ])
 def test_streamk_large_batch(device, batch, max_ctx, width):
     """Stream-K decode over batches past one 256-sequence slice of its context-length scan
-    (tables wide enough for the stream-K route: batch x KV heads x width >= 65536 tiles),
+    (tables wide enough for the stream-K route: batch x KV heads x width >= SK_MIN_TILES),
     against the float64 oracle; empty and one-token contexts included."""
     H, KVH, D = 14, 2, 64
     g = torch.Generator().manual_seed(batch)
     lens = [int(x) for x in torch.randint(0, max_ctx + 1, (batch,), generator=g)]
     lens[0], lens[1] = 0, 1
     note(f"stream-K large batch B={batch} ctx<={max_ctx} width={width}")
-    assert batch * KVH * width >= 65536
+    assert batch * KVH * width >= SK_MIN_TILES
     q, kc, vc, table = wide_table_case(H, KVH, D, lens, torch.bfloat16, width, seed=batch + 1)
     out = run_hip(device, q, kc, vc, table, lens, max_context=width * 16)
     ref = dense.paged_attention_f64(q, kc, vc, table, lens)
@@ -677,9 +682,10 @@ def test_streamk_graph_replays(device):
     note("stream-K graph")
     H, KVH, D = 32, 8, 128
     lens = [3000, 17, 5000, 0, 800, 4096, 1, 2500]
-    width = 1024
-    q, kc, vc, table = wide_table_case(H, KVH, D, [width * 16] * len(lens), torch.bfloat16,
-                                       width, seed=5)
+    width = SK_MIN_TILES // (len(lens) * KVH)  # stream-K capacity; pages for 8192 tokens a row
+    top = 8192
+    q, kc, vc, table = wide_table_case(H, KVH, D, [top] * len(lens), torch.bfloat16, width,
+                                       seed=5)
     kc, vc = kc.to(device), vc.to(device)
     sq = q.to(device)
     stable = table.to(device=device, dtype=torch.int32)
@@ -701,7 +707,7 @@ def test_streamk_graph_replays(device):
         step()
     g = torch.Generator().manual_seed(6)
     for rep in range(4):
-        new = [int(x) for x in torch.randint(0, cap + 1, (len(lens),), generator=g)]
+        new = [int(x) for x in torch.randint(0, top + 1, (len(lens),), generator=g)]
         slens.copy_(torch.tensor(new, dtype=torch.int32))
         graph.replay()
         torch.cuda.synchronize()
@@ -771,7 +777,7 @@ def test_mfma_paths_other_page_sizes(device, bs):
     cases = [  # (H, KVH, D, q_len, table width in pages, kv dtype)
         (28, 4, 128, 64, (max(lens) + bs - 1) // bs + 2, torch.bfloat16),   # prefill
         (14, 2, 64, 1, (max(lens) + bs - 1) // bs + 2, torch.bfloat16),     # partition decode
-        (32, 8, 128, 1, 65536 * 16 // (bs * len(lens) * 8) + 1, torch.bfloat16),  # stream-K
+        (32, 8, 128, 1, SK_MIN_TILES * 16 // (bs * len(lens) * 8) + 1, torch.bfloat16),  # stream-K
         (32, 8, 128, 1, (max(lens) + bs - 1) // bs + 2, torch.float8_e4m3fn),     # fp8
     ]
     for H, KVH, D, q_len, width, kv_dtype in cases:
@@ -861,8 +867,8 @@ CASCADE_CASES = [  # (H, KVH, D, dtype, bs, lens, prefix pages, table width in p
      [int(x) for x in torch.randint(1, 3000, (20,), generator=_g)], 37, 190),
     (32, 8, 128, torch.bfloat16, 32, [700, 64, 4000], 20, 126),     # 32-token pages
     (32, 8, 128, torch.bfloat16, 48, [700, 64, 4000], 9, 90),       # 48-token pages
-    # stream-K decode for the suffix (batch x KV heads x table tiles >= 65536)
-    (32, 8, 128, torch.bfloat16, 16, [30000, 9000, 20000, 1000], 256, 2048),
+    # stream-K decode for the suffix (batch x KV heads x table tiles >= SK_MIN_TILES)
+    (32, 8, 128, torch.bfloat16, 16, [30000, 9000, 20000, 1000], 256, 8192),
     # every key in the prefix: the suffix pass has no work
     (32, 8, 128, torch.bfloat16, 16, [480, 480, 480], 30, 30),
     # head_dim 64 (the prefix pass on the head_dim-64 prefill kernel)

@@ -80,7 +80,7 @@ def check_oracle(out, q, kc, vc, table, lens):
 
 CASES = {  # name -> (H, KVH, D, dtype, q_len, first lens, second lens, width in pages)
     "stream-K": (32, 8, 128, torch.bfloat16, 1, [3000, 17, 5000, 0, 800, 4096, 1, 2500],
-                 [900, 33, 4000], 1024),
+                 [900, 33, 4000], 4096),
     "partition": (14, 2, 64, torch.bfloat16, 1, [1500, 300, 2048, 77, 1024, 640],
                   [100, 1800], 128),
     "partition fp32": (14, 2, 64, torch.float32, 1, [400, 130, 512, 9], [200, 35], 32),
