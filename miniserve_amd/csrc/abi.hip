@@ -50,6 +50,16 @@ constexpr bool kFusedMerge = MSATTN_FUSED_MERGE != 0;
 // shape; its partitions are sized for kWideSlotsPct percent of a workgroup per CU.
 constexpr bool kWideRoute = MSATTN_WIDE_ROUTE != 0;
 constexpr int kWideSlotsPct = MSATTN_WIDE_SLOTS_PCT;
+#ifndef MSATTN_WIDE_MAX_PCT
+#define MSATTN_WIDE_MAX_PCT 150
+#endif
+// The wide shape only when its launch holds at most this percentage of the aimed-for
+// workgroups (two 8-wave workgroups on one CU run one after the other).
+constexpr int kWideMaxPct = MSATTN_WIDE_MAX_PCT;
+#ifndef MSATTN_WIDE_FP8_UNCAPPED
+#define MSATTN_WIDE_FP8_UNCAPPED 1
+#endif
+constexpr bool kWideFp8Uncapped = MSATTN_WIDE_FP8_UNCAPPED != 0;
 
 bool dtype_ok(int d) { return d >= MSATTN_F32 && d <= MSATTN_FP8_E4M3; }
 int dtype_bytes(int d) { return d == MSATTN_F32 ? 4 : (d == MSATTN_FP8_E4M3 ? 1 : 2); }
@@ -476,7 +486,13 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
       const int64_t want = static_cast<int64_t>(device_cus()) * kWideSlotsPct / 100;
       const int64_t np = std::max<int64_t>(1, want / triples);
       const int64_t launched = triples * ceil_div(max_context, kPartWide);
-      if (static_cast<int64_t>(max_context) >= np * kPartWide && 2 * launched <= 3 * want) {
+      // An fp8 cache at 4 rows per tile takes the wide shape however many workgroups the
+      // launch holds: its widening work per byte fills two waves per SIMD (5-10 % faster
+      // on H32/KVH8 decodes of 6-20 workgroups per CU); at 8 rows per tile, and over a
+      // 16-bit cache, the cap stands (up to 18 % slower without it).
+      const bool uncapped = kWideFp8Uncapped && kv_fp8 && RT == 4;
+      if (static_cast<int64_t>(max_context) >= np * kPartWide &&
+          (uncapped || 100 * launched <= static_cast<int64_t>(kWideMaxPct) * want)) {
         p.part = kPartWide;
         p.max_parts = ceil_div(max_context, kPartWide);
         p.mfma_waves = kWideWaves;

@@ -208,6 +208,8 @@ WIDE_CASES = {  # name -> (H, KVH, D, q dtype, cache dtype, batch, window)
     "C5 geometry fp8 cache": (28, 4, 128, torch.bfloat16, torch.float8_e4m3fn, 16, 0),
     "fp16 D64 G4": (16, 4, 64, torch.float16, torch.float16, 16, 0),
     "bf16 window 1500": (28, 4, 128, torch.bfloat16, torch.bfloat16, 16, 1500),
+    # an fp8 cache at 4 rows per tile takes the wide shape past 1.5 workgroups per CU
+    "fp8 cache G4, 512 workgroups": (32, 8, 128, torch.bfloat16, torch.float8_e4m3fn, 16, 0),
 }
 
 
