@@ -35,6 +35,13 @@ constexpr int64_t kTargetSlots = MSATTN_TARGET_SLOTS;  // workgroup slots wanted
 // the partition kernel was measured as fast or faster (3-12 % at 65,536 tiles, even at
 // 131,072 with long contexts), above it stream-K (11 % at 64 sequences of 1-8k tokens).
 constexpr int64_t kStreamKMinTiles = MSATTN_STREAMK_MIN_TILES;
+// The same for a 16-bit query over an fp8 cache at 8 rows per tile (G = 5..8), where
+// stream-K's two waves per SIMD win from 65,536 tiles (37.0 against 44.3 us for 64 x
+// H14/KVH2 at 2-8k tokens); below it the partition kernel does (11.8 against 20.4 us).
+#ifndef MSATTN_STREAMK_MIN_TILES_FP8_RT8
+#define MSATTN_STREAMK_MIN_TILES_FP8_RT8 65536
+#endif
+constexpr int64_t kStreamKMinTilesFp8Rt8 = MSATTN_STREAMK_MIN_TILES_FP8_RT8;
 #ifndef MSATTN_FUSED_MERGE
 #define MSATTN_FUSED_MERGE 1
 #endif
@@ -437,7 +444,9 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   // kernel, whose short runs start faster.
   const int64_t tile_capacity =
       static_cast<int64_t>(batch) * num_kv_heads * ceil_div(max_context, 16);
-  if (use_mfma && q_len == 1 && batch <= kSkMaxBatch && tile_capacity >= kStreamKMinTiles) {
+  const int64_t sk_min_tiles =
+      kv_fp8 && q_dtype != MSATTN_F32 && RT == 8 ? kStreamKMinTilesFp8Rt8 : kStreamKMinTiles;
+  if (use_mfma && q_len == 1 && batch <= kSkMaxBatch && tile_capacity >= sk_min_tiles) {
     *kind = 1;
     const int units = num_kv_heads * p.rtiles;
     p.sk_group = largest_pow2_divisor_upto(
