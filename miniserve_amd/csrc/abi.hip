@@ -67,6 +67,11 @@ constexpr int kWideMaxPct = MSATTN_WIDE_MAX_PCT;
 #define MSATTN_WIDE_FP8_UNCAPPED 1
 #endif
 constexpr bool kWideFp8Uncapped = MSATTN_WIDE_FP8_UNCAPPED != 0;
+#ifndef MSATTN_DEEP_MIN_PER_CU
+#define MSATTN_DEEP_MIN_PER_CU 4
+#endif
+// Workgroups per CU from which a head_dim-64 partition launch takes the deeper residency.
+constexpr int kDeepMinPerCu = MSATTN_DEEP_MIN_PER_CU;
 
 bool dtype_ok(int d) { return d >= MSATTN_F32 && d <= MSATTN_FP8_E4M3; }
 int dtype_bytes(int d) { return d == MSATTN_F32 ? 4 : (d == MSATTN_FP8_E4M3 ? 1 : 2); }
@@ -426,6 +431,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   p.sk_unit_groups = 0;
   p.sk_min_chunk = kSkMinChunk;
   p.mfma_waves = kMfmaWaves;
+  p.mfma_deep = 0;
   p.key_lo = key_lo;
   p.rope_cos = rope.cos;
   p.rope_sin = rope.sin;
@@ -495,11 +501,11 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
       const int64_t want = static_cast<int64_t>(device_cus()) * kWideSlotsPct / 100;
       const int64_t np = std::max<int64_t>(1, want / triples);
       const int64_t launched = triples * ceil_div(max_context, kPartWide);
-      // An fp8 cache at 4 rows per tile takes the wide shape however many workgroups the
-      // launch holds: its widening work per byte fills two waves per SIMD (5-10 % faster
-      // on H32/KVH8 decodes of 6-20 workgroups per CU); at 8 rows per tile, and over a
-      // 16-bit cache, the cap stands (up to 18 % slower without it).
-      const bool uncapped = kWideFp8Uncapped && kv_fp8 && RT == 4;
+      // An fp8 cache at 4 rows per tile and head_dim 128 takes the wide shape however many
+      // workgroups the launch holds: its widening work per byte fills two waves per SIMD
+      // (5-10 % faster on H32/KVH8 decodes of 6-20 workgroups per CU); at 8 rows per tile,
+      // at head_dim 64 and over a 16-bit cache the cap stands (7-18 % slower without it).
+      const bool uncapped = kWideFp8Uncapped && kv_fp8 && RT == 4 && head_dim == 128;
       if (static_cast<int64_t>(max_context) >= np * kPartWide &&
           (uncapped || 100 * launched <= static_cast<int64_t>(kWideMaxPct) * want)) {
         p.part = kPartWide;
@@ -507,6 +513,13 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
         p.mfma_waves = kWideWaves;
       }
     }
+  }
+  // A regular-shape launch at head_dim 64 of kDeepMinPerCu or more workgroups per CU
+  // holds three a CU instead of two (kMfmaWgPerCuDeep).
+  if (use_mfma && p.mfma_waves == kMfmaWaves && head_dim == 64 && (RT == 4 || RT == 8) &&
+      q_dtype != MSATTN_F32) {
+    const int64_t launched = static_cast<int64_t>(p.max_parts) * num_kv_heads * p.rtiles * batch;
+    if (launched >= static_cast<int64_t>(kDeepMinPerCu) * device_cus()) p.mfma_deep = 1;
   }
   if (use_mfma) {
     e = with_mfma_decode_types(q_dtype, kv_dtype, [&](auto t, auto kt) {

@@ -519,6 +519,14 @@ __device__ __forceinline__ void pv_tile(float (&acc)[RT][8], const float (&pr)[4
 #define MSATTN_MFMA_WG_PER_CU 2
 #endif
 constexpr int kMfmaWgPerCu = MSATTN_MFMA_WG_PER_CU;
+// Partition workgroups a CU may hold in a launch of many workgroups per CU at head_dim 64
+// (the regular shape): there a third resident workgroup hides more of each one's memory
+// round trips (128 x H14/KVH2 at 1-4k tokens: 42.1 -> 37.7 us), while in a launch of about
+// one round it only lengthens a CU's queue (C2: 11.6 -> 13.5 us).
+#ifndef MSATTN_MFMA_WG_PER_CU_DEEP
+#define MSATTN_MFMA_WG_PER_CU_DEEP 3
+#endif
+constexpr int kMfmaWgPerCuDeep = MSATTN_MFMA_WG_PER_CU_DEEP;
 constexpr int kCuLdsBytes = 160 * 1024;  // gfx950 LDS per CU
 constexpr int kMfmaWaves = MSATTN_MFMA_WAVES;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
@@ -608,7 +616,7 @@ __device__ __forceinline__ void rope_chunks(typename QChunk<T>::type (&qb)[D / 3
   }
 }
 
-template <typename T, typename KT, int D, int RT, int W = kMfmaWaves>
+template <typename T, typename KT, int D, int RT, int W = kMfmaWaves, int WPC = kMfmaWgPerCu>
 __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParams p) {
   constexpr int kWaves = W;               // waves per workgroup
   constexpr int kThreads = W * kWave;
@@ -625,10 +633,10 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
   __shared__ float s_red[kWaves][RT][D];
   __shared__ float s_ml[kWaves][RT][2];
   __shared__ int s_last;  // in-kernel merge: this workgroup arrived last
-  // LDS reserved beyond s_red / s_ml so that at most kMfmaWgPerCu workgroups share a
+  // LDS reserved beyond s_red / s_ml so that at most WPC workgroups share a
   // CU (the store below never runs; it keeps the array allocated).
   constexpr int kLdsUsed = static_cast<int>(sizeof(s_red) + sizeof(s_ml));
-  constexpr int kLdsWant = kMfmaWgPerCu > 0 ? kCuLdsBytes / (kMfmaWgPerCu + 1) + 2048 : 0;
+  constexpr int kLdsWant = WPC > 0 ? kCuLdsBytes / (WPC + 1) + 2048 : 0;
   constexpr int kPadFloats = kLdsWant > kLdsUsed ? (kLdsWant - kLdsUsed) / 4 : 1;
   __shared__ float s_pad[kPadFloats];
   if (p.batch < 0) s_pad[threadIdx.x % kPadFloats] = 0.0f;
@@ -650,6 +658,7 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
     p.hdr[kHdrKind] = fused ? 2 : 0;
     p.hdr[kHdrPart] = p.part;
     p.hdr[kHdrWaves] = W;
+    p.hdr[kHdrResidency] = WPC;
   }
   // blockIdx.x = kvh + KVH * (part + max_parts * rtile); blockIdx.z = b.
   const unsigned bx = blockIdx.x;
@@ -1118,11 +1127,11 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
   if (fused) fused_merge();
 }
 
-template <typename T, typename KT, int D, int RT, int W = kMfmaWaves>
+template <typename T, typename KT, int D, int RT, int W = kMfmaWaves, int WPC = kMfmaWgPerCu>
 hipError_t launch_decode_mfma_one(const SplitParams& p, hipStream_t stream) {
   const unsigned gx = static_cast<unsigned>(p.max_parts) * static_cast<unsigned>(p.KVH) *
                       static_cast<unsigned>(p.rtiles);
-  hipLaunchKernelGGL((decode_mfma_kernel<T, KT, D, RT, W>),
+  hipLaunchKernelGGL((decode_mfma_kernel<T, KT, D, RT, W, WPC>),
                      dim3(gx, 1, static_cast<unsigned>(p.batch)), dim3(W * kWave), 0, stream, p);
   return hipGetLastError();
 }

@@ -54,7 +54,8 @@ constexpr int kPartMax = MSATTN_PART_MAX;
 //   kind 1 also: hdr[1] sumT, [2] chunk c, [3] sub-ranges, [4] UG, [5] NUG, [6] B,
 //   [7] RT, and hdr[kHdrPrefix + b] = tiles of sequences before b (b = 0..B).
 //   kinds 0 and 2 (partition kernels) also: hdr[8] partition tokens, [9] waves per
-//   workgroup (the launch's shape, for tests and measurements; the merge does not read them).
+//   workgroup, [14] workgroups a CU may hold (the launch's shape, for tests and
+//   measurements; the merge does not read them).
 //   hdr[kHdrTickets + t], t < kMaxTickets: arrival counters of the in-kernel merge, one
 //   per (sequence, KV head, row tile). They sit at the same offset for every geometry,
 //   must be zero when a workspace is first used, and every call leaves them zero.
@@ -62,7 +63,8 @@ constexpr int kHdrTickets = 64;
 constexpr int kMaxTickets = 4096;
 constexpr int kHdrPrefix = kHdrTickets + kMaxTickets;
 constexpr int kHdrKind = 0, kHdrSumT = 1, kHdrChunk = 2, kHdrNsub = 3, kHdrUG = 4,
-              kHdrNUG = 5, kHdrB = 6, kHdrRT = 7, kHdrPart = 8, kHdrWaves = 9;
+              kHdrNUG = 5, kHdrB = 6, kHdrRT = 7, kHdrPart = 8, kHdrWaves = 9,
+              kHdrResidency = 14;
 
 struct SplitParams {
   int* hdr;
@@ -98,6 +100,7 @@ struct SplitParams {
   void* out;
   int* tickets;
   int mfma_waves;  // partition MFMA kernel: waves per workgroup (4, or 8 for long partitions)
+  int mfma_deep;   // partition MFMA kernel, regular shape at head_dim 64: the deeper residency
 };
 
 // Position of row b's query for RoPE, clamped into the tables.

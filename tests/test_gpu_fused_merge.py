@@ -243,3 +243,31 @@ def test_wide_shape_long_contexts(device, name):
             err = float(np.abs(f - ref).max() / max(np.abs(ref).max(), 1e-30))
             assert err < BF16_REL, err
         note(f"oracle err {err:.3e}, partition {int(hdr[8])}")
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_deep_residency_head_dim_64(device, kv_dtype):
+    """A head_dim-64 partition decode of many workgroups per CU (128 sequences x 2 KV heads
+    of 1-3.8k tokens over 512-token partitions: eight per CU) holds three workgroups a CU
+    instead of two: the header must name that residency, and the output must meet the
+    float64 oracle's bar on two consecutive calls (the merge counters back at zero). The
+    table (61,440 tiles of capacity) stays below the fp8 cache's stream-K threshold."""
+    H, KVH, D, B, width = 14, 2, 64, 128, 240
+    caller = Caller(device, 64 << 20)
+    for i in range(2):
+        g = torch.Generator().manual_seed(500 + i)
+        lens = [int(x) for x in torch.randint(1024, width * 16 + 1, (B,), generator=g)]
+        lens[0], lens[1] = 0, 1
+        note(f"deep residency kv={kv_dtype} call {i}: sum {sum(lens)}")
+        q, kc, vc, table = make(H, KVH, D, lens, torch.bfloat16, width, seed=600 + i)
+        kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+        fused, two, hdr, hdr2 = caller.run(q, kc, vc, table, lens)
+        assert (int(hdr[0]), int(hdr[9]), int(hdr[14])) == (2, 4, 3), hdr[:16].tolist()
+        assert not hdr[HDR_TICKETS:].any(), "merge counters not left at zero"
+        assert not fused[0].cpu().any()
+        ref = dense.paged_attention_f64(q, kc, vc, table.long(), lens, kv_cast=True)
+        for out in (fused, two):
+            f = out.double().cpu().numpy()
+            err = float(np.abs(f - ref).max() / max(np.abs(ref).max(), 1e-30))
+            assert err < BF16_REL, err
+        note(f"oracle err {err:.3e}")
