@@ -611,14 +611,40 @@ namespace {
 // Chunked prefill (more than one 16-row tile of query rows per KV head) on the MFMA
 // prefill kernel, which writes the normalised output directly, four elements (8 bytes)
 // a store, and uses no workspace.
+// Query rows per KV head (q_len x G) above which a multi-token query may take the chunked
+// prefill kernel; at or below it, the partition decode kernel's 16-row tiles.
+#ifndef MSATTN_PREFILL_MIN_ROWS
+#define MSATTN_PREFILL_MIN_ROWS 16
+#endif
+constexpr int64_t kPrefillMinRows = MSATTN_PREFILL_MIN_ROWS;
+// Past that, the prefill kernel runs one workgroup per (sequence, KV head, 128-row block)
+// over the whole context, so a launch of few such tasks leaves CUs idle, while the
+// partition kernel splits the keys over many workgroups but reads the K/V rows once per
+// 16-row tile. The partition kernel is taken when (16-row tiles x sequences x KV heads)
+// is at most kPrefillSplitPct percent of (CUs x the prefill launch's rounds of one task
+// per CU): measured speculative-decoding shapes (q_len 3-16, G 4-7, contexts 1-8k) ran
+// 1.1-3x faster there (8 x q_len 4 at G 7: 150.6 -> 49.7 us) and slower past it (64 x
+// q_len 6 at G 4: 157.5 against 241.8 us on the partition kernel).
+#ifndef MSATTN_PREFILL_SPLIT_PCT
+#define MSATTN_PREFILL_SPLIT_PCT 100
+#endif
+constexpr int64_t kPrefillSplitPct = MSATTN_PREFILL_SPLIT_PCT;
+
 bool direct_prefill_route(const void* query, const void* out, int64_t cache_slot_stride,
                           int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
                           int block_size, int q_dtype, int kv_dtype) {
-  return q_len > 1 &&
-         mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, cache_slot_stride) &&
-         aligned(out, 8) && batch <= 65535 && num_heads > 0 && num_kv_heads > 0 &&
-         num_heads % num_kv_heads == 0 &&
-         static_cast<int64_t>(q_len) * (num_heads / num_kv_heads) > 16;
+  if (!(q_len > 1 &&
+        mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, cache_slot_stride) &&
+        aligned(out, 8) && batch <= 65535 && num_heads > 0 && num_kv_heads > 0 &&
+        num_heads % num_kv_heads == 0))
+    return false;
+  const int64_t rows = static_cast<int64_t>(q_len) * (num_heads / num_kv_heads);
+  if (rows <= kPrefillMinRows) return false;
+  const int64_t pairs = static_cast<int64_t>(batch) * num_kv_heads;
+  const int64_t tasks = pairs * ((rows + kPfRows - 1) / kPfRows);
+  const int64_t cus = device_cus();
+  const int64_t rounds = (tasks + cus - 1) / cus;
+  return 100 * ((rows + 15) / 16) * pairs > kPrefillSplitPct * cus * rounds;
 }
 
 // msattn_paged_attention's body. `prefill_needs_ws`: whether the direct prefill route

@@ -227,10 +227,41 @@ def test_fp8_kv_mfma_equals_dequantized(device, H, KVH, D, dtype, wide, window):
     assert not got[0].any()
 
 
+@pytest.mark.parametrize("B,H,KVH,D,q_len,kv_dtype", [
+    (8, 28, 4, 128, 4, torch.bfloat16),      # 28 rows per KV head, 32 (sequence, KV head)s
+    (4, 32, 8, 128, 16, torch.bfloat16),     # 64 rows: four 16-row tiles
+    (32, 14, 2, 64, 3, torch.bfloat16),      # head_dim 64
+    (16, 32, 8, 128, 5, torch.float8_e4m3fn),
+])
+def test_speculative_rows_on_partition_kernel(device, B, H, KVH, D, q_len, kv_dtype):
+    """Multi-token queries (speculative decoding: q_len 3-16, more than 16 rows per KV head)
+    over few (sequence, KV head) pairs take the partition kernel's 16-row tiles, which
+    split the keys over many workgroups, rather than the prefill kernel's one workgroup per
+    128-row block: the header must name the in-kernel-merge route, and the causal result
+    must meet the float64 oracle's bar."""
+    g = torch.Generator().manual_seed(B * q_len)
+    lens = [int(x) for x in torch.randint(max(q_len, 900), 6001, (B,), generator=g)]
+    bs = 16
+    width = (max(lens) + bs - 1) // bs + 1
+    note(f"speculative rows B={B} H={H} KVH={KVH} D={D} q_len={q_len} kv={kv_dtype}")
+    q, kc, vc, table = paged_case(H, KVH, D, lens, torch.bfloat16, bs, width, seed=B + q_len,
+                                  q_len=q_len)
+    kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=device)
+    out = paged_attention(q.to(device), kc.to(device), vc.to(device), table, lens,
+                          max_context=width * bs, workspace=ws)
+    torch.cuda.synchronize()
+    assert int(ws[:4].view(torch.int32).item()) == 2  # partition kernel, merged in-kernel
+    ref = dense.paged_attention_f64(q, kc, vc, table, lens)
+    err = rel_err(out, ref)
+    note(f"speculative rows max-rel {err:.3e}")
+    assert err < BF16_REL
+
+
 @pytest.mark.parametrize("H,KVH,D,q_len,dtype,causal,window,prefix", [
     (28, 4, 128, 512, torch.bfloat16, True, None, 0),     # chunked prefill (C5 shape)
     (32, 8, 128, 100, torch.float16, True, 64, 0),        # fp16 query, sliding window
-    (16, 2, 128, 48, torch.bfloat16, False, None, 0),     # non-causal
+    (16, 2, 128, 96, torch.bfloat16, False, None, 0),     # non-causal
     (14, 2, 64, 200, torch.bfloat16, True, None, 0),      # head_dim 64
     (32, 8, 128, 1, torch.bfloat16, True, None, 12),      # cascade decode: the prefix pass
 ])
