@@ -286,15 +286,17 @@ def main():
     # (1 = stream-K); otherwise the partition kernel, on MFMA with head_dim 64 or 128 for a
     # bf16/fp16 query over its own type, fp8 or fp32 and for an fp32 query over fp32, else
     # the generic kernel.
-    hdr = ws[:40].view(torch.int32).cpu()
+    hdr = ws[:64].view(torch.int32).cpu()
     kind = int(hdr[0])
     # The partition kernels record their launch's partition length and waves per
     # workgroup in header words 8 and 9 (the wide shape takes longer partitions than
-    # msattn_partition_tokens reports).
+    # msattn_partition_tokens reports), and in word 14 the workgroups per CU the MFMA
+    # kernel was built to keep resident (0: the compiler's own occupancy).
     if kind in (0, 2) and int(hdr[8]) > 0:
         part_tokens, part_waves = int(hdr[8]), int(hdr[9])
+        part_residency = int(hdr[14])
     else:
-        part_waves = None
+        part_waves = part_residency = None
     kv_t = w.k_caches[0].dtype
     mfma_pair = ((w.dtype in (torch.bfloat16, torch.float16)
                   and kv_t in (w.dtype, torch.float8_e4m3fn, torch.float32))
@@ -362,7 +364,7 @@ def main():
             "batch": B, "q_len": 1, "num_heads": H, "num_kv_heads": KVH, "head_dim": D,
             "block_size": bs, "layers": w.layers, "context_tokens": sum(w.lens),
             "pool_pages": w.num_blocks, "partition_tokens": part_tokens,
-            "partition_waves": part_waves,
+            "partition_waves": part_waves, "partition_wg_per_cu": part_residency,
             "algorithmic_bytes_per_layer": per_layer_bytes,
             "shared_prefix_pages": w.shared_prefix_pages, "cascade": bool(cascade),
             "kv_dtype": str(w.k_caches[0].dtype).replace("torch.", ""),

@@ -146,6 +146,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
     p.hdr[kHdrKind] = 0;
     p.hdr[kHdrPart] = p.part;
     p.hdr[kHdrWaves] = kSplitWaves;
+    p.hdr[kHdrResidency] = 0;
   }
 
   // blockIdx.x = part + max_parts * (kvh + KVH * rtile); blockIdx.z = b.
