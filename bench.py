@@ -38,6 +38,7 @@ if str(ROOT) not in sys.path:
 METRIC = ("paged-decode µs/layer; KV-read HBM GB/s as % of peak (bs64, ctx<=8k, 1 GPU)")
 HBM_PEAK_GBS = 8000.0
 PROFILES = ROOT / "profiles"
+MIN_WARMUP_REPLAYS = 5
 
 
 def parse():
@@ -66,6 +67,15 @@ def parse():
                     help="C5's chunked-prefill part (2 x 512 query tokens onto 4096 cached): "
                          "MFMA-bound, reported in TFLOP/s; with --q-dtype fp32 --kv-dtype fp32 "
                          "the reference runner's types, priced against the fp32 matrix peak")
+    ap.add_argument("--runner", action="store_true",
+                    help="time GraphedDecodeRunner.decode (one bucketed hipGraph decode step "
+                         "per call, write_kv included, host-side input staging included) on "
+                         "the config's decode shape (C2: bucket 32, 24 layers; C3: bucket 64)")
+    ap.add_argument("--eager", action="store_true",
+                    help="time PagedAttention.write_kv + forward called per layer as the "
+                         "reference runner calls them (model_runner.py:72-76: transposed q/k/v "
+                         "views, an int64 device table, Python-list starts and lengths), "
+                         "against the kernel's own time")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--stream-probe", action="store_true",
@@ -139,6 +149,14 @@ def stream_read_gbs(dev, launches: int = 20) -> float:
     return nbytes / (ms * 1e-3) / 1e9
 
 
+def warmup_replays(warmup: int, steps_per_graph: int) -> int:
+    """Untimed replays of a captured graph before the timed ones: the --warmup steps'
+    worth, and never fewer than MIN_WARMUP_REPLAYS (the first replays of a new graph run
+    slower than the steady state: a 20-step run after 5 warm-up steps, one replay, came
+    out 3.5 % above a 200-step run)."""
+    return max(MIN_WARMUP_REPLAYS, -(-warmup // steps_per_graph))
+
+
 def graph_steps(args) -> int:
     """Steps captured per graph: --graph-steps, else the largest divisor of K up to 10."""
     if args.graph_steps > 0:
@@ -162,11 +180,17 @@ def main():
     if args.prefill:
         prefill_bench(args)
         return
+    if args.runner:
+        runner_bench(args)
+        return
+    if args.eager:
+        eager_bench(args)
+        return
 
     import torch
 
     from miniserve_amd import _native as nat
-    from miniserve_amd.attention import paged_attention
+    from miniserve_amd.attention import kernel_route, paged_attention
     from miniserve_amd.workloads import make_workload
 
     if not torch.cuda.is_available():
@@ -227,7 +251,7 @@ def main():
             for _ in range(n_in_graph):
                 step()
         torch.cuda.synchronize()
-        for _ in range(max(1, args.warmup // n_in_graph)):
+        for _ in range(warmup_replays(args.warmup, n_in_graph)):
             graph.replay()
         torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -297,18 +321,20 @@ def main():
         part_residency = int(hdr[14])
     else:
         part_waves = part_residency = None
-    kv_t = w.k_caches[0].dtype
-    mfma_pair = ((w.dtype in (torch.bfloat16, torch.float16)
-                  and kv_t in (w.dtype, torch.float8_e4m3fn, torch.float32))
-                 or (w.dtype == torch.float32 and kv_t == torch.float32))
-    if fused:
-        kernel_name = "msattn::decode_mfma_kernel (partition split-K, merged in-kernel)"
-    elif kind == 1:
-        kernel_name = "msattn::decode_streamk_kernel (stream-K split-K partials)"
-    elif mfma_pair and D in (64, 128):
-        kernel_name = "msattn::decode_mfma_kernel (partition split-K partials)"
-    else:
-        kernel_name = "msattn::split_kernel (generic partition split-K partials)"
+    # The kernel the library routes this call to (msattn_paged_attention_route); the
+    # header's kind after the call must agree with it.
+    route = kernel_route(q, w.k_caches[0], table, max_context=max_ctx, out=outs[0])
+    kernel_name = {
+        "partition-fused": "msattn::decode_mfma_kernel (partition split-K, merged in-kernel)",
+        "stream-K": "msattn::decode_streamk_kernel (stream-K split-K partials)",
+        "partition": "msattn::decode_mfma_kernel (partition split-K partials)",
+        "generic": "msattn::split_kernel (generic partition split-K partials)",
+    }[route]
+    if cascade:  # the suffix pass: stream-K or the partition kernel, then the merge
+        kernel_name = ("msattn::decode_streamk_kernel (stream-K split-K partials)" if kind == 1
+                       else "msattn::decode_mfma_kernel (partition split-K partials)")
+    elif {"partition-fused": 2, "stream-K": 1}.get(route, 0) != kind:
+        raise SystemExit(f"route {route} but workspace kind {kind}")
     split_ms = sorted(a.elapsed_time(b) for a, b, _ in evs)
     merge_ms = sorted(b.elapsed_time(c) for _, b, c in evs)
     split_avg = sum(split_ms) / len(split_ms)
@@ -398,11 +424,13 @@ def main():
 
 
 def prefill_bench(args):
-    """C5 prefill: one forward over 2 x 512 query rows, captured in a hipGraph."""
+    """C5 prefill: one forward over 2 x 512 query rows, captured in a hipGraph; the kernel
+    itself timed per launch with HIP events on its stream; the reference's CPU path on a
+    bounded sample of the same call."""
     import torch
 
     from miniserve_amd import _native as nat
-    from miniserve_amd.attention import paged_attention
+    from miniserve_amd.attention import kernel_route, paged_attention
     from miniserve_amd.workloads import make_workload
 
     dev = torch.device("cuda:0")
@@ -414,16 +442,19 @@ def prefill_bench(args):
         w.k_caches = [c.to(kv_torch) for c in w.k_caches]
         w.v_caches = [c.to(kv_torch) for c in w.v_caches]
     B, T, H, D = w.query.shape
+    KVH = w.num_kv_heads
     table = w.table.to(device=dev, dtype=torch.int32).contiguous()
     lens = torch.tensor(w.lens, dtype=torch.int32, device=dev)
     cap = table.shape[1] * w.block_size
     out = torch.empty_like(w.query)
-    ws_bytes = nat.lib().msattn_workspace_bytes(B, T, H, w.num_kv_heads, D, cap)
+    lib = nat.lib()
+    ws_bytes = lib.msattn_workspace_bytes(B, T, H, KVH, D, cap)
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    kc, vc = w.k_caches[0], w.v_caches[0]
+    route = kernel_route(w.query, kc, table, max_context=cap, out=out)
 
     def step():
-        paged_attention(w.query, w.k_caches[0], w.v_caches[0], table, lens, max_context=cap,
-                        workspace=ws, out=out)
+        paged_attention(w.query, kc, vc, table, lens, max_context=cap, workspace=ws, out=out)
 
     side = torch.cuda.Stream(dev)
     side.wait_stream(torch.cuda.current_stream(dev))
@@ -437,7 +468,7 @@ def prefill_bench(args):
         with torch.cuda.graph(graph):
             for _ in range(n_in_graph):
                 step()
-        for _ in range(max(1, args.warmup // n_in_graph)):
+        for _ in range(warmup_replays(args.warmup, n_in_graph)):
             graph.replay()
         torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -450,30 +481,68 @@ def prefill_bench(args):
 
     ms_single = timed(1)
     ms = timed(gsteps) if gsteps > 1 else ms_single
+
+    # The kernel per launch: msattn_paged_attention is one launch on this route (the
+    # prefill kernel, or the partition kernel merging in-kernel), bracketed by HIP events
+    # on the stream it is launched on, back to back as in the graph.
+    stream = nat.stream_handle(dev)
+    qcode, kvcode = nat.dtype_code(w.query.dtype), nat.dtype_code(kc.dtype)
+    n_k = max(10, min(args.steps, 200))
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n_k)]
+    for i in range(n_k + 5):
+        e = evs[i - 5] if i >= 5 else None
+        if e:
+            e[0].record()
+        st = lib.msattn_paged_attention(
+            w.query.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
+            kc.stride(2), table.data_ptr(), lens.data_ptr(), out.data_ptr(), ws.data_ptr(),
+            ws_bytes, B, T, H, KVH, D, w.block_size, w.num_blocks, table.shape[1], cap, 1, 0,
+            w.scale, qcode, kvcode, stream)
+        nat.check("prefill", st)
+        if e:
+            e[1].record()
+    torch.cuda.synchronize()
+    k_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    k_avg = sum(k_ms) / len(k_ms)
+
     # causal: row i of a sequence with context L sees L - T + i + 1 keys
     flops = sum(4 * D * H * (L - T + i + 1) for L in w.lens for i in range(T) if L - T + i + 1 > 0)
     tflops = flops / (ms * 1e-3) / 1e12
+    k_tflops = flops / (k_avg * 1e-3) / 1e12
     fp32 = w.query.dtype == torch.float32
     # MI355X dense matrix peaks: bf16 2.5 PFLOP/s, fp32 157.3 TFLOP/s.
     peak = 157.3 if fp32 else 2500.0
-    kernel = ("msattn::decode_mfma_kernel (fp32, 16-row tiles, P.V on the matrix core, "
-              "merged in-kernel)" if fp32 and w.k_caches[0].dtype == torch.float32
-              else "msattn::prefill_mfma_kernel")
-    print(json.dumps({
+    kernel = {"prefill": "msattn::prefill_mfma_kernel",
+              "partition-fused": "msattn::decode_mfma_kernel (16-row tiles, merged in-kernel)"
+              }.get(route, route)
+    result = {
         "metric": "C5 chunked-prefill attention (2 x 512 tokens onto 4096 cached)",
         "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
         "dtype": "f32" if fp32 else "bf16",
         "data": "synthetic: seeded N(0,1) q/K/V, scattered block tables",
-        "config": {"workload": "C5-prefill", "batch": B, "q_len": T, "num_heads": H,
-                   "num_kv_heads": w.num_kv_heads, "head_dim": D, "flops": flops,
-                   "kv_dtype": str(w.k_caches[0].dtype).replace("torch.", ""),
-                   "steps_per_graph": gsteps, "us_per_step_one_per_graph": round(ms_single * 1e3, 2)},
+        "config": {"workload": "C5-prefill: causal chunked prefill, H28/KVH4/D128, 2 sequences "
+                               "x 512 new tokens onto 4096 cached, hipGraph replay",
+                   "batch": B, "q_len": T, "num_heads": H,
+                   "num_kv_heads": KVH, "head_dim": D, "flops": flops,
+                   "kv_dtype": str(kc.dtype).replace("torch.", ""), "route": route,
+                   "steps_per_graph": gsteps,
+                   "us_per_step_one_per_graph": round(ms_single * 1e3, 2)},
         "roofline": {"kernel": kernel, "bound": "mfma",
-                     "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(tflops / peak, 4), "traffic": None},
+                     "achieved": round(k_tflops, 1), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(k_tflops / peak, 4), "traffic": None,
+                     "kernel_avg_us": round(k_avg * 1e3, 2),
+                     "kernel_median_us": round(k_ms[len(k_ms) // 2] * 1e3, 2),
+                     "kernel_min_us": round(k_ms[0] * 1e3, 2),
+                     "library_sha256": library_sha256()},
+        "cpu_baseline": None,
         "reference_gpu": reference_forward_us(w, table, lens, T),
-    }), flush=True)
+    }
+    if not args.no_cpu_baseline and args.kv_dtype == "same" and args.q_dtype == "same":
+        result["cpu_baseline"] = cpu_baseline_prefill(w, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
 
 
 def reference_forward_us(w, table, lens, T) -> dict:
@@ -582,6 +651,221 @@ def cpu_baseline(w, target_s: float):
         "sample": f"rows 0..{n_rows - 1} of {w.name} ({tokens} of {full_tokens} context tokens), "
                   f"median of 5 runs of the oracle's SDPA restatement in {str(w.dtype)[6:]}",
         "us_per_layer_extrapolated": round(med * 1e6 * full_tokens / tokens, 1),
+        "cpu_model": cpu_model(),
+        "torch": torch.__version__,
+    }
+
+
+def _decode_inputs(w, dev):
+    """Per-layer new-token q/k/v of a decode step ([layers, batch, 1, heads, D]), seeded."""
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(7)
+    shape_q = (w.layers, w.batch, 1, w.num_heads, w.head_dim)
+    shape_kv = (w.layers, w.batch, 1, w.num_kv_heads, w.head_dim)
+    q = torch.randn(shape_q, generator=g, device=dev).to(w.dtype)
+    k = torch.randn(shape_kv, generator=g, device=dev).to(w.dtype)
+    v = torch.randn(shape_kv, generator=g, device=dev).to(w.dtype)
+    return q, k, v
+
+
+def runner_bench(args):
+    """GraphedDecodeRunner.decode on the config's decode batch: each call stages the
+    inputs (q/k/v copies, block tables and lengths from host lists), replays the bucket's
+    captured graph (write_kv + attention per layer) and copies the output out. Timed on
+    the host clock over whole calls (synchronised at the end), and the device time of the
+    replays alone with events."""
+    import torch
+
+    from miniserve_amd import PagedAttention
+    from miniserve_amd.graphs import DecodeLayer, GraphedDecodeRunner
+    from miniserve_amd.workloads import make_workload
+
+    dev = torch.device("cuda:0")
+    w = make_workload(args.config, device=dev, values_device=dev, part="decode")
+    B, H, KVH, D, bs = w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    layers = [DecodeLayer(PagedAttention(H, KVH, D, num_blocks=w.num_blocks, block_size=bs,
+                                         dtype=w.dtype, kv_dtype=w.k_caches[i].dtype,
+                                         device=dev), w.k_caches[i], w.v_caches[i])
+              for i in range(w.layers)]
+    width = w.table.shape[1]
+    runner = GraphedDecodeRunner(layers, table_width=width, buckets=(1, 2, 4, 8, 16, 32, 64))
+    # every row's last cached token is rewritten with its new k/v each step, so the
+    # context stays the workload's
+    ctx = [max(L - 1, 0) for L in w.lens]
+    tables = [w.table[b, : -(-w.lens[b] // bs)].tolist() for b in range(B)]
+    q, k, v = _decode_inputs(w, dev)
+    bucket = next(b for b in runner.buckets if b >= B)
+    for _ in range(max(MIN_WARMUP_REPLAYS, args.warmup)):  # captures both input sets
+        runner.decode(q, k, v, tables, ctx)
+    torch.cuda.synchronize()
+    n = args.steps
+    t0 = time.perf_counter()
+    for _ in range(n):
+        runner.decode(q, k, v, tables, ctx)
+    torch.cuda.synchronize()
+    wall_us = (time.perf_counter() - t0) / n * 1e6
+    # device time of the replays alone
+    graphs = runner._graphs[bucket]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(n):
+        graphs[i % 2]()
+    stop.record()
+    torch.cuda.synchronize()
+    replay_us = start.elapsed_time(stop) / n * 1e3
+    bytes_step = w.algorithmic_bytes(unique=True) * w.layers
+    print(json.dumps({
+        "metric": "GraphedDecodeRunner.decode step (bucketed hipGraph: write_kv + attention "
+                  "per layer)",
+        "value": round(wall_us, 2), "unit": "us/step (host clock, whole call)",
+        "n_gpus": 1, "steps": n, "higher_is_better": False,
+        "replay_us_per_step": round(replay_us, 2),
+        "replay_us_per_layer": round(replay_us / w.layers, 2),
+        "host_us_per_step": round(wall_us - replay_us, 2),
+        "replay_gbs": round(bytes_step / (replay_us * 1e-6) / 1e9, 1),
+        "config": {"workload": f"{w.name} decode through GraphedDecodeRunner", "batch": B,
+                   "bucket": bucket, "layers": w.layers, "num_heads": H, "num_kv_heads": KVH,
+                   "head_dim": D, "table_width": width,
+                   "dtype": str(w.dtype).replace("torch.", "")},
+    }), flush=True)
+
+
+def eager_bench(args):
+    """The reference runner's eager per-layer calls (model_runner.py:72-76) on the
+    config's decode batch: write_kv with transposed k/v views and a Python-list start,
+    then forward with a transposed q view, the int64 device block table and a
+    Python-list context_lens. Host clock over N layers (synchronised at the end), against
+    the attention kernel alone (HIP events, the same call through the C ABI)."""
+    import torch
+
+    from miniserve_amd import PagedAttention
+    from miniserve_amd import _native as nat
+    from miniserve_amd.workloads import make_workload
+
+    dev = torch.device("cuda:0")
+    w = make_workload(args.config, device=dev, values_device=dev, part="decode")
+    B, H, KVH, D, bs = w.batch, w.num_heads, w.num_kv_heads, w.head_dim, w.block_size
+    kc, vc = w.k_caches[0], w.v_caches[0]
+    pa = PagedAttention(H, KVH, D, num_blocks=w.num_blocks, block_size=bs, dtype=w.dtype,
+                        kv_dtype=kc.dtype, device=dev)
+    table64 = w.table.to(dev)  # int64, as the reference runner keeps it
+    starts = [max(L - 1, 0) for L in w.lens]
+    lens_list = [s + 1 for s in starts]
+    q5, k5, v5 = _decode_inputs(w, dev)
+    # the runner's views: [B, H, 1, D] projections transposed to [B, 1, H, D]
+    q = q5[0].transpose(1, 2).contiguous().transpose(1, 2)
+    k = k5[0].transpose(1, 2).contiguous().transpose(1, 2)
+    v = v5[0].transpose(1, 2).contiguous().transpose(1, 2)
+
+    def layer_call(write=True):
+        if write:
+            pa.write_kv(kc, vc, k, v, table64, start=starts)
+        return pa.forward(q, kc, vc, table64, lens_list)
+
+    for _ in range(max(MIN_WARMUP_REPLAYS, args.warmup)):
+        layer_call()
+    torch.cuda.synchronize()
+    n = args.steps
+
+    def host_clock(write):
+        t0 = time.perf_counter()
+        for _ in range(n):
+            layer_call(write)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e6
+
+    both_us = host_clock(True)
+    fwd_us = host_clock(False)
+    # the attention kernel alone, through the C ABI on prepared device inputs
+    lib = nat.lib()
+    qc = q.contiguous()
+    table = table64.to(torch.int32)
+    lens = torch.tensor(lens_list, dtype=torch.int32, device=dev)
+    max_ctx = max(lens_list)
+    ws_bytes = lib.msattn_workspace_bytes(B, 1, H, KVH, D, max_ctx)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(qc)
+    stream = nat.stream_handle(dev)
+
+    def raw():
+        nat.check("attention", lib.msattn_paged_attention(
+            qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
+            kc.stride(2), table.data_ptr(), lens.data_ptr(), out.data_ptr(), ws.data_ptr(),
+            ws_bytes, B, 1, H, KVH, D, bs, w.num_blocks, table.shape[1], max_ctx, 1, 0, w.scale,
+            nat.dtype_code(w.dtype), nat.dtype_code(kc.dtype), stream))
+
+    for _ in range(5):
+        raw()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(n):
+        raw()
+    stop.record()
+    torch.cuda.synchronize()
+    kernel_us = start.elapsed_time(stop) / n * 1e3
+    t0 = time.perf_counter()
+    for _ in range(n):
+        raw()
+    torch.cuda.synchronize()
+    raw_host_us = (time.perf_counter() - t0) / n * 1e6
+    print(json.dumps({
+        "metric": "eager PagedAttention per layer as the reference runner calls it "
+                  "(write_kv + forward)",
+        "value": round(both_us, 2), "unit": "us/layer (host clock)", "n_gpus": 1, "steps": n,
+        "higher_is_better": False,
+        "forward_us": round(fwd_us, 2),
+        "write_kv_us": round(both_us - fwd_us, 2),
+        "kernel_us": round(kernel_us, 2),
+        "c_abi_call_host_us": round(raw_host_us, 2),
+        "forward_overhead_us": round(fwd_us - max(kernel_us, raw_host_us), 2),
+        "config": {"workload": f"{w.name} decode, one layer, eager", "batch": B,
+                   "num_heads": H, "num_kv_heads": KVH, "head_dim": D,
+                   "dtype": str(w.dtype).replace("torch.", ""),
+                   "kv_dtype": str(kc.dtype).replace("torch.", "")},
+    }), flush=True)
+
+
+def cpu_baseline_prefill(w, target_s: float):
+    """The reference's CPU path for the C5 prefill call (the oracle's restatement of
+    attention.py:205-250: gather to the longest context, GQA expand, causal mask, torch
+    SDPA in the config dtype) on a bounded sample: the whole call when it runs in about
+    `target_s` seconds or less, else its first sequence (same chunk, same context).
+    Reported as TFLOP/s of the sample's causal attention."""
+    import torch
+
+    from oracle import paged_sdpa
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    kc, vc, q = w.k_caches[0].cpu(), w.v_caches[0].cpu(), w.query.cpu()
+    T, H, D = q.shape[1], q.shape[2], q.shape[3]
+    rows = list(range(w.batch))
+    args = (q, kc, vc, w.table, list(w.lens))
+    t = time.perf_counter()
+    paged_sdpa.paged_attention_sdpa(*args)
+    first = time.perf_counter() - t
+    if first * 3 > target_s and w.batch > 1:
+        rows = [0]
+        args = (q[rows], kc, vc, w.table[rows], [w.lens[0]])
+    runs = 3
+    times = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        paged_sdpa.paged_attention_sdpa(*args)
+        times.append(time.perf_counter() - t)
+    med = sorted(times)[len(times) // 2]
+    flops = sum(4 * D * H * (w.lens[b] - T + i + 1) for b in rows for i in range(T)
+                if w.lens[b] - T + i + 1 > 0)
+    return {
+        "value": round(flops / med / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"sequence(s) {rows} of C5-prefill ({len(rows) * T} query rows onto "
+                  f"{w.lens[0]}-token contexts), median of {runs} runs of the oracle's SDPA "
+                  f"restatement in {str(q.dtype)[6:]}",
+        "us_per_call_extrapolated": round(med * 1e6 * w.batch / len(rows), 1),
         "cpu_model": cpu_model(),
         "torch": torch.__version__,
     }

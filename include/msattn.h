@@ -49,6 +49,15 @@ typedef enum msattn_status {
   MSATTN_ERR_HIP = 4,          /* a HIP launch reported an error */
 } msattn_status;
 
+/* Kernel routes of msattn_paged_attention (msattn_paged_attention_route). */
+typedef enum msattn_route {
+  MSATTN_ROUTE_PREFILL = 1,          /* chunked-prefill MFMA kernel; output written directly */
+  MSATTN_ROUTE_PARTITION_FUSED = 2,  /* MFMA partition kernel, split-K merged in-kernel */
+  MSATTN_ROUTE_PARTITION = 3,        /* MFMA partition kernel, then the merge kernel */
+  MSATTN_ROUTE_STREAMK = 4,          /* MFMA stream-K decode kernel, then the merge kernel */
+  MSATTN_ROUTE_GENERIC = 5,          /* generic VALU kernel, then the merge kernel */
+} msattn_route;
+
 /* ABI version (MSATTN_ABI_VERSION). No reference counterpart. */
 int msattn_abi_version(void);
 
@@ -93,15 +102,19 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
  * window <= 0 means no sliding window. q_dtype and kv_dtype may differ: the cache is
  * cast to the query type as it is read (exact when widening, round to nearest even when
  * narrowing), as the reference casts the gathered K/V to query.dtype
- * (miniserve/attention.py:240-241). Decode (q_len 1, or at most 16 query rows per KV
- * head) runs on the MFMA kernels for a bf16/fp16 query over a cache of its type, fp8 e4m3
- * or fp32, and for an fp32 query over any cache (head_dim 64 or 128, 16-byte aligned
- * query, block_size a multiple of 16); an fp32 query's chunked prefill (more than 16 query
- * rows per KV head) also runs there. Other pairs and shapes take the generic kernel.
+ * (miniserve/attention.py:240-241). head_dim may be any even size up to 256. Decode
+ * (q_len 1, or at most 16 query rows per KV head) runs on the MFMA kernels for a bf16/fp16
+ * query over a cache of its type, fp8 e4m3 or fp32, and for an fp32 query over any cache
+ * (head_dim 64 or 128, 16-byte aligned query, cache pointers and strides on 16-byte
+ * boundaries, block_size a multiple of 16); an fp32 query's chunked prefill (more than 16
+ * query rows per KV head) also runs there. Other pairs and shapes take the generic kernel,
+ * which needs only element-aligned caches. msattn_paged_attention_route names the route.
  * Runs msattn_paged_attention_partials followed by msattn_merge_partials, except:
  * chunked prefill on the MFMA kernel (bf16/fp16 query 16-byte aligned, output 8-byte
  * aligned, cache of the query's type, fp8 e4m3 or fp32, head_dim 64 or 128, more than 16
- * query rows per KV head), which writes the output directly; and decodes on the MFMA
+ * query rows per KV head, and either more than 64 rows per KV head or enough
+ * (sequence, KV head) pairs to fill the device; fewer go to the partition kernel, which
+ * splits their keys over more workgroups), which writes the output directly; and decodes on the MFMA
  * partition kernel (those below the stream-K threshold, with batch x num_kv_heads x row
  * tiles <= 4096), which merge in-kernel in one launch: the last partition of each
  * (sequence, KV head, row tile) to finish folds the others' partials into `out`, and a
@@ -126,9 +139,10 @@ int msattn_paged_attention(const void* query, const void* k_cache, const void* v
  * the split-K partials go to a scratch array of MSATTN_NOALLOC_SCRATCH_BYTES that the
  * library holds on each device it runs on (allocated with the library's code object,
  * kept until the process ends); its address is looked up on the first call on a device.
- * A call whose msattn_workspace_bytes exceeds that size returns MSATTN_ERR_WORKSPACE
- * (chunked prefill on the MFMA kernel needs no scratch and is not limited); it calls no
- * allocator. Every call on one device shares that device's scratch: calls that overlap
+ * A call whose msattn_workspace_bytes exceeds that size runs a chunked prefill on the
+ * prefill kernel when that kernel can take it (it needs no scratch; this includes
+ * chunked prefills msattn_paged_attention would send to the partition kernel), and
+ * otherwise returns MSATTN_ERR_WORKSPACE; it calls no allocator. Every call on one device shares that device's scratch: calls that overlap
  * in time on one device (two streams, two threads) race and must be serialised by the
  * caller. The scratch keeps the last call's contents; nothing in it needs clearing.
  */
@@ -141,6 +155,23 @@ int msattn_paged_attention_noalloc(const void* query, const void* k_cache, const
                                    int num_blocks, int table_width, int max_context, int causal,
                                    int window, float scale, int q_dtype, int kv_dtype,
                                    void* stream);
+
+/*
+ * The kernel route (msattn_route) that msattn_paged_attention takes for a call with these
+ * pointers, strides and sizes and a workspace of workspace_bytes (pass
+ * MSATTN_NOALLOC_SCRATCH_BYTES for msattn_paged_attention_noalloc), written to *route.
+ * The choice depends on sizes, types and alignment only (capture-safe), never on the
+ * context lengths' values. Returns MSATTN_ERR_WORKSPACE when the call would need more
+ * workspace than workspace_bytes, MSATTN_ERR_INVALID_ARG for an invalid geometry. No
+ * reference counterpart: the reference has one path per backend
+ * (miniserve/attention.py:231-235); this library picks among its kernels by shape.
+ */
+int msattn_paged_attention_route(const void* query, const void* out, const void* k_cache,
+                                 const void* v_cache, int64_t cache_block_stride,
+                                 int64_t cache_slot_stride, int64_t cache_head_stride, int batch,
+                                 int q_len, int num_heads, int num_kv_heads, int head_dim,
+                                 int block_size, int max_context, int q_dtype, int kv_dtype,
+                                 size_t workspace_bytes, int* route);
 
 /*
  * msattn_paged_attention for decode (q_len == 1) with rotate-half RoPE applied to

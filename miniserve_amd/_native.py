@@ -23,6 +23,14 @@ DTYPE_CODES = {
 
 OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_HIP = 0, 1, 2, 3, 4
 
+# msattn_route codes: the kernel msattn_paged_attention runs for a call's shape.
+ROUTE_PREFILL, ROUTE_PARTITION_FUSED, ROUTE_PARTITION, ROUTE_STREAMK, ROUTE_GENERIC = 1, 2, 3, 4, 5
+ROUTE_NAMES = {ROUTE_PREFILL: "prefill", ROUTE_PARTITION_FUSED: "partition-fused",
+               ROUTE_PARTITION: "partition", ROUTE_STREAMK: "stream-K",
+               ROUTE_GENERIC: "generic"}
+NOALLOC_SCRATCH_BYTES = 64 << 20
+MAX_HEAD_DIM = 256
+
 c_int, c_i64, c_size, c_vp, c_float = (ctypes.c_int, ctypes.c_int64, ctypes.c_size_t,
                                        ctypes.c_void_p, ctypes.c_float)
 
@@ -40,6 +48,9 @@ SIGNATURES = {
         c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
         c_float, c_int, c_int, c_vp]),
+    "msattn_paged_attention_route": (c_int, [
+        c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_int, c_int, c_int,
+        c_int, c_int, c_int, c_size, ctypes.POINTER(c_int)]),
     "msattn_paged_attention_rope": (c_int, [
         c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_size,
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,

@@ -21,6 +21,8 @@ Differences from the reference, all deliberate:
 from __future__ import annotations
 
 import math
+import threading
+import weakref
 from typing import Sequence
 
 import torch
@@ -28,6 +30,16 @@ import torch
 from . import _native as nat
 
 _BACKENDS = ("sdpa", "triton_flash")
+
+# Per-call host work of the eager path (the reference runner calls forward once per layer
+# with an int64 device table and a Python-list context_lens, model_runner.py:72-83) is kept
+# off the common case: the int32 table of a source tensor is converted once while the
+# tensor is unchanged, list lengths go through pinned memory, and a call without a
+# workspace reuses one zeroed workspace per (device, stream).
+_cache_lock = threading.Lock()
+_table_cache: dict[tuple, tuple] = {}   # (id, device) -> (weakref, version, meta, int32 table)
+_TABLE_CACHE_MAX = 16
+_workspaces: dict[tuple, torch.Tensor] = {}  # (device index, stream handle) -> uint8 tensor
 
 
 def _rotate_half(x: torch.Tensor) -> torch.Tensor:
@@ -58,9 +70,7 @@ def _require_gpu(t: torch.Tensor, what: str) -> None:
             f"msattn needs ROCm GPU tensors: {what} is on {t.device} (there is no CPU path)")
 
 
-def block_table_i32(block_table, device: torch.device) -> torch.Tensor:
-    """Block table as a contiguous int32 [batch, width] tensor on `device`."""
-    table = torch.as_tensor(block_table, device=device)
+def _convert_table(table: torch.Tensor) -> torch.Tensor:
     if table.ndim == 1:
         table = table[None, :]
     if table.ndim != 2:
@@ -68,6 +78,45 @@ def block_table_i32(block_table, device: torch.device) -> torch.Tensor:
     if table.dtype != torch.int32:
         table = table.to(torch.int32)
     return table.contiguous()
+
+
+def block_table_i32(block_table, device: torch.device) -> torch.Tensor:
+    """Block table as a contiguous int32 [batch, width] tensor on `device`.
+
+    A device tensor that needs converting (the reference keeps int64 tables,
+    attention.py:237) is converted once and reused while it is unchanged: same object,
+    same torch version counter (every in-place write through torch bumps it), same shape
+    and strides. Not during graph capture, whose conversions must be captured."""
+    if not isinstance(block_table, torch.Tensor) or block_table.device != device or \
+            (block_table.dtype == torch.int32 and block_table.is_contiguous() and
+             block_table.ndim == 2) or torch.cuda.is_current_stream_capturing():
+        return _convert_table(torch.as_tensor(block_table, device=device))
+    try:
+        version = block_table._version
+    except RuntimeError:  # inference-mode tensors keep no version counter: no reuse
+        return _convert_table(block_table)
+    key = (id(block_table), str(device))
+    meta = (block_table.data_ptr(), tuple(block_table.shape), block_table.stride(),
+            block_table.dtype)
+    with _cache_lock:
+        hit = _table_cache.get(key)
+        if hit is not None and hit[0]() is block_table and hit[1] == version and hit[2] == meta:
+            return hit[3]
+    table = _convert_table(block_table)
+    with _cache_lock:
+        if len(_table_cache) >= _TABLE_CACHE_MAX:
+            _table_cache.clear()
+        _table_cache[key] = (weakref.ref(block_table), version, meta, table)
+    return table
+
+
+def _host_ints_to_device(values: list[int], device: torch.device) -> torch.Tensor:
+    """int32 device copy of host integers through pinned memory (an asynchronous copy;
+    torch's pinned-memory allocator keeps the staging block until the copy has run)."""
+    if device.type != "cuda":
+        return torch.tensor(values, dtype=torch.int32, device=device)
+    staged = torch.tensor(values, dtype=torch.int32, pin_memory=True)
+    return staged.to(device, non_blocking=True)
 
 
 def context_lens_i32(context_lens, device: torch.device, batch: int) -> tuple[torch.Tensor, int | None]:
@@ -79,10 +128,30 @@ def context_lens_i32(context_lens, device: torch.device, batch: int) -> tuple[to
     else:
         values = [int(x) for x in context_lens]
         host_max = max(values) if values else 0
-        lens = torch.tensor(values, dtype=torch.int32, device=device)
+        lens = _host_ints_to_device(values, device)
     if lens.numel() != batch:
         raise ValueError(f"context_lens has {lens.numel()} entries for a batch of {batch}")
     return lens, host_max
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A zeroed workspace of at least `nbytes` for calls on the current stream of `device`.
+
+    One per (device, stream): calls on one stream run one after another, and every call
+    leaves the in-kernel merge's counters at zero, so the next call may reuse it. Under
+    graph capture a fresh one is allocated (from the graph's pool)."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           nat.stream_handle(device))
+    with _cache_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            if ws is None and len(_workspaces) >= 16:  # streams come and go: keep a few
+                _workspaces.clear()
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+    return ws
 
 
 class PagedAttention:
@@ -167,7 +236,7 @@ class PagedAttention:
         if isinstance(start, torch.Tensor):
             starts = start.reshape(-1).to(device=dev, dtype=torch.int32)
         elif isinstance(start, Sequence):
-            starts = torch.tensor([int(s) for s in start], dtype=torch.int32, device=dev)
+            starts = _host_ints_to_device([int(s) for s in start], dev)
         else:
             starts = torch.full((B,), int(start), dtype=torch.int32, device=dev)
         if starts.numel() < B:
@@ -291,6 +360,9 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     nb, bs, KVH, Dk = k_cache.shape
     if Dk != D:
         raise ValueError(f"head_dim mismatch: query {D}, cache {Dk}")
+    if D > nat.MAX_HEAD_DIM or D % 2:
+        raise ValueError(f"head_dim {D}: the kernels take even head sizes up to "
+                         f"{nat.MAX_HEAD_DIM}")
     if H % KVH:
         raise ValueError("num_heads must be a multiple of num_kv_heads")
     if k_cache.stride(3) != 1:
@@ -329,7 +401,7 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
         raise ValueError("unsupported attention geometry")
     if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
         # zeroed: the in-kernel merge's tickets must start at zero (calls leave them so)
-        workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+        workspace = _workspace(dev, ws_bytes)
     if out is None:
         out = torch.empty((B, q_len, H, D), dtype=query.dtype, device=dev)
     args = (q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
@@ -365,6 +437,36 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
                                            cos.shape[0], nat.stream_handle(dev))
     nat.check("msattn_paged_attention_rope", status)
     return out
+
+
+def kernel_route(query: torch.Tensor, k_cache: torch.Tensor, block_table,
+                 max_context: int | None = None, out: torch.Tensor | None = None,
+                 workspace_bytes: int | None = None) -> str:
+    """Name of the kernel ``paged_attention`` runs for this call: "prefill",
+    "partition-fused", "partition", "stream-K" or "generic" (msattn_paged_attention_route).
+
+    The choice depends on shapes, types and alignment, not on context-length values;
+    ``max_context`` defaults to the table capacity, ``workspace_bytes`` to the call's own
+    workspace size (pass ``_native.NOALLOC_SCRATCH_BYTES`` for the no-allocation entry)."""
+    import ctypes
+
+    B, q_len, H, D = query.shape
+    nb, bs, KVH, _ = k_cache.shape
+    width = block_table.shape[-1]
+    cap = width * bs
+    max_context = cap if max_context is None else max(0, min(int(max_context), cap))
+    lib = nat.lib()
+    if workspace_bytes is None:
+        workspace_bytes = lib.msattn_workspace_bytes(B, q_len, H, KVH, D, max_context)
+    q = query if query.is_contiguous() else query.contiguous()
+    out_ptr = out.data_ptr() if out is not None else q.data_ptr()
+    r = ctypes.c_int(0)
+    nat.check("msattn_paged_attention_route", lib.msattn_paged_attention_route(
+        q.data_ptr(), out_ptr, k_cache.data_ptr(), k_cache.data_ptr(), k_cache.stride(0),
+        k_cache.stride(1), k_cache.stride(2), B, q_len, H, KVH, D, bs, max_context,
+        nat.dtype_code(query.dtype), nat.dtype_code(k_cache.dtype), workspace_bytes,
+        ctypes.byref(r)))
+    return nat.ROUTE_NAMES[r.value]
 
 
 def gather_kv(cache: torch.Tensor, block_table, context_lens, max_context: int | None = None

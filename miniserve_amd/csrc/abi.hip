@@ -77,12 +77,17 @@ bool dtype_ok(int d) { return d >= MSATTN_F32 && d <= MSATTN_FP8_E4M3; }
 int dtype_bytes(int d) { return d == MSATTN_F32 ? 4 : (d == MSATTN_FP8_E4M3 ? 1 : 2); }
 bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
 
+// Head sizes: every even size up to kMaxHeadDim (miniserve/attention.py:87-88 accepts any
+// positive even head_dim; the generic kernel spreads a row over at most one wave, and the
+// merge kernel holds rows of up to 256 dims).
+constexpr int kMaxHeadDim = 256;
+
 bool geometry_ok(int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
                  int max_context) {
   if (batch <= 0 || q_len <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return false;
   if (num_heads % num_kv_heads) return false;
   if (max_context < 0) return false;
-  if (head_dim % 4) return false;
+  if (head_dim % 2 || head_dim > kMaxHeadDim) return false;
   const int64_t rows = static_cast<int64_t>(batch) * q_len * num_heads;
   return rows < (int64_t(1) << 31);
 }
@@ -239,26 +244,28 @@ int device_cus() {
 // Generic kernel for every (query, cache) type pair: the cache is read as stored and
 // cast to the query type (miniserve/attention.py:240-241).
 template <typename QT>
-hipError_t dispatch_split_q(const SplitParams& p, int kv_dtype, int D, int RT, hipStream_t s,
-                            bool* sup) {
+hipError_t dispatch_split_q(const SplitParams& p, int kv_dtype, int D, int RT, bool rows16,
+                            hipStream_t s, bool* sup) {
   switch (kv_dtype) {
-    case MSATTN_F32: return launch_split<QT, float>(p, D, RT, s, sup);
-    case MSATTN_F16: return launch_split<QT, _Float16>(p, D, RT, s, sup);
-    case MSATTN_BF16: return launch_split<QT, bf16_t>(p, D, RT, s, sup);
-    case MSATTN_FP8_E4M3: return launch_split<QT, fp8_t>(p, D, RT, s, sup);
+    case MSATTN_F32: return launch_split<QT, float>(p, D, RT, rows16, s, sup);
+    case MSATTN_F16: return launch_split<QT, _Float16>(p, D, RT, rows16, s, sup);
+    case MSATTN_BF16: return launch_split<QT, bf16_t>(p, D, RT, rows16, s, sup);
+    case MSATTN_FP8_E4M3: return launch_split<QT, fp8_t>(p, D, RT, rows16, s, sup);
     default: break;
   }
   *sup = false;
   return hipSuccess;
 }
 
+// rows16: the cache rows start on 16-byte boundaries and span whole 16-byte chunks, so
+// the generic kernel may read them with 16-byte loads (else element by element).
 hipError_t dispatch_split(const SplitParams& p, int q_dtype, int kv_dtype, int D, int RT,
-                          hipStream_t s, bool* sup) {
+                          bool rows16, hipStream_t s, bool* sup) {
   *sup = false;
   switch (q_dtype) {
-    case MSATTN_F32: return dispatch_split_q<float>(p, kv_dtype, D, RT, s, sup);
-    case MSATTN_F16: return dispatch_split_q<_Float16>(p, kv_dtype, D, RT, s, sup);
-    case MSATTN_BF16: return dispatch_split_q<bf16_t>(p, kv_dtype, D, RT, s, sup);
+    case MSATTN_F32: return dispatch_split_q<float>(p, kv_dtype, D, RT, rows16, s, sup);
+    case MSATTN_F16: return dispatch_split_q<_Float16>(p, kv_dtype, D, RT, rows16, s, sup);
+    case MSATTN_BF16: return dispatch_split_q<bf16_t>(p, kv_dtype, D, RT, rows16, s, sup);
     default: break;
   }
   return hipSuccess;
@@ -270,10 +277,10 @@ hipError_t dispatch_split(const SplitParams& p, int q_dtype, int kv_dtype, int D
 // of whole 16-token tiles, a tile span their 32-bit offsets reach, and a query they can
 // read with 16-byte loads.
 bool mfma_route_ok(const void* query, int q_dtype, int kv_dtype, int head_dim, int block_size,
-                   int64_t slot_stride) {
+                   int64_t slot_stride, bool rows16) {
   return (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
          (kv_dtype == q_dtype || kv_dtype == MSATTN_FP8_E4M3 || kv_dtype == MSATTN_F32) &&
-         (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 &&
+         (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 && rows16 &&
          tile_span_ok(slot_stride, head_dim, kv_dtype) && aligned(query, 16);
 }
 
@@ -298,11 +305,11 @@ hipError_t with_mfma_types(int q_dtype, int kv_dtype, F&& f) {
 // fp32 FMAs, or fp32 MFMAs at 16 rows per tile over an fp32 cache. The cascade's prefix
 // pass keeps the generic kernel for an fp32 query.
 bool mfma_decode_route_ok(const void* query, int q_dtype, int kv_dtype, int head_dim,
-                          int block_size, int64_t slot_stride) {
+                          int block_size, int64_t slot_stride, bool rows16) {
   if (q_dtype == MSATTN_F32)
-    return (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 &&
+    return (head_dim == 64 || head_dim == 128) && block_size % 16 == 0 && rows16 &&
            tile_span_ok(slot_stride, head_dim, kv_dtype) && aligned(query, 16);
-  return mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, slot_stride);
+  return mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, slot_stride, rows16);
 }
 template <typename F>
 hipError_t with_mfma_decode_types(int q_dtype, int kv_dtype, F&& f) {
@@ -316,15 +323,25 @@ hipError_t with_mfma_decode_types(int q_dtype, int kv_dtype, F&& f) {
   }
 }
 
+// Caches must be element-aligned with non-negative strides. Rows that start on 16-byte
+// boundaries (pointers and every stride) and span whole 16-byte chunks are read with
+// 16-byte loads (cache_rows16); other layouts (odd head sizes such as 6 or 40 over a
+// 2-byte cache, padded strides) take the generic kernel's element loads.
 int check_cache_args(const void* k_cache, const void* v_cache, int64_t blk, int64_t slot,
                      int64_t head, int kv_dtype, int block_size, int num_blocks, int table_width) {
   if (!k_cache || !v_cache) return MSATTN_ERR_INVALID_ARG;
   if (block_size <= 0 || num_blocks <= 0 || table_width <= 0) return MSATTN_ERR_INVALID_ARG;
   if (blk < 0 || slot < 0 || head < 0) return MSATTN_ERR_INVALID_ARG;
   const int eb = dtype_bytes(kv_dtype);
-  if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return MSATTN_ERR_INVALID_ARG;
-  if ((blk * eb) % 16 || (slot * eb) % 16 || (head * eb) % 16) return MSATTN_ERR_INVALID_ARG;
+  if (!aligned(k_cache, eb) || !aligned(v_cache, eb)) return MSATTN_ERR_INVALID_ARG;
   return MSATTN_OK;
+}
+
+bool cache_rows16(const void* k_cache, const void* v_cache, int64_t blk, int64_t slot,
+                  int64_t head, int head_dim, int kv_dtype) {
+  const int eb = dtype_bytes(kv_dtype);
+  return aligned(k_cache, 16) && aligned(v_cache, 16) && (blk * eb) % 16 == 0 &&
+         (slot * eb) % 16 == 0 && (head * eb) % 16 == 0 && (head_dim * eb) % 16 == 0;
 }
 
 }  // namespace
@@ -369,6 +386,45 @@ struct RopeArgs {
   int max_pos;
 };
 
+// Which partials kernel a call takes (kind as the workspace header records it: 1 stream-K,
+// 2 the partition kernel merging in-kernel, 0 the partition or generic kernel with a merge
+// launch after it), from sizes, types and alignment only, so the choice is capture-safe.
+struct PartialsPlan {
+  bool use_mfma;  // the MFMA decode kernels (else the generic kernel)
+  int RT;         // query rows per tile
+  int kind;
+};
+
+PartialsPlan plan_partials(const void* query, int q_dtype, int kv_dtype, int head_dim,
+                           int block_size, int64_t slot_stride, bool rows16, int batch,
+                           int q_len, int num_heads, int num_kv_heads, int max_context,
+                           bool has_out, int key_lo) {
+  PartialsPlan pl;
+  const int rows = q_len * (num_heads / num_kv_heads);
+  pl.use_mfma = mfma_decode_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, slot_stride,
+                                     rows16);
+  pl.RT = pl.use_mfma ? mfma_rows_per_tile(rows) : rows_per_tile(rows);
+  // Decode with enough work to fill the chip: stream-K over every (sequence, KV head)
+  // tile run, one workgroup per CU. Small decodes keep the partition kernel, whose short
+  // runs start faster.
+  const int64_t tile_capacity =
+      static_cast<int64_t>(batch) * num_kv_heads * ceil_div(max_context, 16);
+  const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
+  const int64_t sk_min_tiles =
+      kv_fp8 && q_dtype != MSATTN_F32 && pl.RT == 8 ? kStreamKMinTilesFp8Rt8 : kStreamKMinTiles;
+  const int64_t triples = static_cast<int64_t>(batch) * num_kv_heads * ceil_div(rows, pl.RT);
+  if (pl.use_mfma && q_len == 1 && batch <= kSkMaxBatch && tile_capacity >= sk_min_tiles)
+    pl.kind = 1;
+  // With an output to write, the MFMA partition kernel merges in-kernel (the last
+  // partition of each (sequence, KV head, row tile) to finish folds the others in), so
+  // no merge launch follows; it needs one header ticket per such triple.
+  else if (pl.use_mfma && has_out && key_lo == 0 && kFusedMerge && triples <= kMaxTickets)
+    pl.kind = 2;
+  else
+    pl.kind = 0;
+  return pl;
+}
+
 int partials_impl(const void* query, const void* k_cache, const void* v_cache,
                   int64_t cache_block_stride, int64_t cache_slot_stride,
                   int64_t cache_head_stride, const int32_t* block_table,
@@ -395,9 +451,14 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   const int rows = q_len * G;
   // MFMA path where mfma_decode_route_ok allows it; everything else takes the generic kernel.
   const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
-  const bool use_mfma = mfma_decode_route_ok(query, q_dtype, kv_dtype, head_dim, block_size,
-                                             cache_slot_stride);
-  const int RT = use_mfma ? mfma_rows_per_tile(rows) : rows_per_tile(rows);
+  const bool rows16 = cache_rows16(k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                                   cache_head_stride, head_dim, kv_dtype);
+  const PartialsPlan plan =
+      plan_partials(query, q_dtype, kv_dtype, head_dim, block_size, cache_slot_stride, rows16,
+                    batch, q_len, num_heads, num_kv_heads, max_context, fused_out != nullptr,
+                    key_lo);
+  const bool use_mfma = plan.use_mfma;
+  const int RT = plan.RT;
   char* ws = static_cast<char*>(workspace);
   SplitParams p;
   p.hdr = reinterpret_cast<int*>(ws);
@@ -439,20 +500,15 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   p.rope_max_pos = rope.max_pos;
   p.out = nullptr;
   p.tickets = nullptr;
+  p.head_dim = head_dim;
+  p.rows16 = rows16 ? 1 : 0;
   const int64_t gx = static_cast<int64_t>(p.max_parts) * num_kv_heads * p.rtiles;
   if (gx >= (int64_t(1) << 31) || batch > 65535) return MSATTN_ERR_UNSUPPORTED;
 
   bool sup = false;
   hipError_t e = hipSuccess;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  // Decode with enough work to fill the chip: stream-K over every (sequence,
-  // KV head) tile run, one workgroup per CU. Small decodes keep the partition
-  // kernel, whose short runs start faster.
-  const int64_t tile_capacity =
-      static_cast<int64_t>(batch) * num_kv_heads * ceil_div(max_context, 16);
-  const int64_t sk_min_tiles =
-      kv_fp8 && q_dtype != MSATTN_F32 && RT == 8 ? kStreamKMinTilesFp8Rt8 : kStreamKMinTiles;
-  if (use_mfma && q_len == 1 && batch <= kSkMaxBatch && tile_capacity >= sk_min_tiles) {
+  if (plan.kind == 1) {  // stream-K
     *kind = 1;
     const int units = num_kv_heads * p.rtiles;
     p.sk_group = largest_pow2_divisor_upto(
@@ -466,11 +522,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
     return hip_status(e);
   }
   *kind = 0;  // the partition kernels below
-  // With an output to write, the MFMA partition kernel merges in-kernel (the last
-  // partition of each (sequence, KV head, row tile) to finish folds the others in), so
-  // no merge launch follows; it needs one header ticket per such triple.
-  if (use_mfma && fused_out != nullptr && key_lo == 0 && kFusedMerge &&
-      static_cast<int64_t>(batch) * num_kv_heads * p.rtiles <= kMaxTickets) {
+  if (plan.kind == 2) {  // the partition kernel merging in-kernel
     *kind = 2;
     p.out = fused_out;
     p.tickets = p.hdr + kHdrTickets;
@@ -526,7 +578,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
       return launch_decode_mfma<decltype(t), decltype(kt)>(p, head_dim, RT, st, &sup);
     });
   } else {
-    e = dispatch_split(p, q_dtype, kv_dtype, head_dim, RT, st, &sup);
+    e = dispatch_split(p, q_dtype, kv_dtype, head_dim, RT, rows16, st, &sup);
   }
   if (!sup) return MSATTN_ERR_UNSUPPORTED;
   return hip_status(e);
@@ -582,9 +634,11 @@ int merge_impl(const void* workspace, size_t workspace_bytes, const int32_t* con
   p.G = num_heads / num_kv_heads;
   p.D = head_dim;
   p.max_parts = L.max_parts;
+  p.slots = L.slots;
   p.pml = pml;
   p.pacc = pacc;
   p.npp = npp;
+  p.pslots = npp > 0 ? L.rows * npp : 0;
   p.kind_hint = kind_hint;
   bool sup = false;
   const hipError_t e = launch_merge(p, q_dtype, static_cast<hipStream_t>(stream), &sup);
@@ -629,22 +683,64 @@ constexpr int64_t kPrefillMinRows = MSATTN_PREFILL_MIN_ROWS;
 #define MSATTN_PREFILL_SPLIT_PCT 100
 #endif
 constexpr int64_t kPrefillSplitPct = MSATTN_PREFILL_SPLIT_PCT;
+// The rule above holds over the measured shapes, at most 64 query rows per KV head (4
+// tiles); longer chunks stay on the prefill kernel, since every 16-row tile of the
+// partition kernel streams the whole context again.
+#ifndef MSATTN_PREFILL_SPLIT_MAX_ROWS
+#define MSATTN_PREFILL_SPLIT_MAX_ROWS 64
+#endif
+constexpr int64_t kPrefillSplitMaxRows = MSATTN_PREFILL_SPLIT_MAX_ROWS;
 
-bool direct_prefill_route(const void* query, const void* out, int64_t cache_slot_stride,
-                          int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
-                          int block_size, int q_dtype, int kv_dtype) {
+// Whether the chunked-prefill kernel can run this call: a multi-token bf16/fp16 query
+// with more than kPrefillMinRows rows per KV head on the MFMA route's types and layouts.
+bool prefill_kernel_ok(const void* query, const void* out, int64_t cache_slot_stride,
+                       bool rows16, int batch, int q_len, int num_heads, int num_kv_heads,
+                       int head_dim, int block_size, int q_dtype, int kv_dtype) {
   if (!(q_len > 1 &&
-        mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, cache_slot_stride) &&
+        mfma_route_ok(query, q_dtype, kv_dtype, head_dim, block_size, cache_slot_stride,
+                      rows16) &&
         aligned(out, 8) && batch <= 65535 && num_heads > 0 && num_kv_heads > 0 &&
         num_heads % num_kv_heads == 0))
     return false;
   const int64_t rows = static_cast<int64_t>(q_len) * (num_heads / num_kv_heads);
-  if (rows <= kPrefillMinRows) return false;
+  return rows > kPrefillMinRows;
+}
+
+// Whether the cost model prefers the prefill kernel to the partition kernel (for a call
+// both can run).
+bool prefill_preferred(int batch, int q_len, int num_heads, int num_kv_heads) {
+  const int64_t rows = static_cast<int64_t>(q_len) * (num_heads / num_kv_heads);
+  if (rows > kPrefillSplitMaxRows) return true;
   const int64_t pairs = static_cast<int64_t>(batch) * num_kv_heads;
   const int64_t tasks = pairs * ((rows + kPfRows - 1) / kPfRows);
   const int64_t cus = device_cus();
   const int64_t rounds = (tasks + cus - 1) / cus;
   return 100 * ((rows + 15) / 16) * pairs > kPrefillSplitPct * cus * rounds;
+}
+
+// The route of msattn_paged_attention (and of the no-allocation entry point, whose
+// workspace is its scratch): the prefill kernel when it can run and the cost model
+// prefers it, or when the partition layout does not fit the workspace (the prefill
+// kernel uses none); else the partials kernel plan_partials names.
+int choose_route(const void* query, const void* out, const void* k_cache, const void* v_cache,
+                 int64_t cache_block_stride, int64_t cache_slot_stride, int64_t cache_head_stride,
+                 int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                 int block_size, int max_context, int q_dtype, int kv_dtype,
+                 size_t workspace_bytes) {
+  const bool rows16 = cache_rows16(k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                                   cache_head_stride, head_dim, kv_dtype);
+  const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
+  const bool fits = workspace_bytes >= L.total();
+  if (prefill_kernel_ok(query, out, cache_slot_stride, rows16, batch, q_len, num_heads,
+                        num_kv_heads, head_dim, block_size, q_dtype, kv_dtype) &&
+      (!fits || prefill_preferred(batch, q_len, num_heads, num_kv_heads)))
+    return MSATTN_ROUTE_PREFILL;
+  const PartialsPlan pl =
+      plan_partials(query, q_dtype, kv_dtype, head_dim, block_size, cache_slot_stride, rows16,
+                    batch, q_len, num_heads, num_kv_heads, max_context, true, 0);
+  if (pl.kind == 1) return MSATTN_ROUTE_STREAMK;
+  if (pl.kind == 2) return MSATTN_ROUTE_PARTITION_FUSED;
+  return pl.use_mfma ? MSATTN_ROUTE_PARTITION : MSATTN_ROUTE_GENERIC;
 }
 
 // msattn_paged_attention's body. `prefill_needs_ws`: whether the direct prefill route
@@ -660,11 +756,12 @@ int attention_impl(const void* query, const void* k_cache, const void* v_cache,
                    int q_dtype, int kv_dtype, bool prefill_needs_ws, void* stream) {
   if (!out) return MSATTN_ERR_INVALID_ARG;
   if (!dtype_ok(q_dtype) || !aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
-  if (direct_prefill_route(query, out, cache_slot_stride, batch, q_len, num_heads, num_kv_heads,
-                           head_dim, block_size, q_dtype, kv_dtype)) {
+  if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
+    return MSATTN_ERR_INVALID_ARG;
+  if (choose_route(query, out, k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                   cache_head_stride, batch, q_len, num_heads, num_kv_heads, head_dim, block_size,
+                   max_context, q_dtype, kv_dtype, workspace_bytes) == MSATTN_ROUTE_PREFILL) {
     if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
-    if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
-      return MSATTN_ERR_INVALID_ARG;
     if (!std::isfinite(scale)) return MSATTN_ERR_INVALID_ARG;
     const int rc = check_cache_args(k_cache, v_cache, cache_block_stride, cache_slot_stride,
                                     cache_head_stride, kv_dtype, block_size, num_blocks,
@@ -779,10 +876,11 @@ int msattn_paged_attention_noalloc(const void* query, const void* k_cache, const
   if (!out || !dtype_ok(q_dtype) || q_dtype == MSATTN_FP8_E4M3) return MSATTN_ERR_INVALID_ARG;
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
     return MSATTN_ERR_INVALID_ARG;
-  const bool direct = direct_prefill_route(query, out, cache_slot_stride, batch, q_len,
-                                           num_heads, num_kv_heads, head_dim, block_size,
-                                           q_dtype, kv_dtype);
-  if (!direct) {
+  // A partition layout that does not fit the scratch sends a chunked prefill the prefill
+  // kernel can run there (it uses no scratch); any other call past the scratch is refused.
+  if (choose_route(query, out, k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                   cache_head_stride, batch, q_len, num_heads, num_kv_heads, head_dim, block_size,
+                   max_context, q_dtype, kv_dtype, kScratchBytes) != MSATTN_ROUTE_PREFILL) {
     const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
     if (L.total() > kScratchBytes) return MSATTN_ERR_WORKSPACE;
   }
@@ -794,6 +892,31 @@ int msattn_paged_attention_noalloc(const void* query, const void* k_cache, const
                         batch, q_len, num_heads, num_kv_heads, head_dim, block_size, num_blocks,
                         table_width, max_context, causal, window, scale, q_dtype, kv_dtype,
                         false, stream);
+}
+
+int msattn_paged_attention_route(const void* query, const void* out, const void* k_cache,
+                                 const void* v_cache, int64_t cache_block_stride,
+                                 int64_t cache_slot_stride, int64_t cache_head_stride, int batch,
+                                 int q_len, int num_heads, int num_kv_heads, int head_dim,
+                                 int block_size, int max_context, int q_dtype, int kv_dtype,
+                                 size_t workspace_bytes, int* route) {
+  if (!route) return MSATTN_ERR_INVALID_ARG;
+  *route = 0;
+  if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
+    return MSATTN_ERR_INVALID_ARG;
+  if (!dtype_ok(q_dtype) || q_dtype == MSATTN_FP8_E4M3 || !dtype_ok(kv_dtype))
+    return MSATTN_ERR_INVALID_ARG;
+  if (block_size <= 0 || cache_block_stride < 0 || cache_slot_stride < 0 || cache_head_stride < 0)
+    return MSATTN_ERR_INVALID_ARG;
+  const int r = choose_route(query, out, k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                             cache_head_stride, batch, q_len, num_heads, num_kv_heads, head_dim,
+                             block_size, max_context, q_dtype, kv_dtype, workspace_bytes);
+  if (r != MSATTN_ROUTE_PREFILL &&
+      workspace_bytes < workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim,
+                                         max_context).total())
+    return MSATTN_ERR_WORKSPACE;
+  *route = r;
+  return MSATTN_OK;
 }
 
 int msattn_paged_attention_rope(const void* query, const void* k_cache, const void* v_cache,
@@ -860,8 +983,10 @@ int msattn_paged_attention_prefix(const void* query, const void* k_cache, const 
   if (workspace_bytes < X.total) return MSATTN_ERR_WORKSPACE;
   // The shared-prefix pass runs the MFMA prefill kernel; other types and head sizes,
   // and calls without a shared prefix, attend in one pass over the whole context.
+  const bool rows16 = cache_rows16(k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                                   cache_head_stride, head_dim, kv_dtype);
   const bool cascade = X.prefix > 0 && mfma_route_ok(query, q_dtype, kv_dtype, head_dim,
-                                                     block_size, cache_slot_stride);
+                                                     block_size, cache_slot_stride, rows16);
   if (!cascade)
     return msattn_paged_attention(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
                                   cache_head_stride, block_table, context_lens, out, workspace,

@@ -2,6 +2,7 @@
 #pragma once
 
 #include "common.h"
+#include "merge_slots.h"
 #include "split_kernel.h"
 
 namespace msattn {
@@ -14,11 +15,13 @@ struct MergeParams {
   int64_t rows;       // batch * q_len * H
   int batch, H, KVH, G, D;
   int max_parts;      // slots per row of the partition layout
+  int64_t slots;      // (m, l) / acc slots the workspace holds: no slot at or past it is read
   // Shared-prefix partials folded in as well (npp per row at slots row * npp ..; npp = 0:
   // none), as the prefix pass of a cascade decode writes them.
   const float* pml;
   const float* pacc;
   int npp;
+  int64_t pslots;     // slots of the shared-prefix source (rows * npp)
   int kind_hint;      // layout the caller knows the partials kernel used (0: partition
                       // slots), or -1: read it from the header
 };

@@ -61,6 +61,53 @@ __global__ __launch_bounds__(kOpsThreads) void write_kv_copy_kernel(const WriteK
   }
 }
 
+// Vector form of both scatters: one thread per E consecutive elements of a row (E * the
+// source element = 16 bytes, or 4 fp32 elements), loaded with one load and stored with one
+// store (E elements of the cache type), the table looked up once per thread. Used when
+// head_dim is a multiple of E and the cache pointer and strides sit on the store's
+// alignment; the same conversions as the element kernels (same-type: the bits copied).
+template <int N>
+struct alignas(N) RawN {
+  unsigned char b[N];
+};
+
+template <typename ST, typename DT, int E>
+__global__ __launch_bounds__(kOpsThreads) void write_kv_vec_kernel(const WriteKVParams p) {
+  const int CPR = p.D / E;  // chunks per row
+  const int64_t total = static_cast<int64_t>(p.batch) * p.tokens * p.KVH * CPR;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kOpsThreads + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * kOpsThreads) {
+    const int c = static_cast<int>(idx % CPR);
+    int64_t rest = idx / CPR;
+    const int h = static_cast<int>(rest % p.KVH);
+    rest /= p.KVH;
+    const int t = static_cast<int>(rest % p.tokens);
+    const int b = static_cast<int>(rest / p.tokens);
+    const int64_t off = token_offset(p.table, b, p.starts[b] + t, p.bs, p.W, p.num_blocks,
+                                     p.blk_stride, p.slot_stride);
+    if (off < 0) continue;
+    const int64_t src = idx * E;  // [b, t, h, c * E] of the contiguous source
+    const int64_t dst = off + static_cast<int64_t>(h) * p.head_stride + static_cast<int64_t>(c) * E;
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+      const ST* sp = static_cast<const ST*>(which ? p.v : p.k) + src;
+      DT* dp = static_cast<DT*>(which ? p.v_cache : p.k_cache) + dst;
+      if constexpr (std::is_same<ST, DT>::value) {
+        *reinterpret_cast<RawN<E * sizeof(ST)>*>(dp) =
+            *reinterpret_cast<const RawN<E * sizeof(ST)>*>(sp);
+      } else {
+        const RawN<E * sizeof(ST)> in = *reinterpret_cast<const RawN<E * sizeof(ST)>*>(sp);
+        RawN<E * sizeof(DT)> o;
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          Elt<DT>::store(reinterpret_cast<DT*>(o.b) + e,
+                         Elt<ST>::load(reinterpret_cast<const ST*>(in.b) + e));
+        *reinterpret_cast<RawN<E * sizeof(DT)>*>(dp) = o;
+      }
+    }
+  }
+}
+
 static unsigned grid_for(int64_t total) {
   int64_t blocks = (total + kOpsThreads - 1) / kOpsThreads;
   if (blocks > 65536) blocks = 65536;
@@ -68,8 +115,27 @@ static unsigned grid_for(int64_t total) {
   return static_cast<unsigned>(blocks);
 }
 
+// Whether the vector form with E elements per thread applies: head_dim a multiple of E,
+// the source (contiguous) on E source elements' alignment, the caches and their strides
+// on E cache elements' alignment.
+template <typename ST, typename DT, int E>
+static bool wkv_vec_ok(const WriteKVParams& p) {
+  const uintptr_t sa = E * sizeof(ST), da = E * sizeof(DT);
+  auto al = [](const void* q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q) % a == 0; };
+  return p.D % E == 0 && al(p.k, sa) && al(p.v, sa) && al(p.k_cache, da) && al(p.v_cache, da) &&
+         (p.blk_stride * sizeof(DT)) % da == 0 && (p.slot_stride * sizeof(DT)) % da == 0 &&
+         (p.head_stride * sizeof(DT)) % da == 0;
+}
+
 template <typename ST, typename DT>
 static hipError_t launch_wkv(const WriteKVParams& p, hipStream_t stream) {
+  constexpr int E = sizeof(ST) >= 4 || sizeof(DT) >= 4 ? 4 : 8;
+  if (wkv_vec_ok<ST, DT, E>(p)) {
+    const int64_t total = static_cast<int64_t>(p.batch) * p.tokens * p.KVH * (p.D / E);
+    hipLaunchKernelGGL((write_kv_vec_kernel<ST, DT, E>), dim3(grid_for(total)), dim3(kOpsThreads),
+                       0, stream, p);
+    return hipGetLastError();
+  }
   const int64_t total = static_cast<int64_t>(p.batch) * p.tokens * p.KVH * p.D;
   hipLaunchKernelGGL((write_kv_kernel<ST, DT>), dim3(grid_for(total)), dim3(kOpsThreads), 0,
                      stream, p);
@@ -78,6 +144,13 @@ static hipError_t launch_wkv(const WriteKVParams& p, hipStream_t stream) {
 
 template <typename T>
 static hipError_t launch_wkv_copy(const WriteKVParams& p, hipStream_t stream) {
+  constexpr int E = 16 / sizeof(T);
+  if (wkv_vec_ok<T, T, E>(p)) {
+    const int64_t total = static_cast<int64_t>(p.batch) * p.tokens * p.KVH * (p.D / E);
+    hipLaunchKernelGGL((write_kv_vec_kernel<T, T, E>), dim3(grid_for(total)), dim3(kOpsThreads),
+                       0, stream, p);
+    return hipGetLastError();
+  }
   const int64_t total = static_cast<int64_t>(p.batch) * p.tokens * p.KVH * p.D;
   hipLaunchKernelGGL(write_kv_copy_kernel<T>, dim3(grid_for(total)), dim3(kOpsThreads), 0, stream,
                      p);

@@ -8,6 +8,8 @@
 //     (rtile = (h % G) / RT), unit group ug = u / UG; its segment ug * B + b spans
 //     positions [ug * sumT + P_b, ... + T_b) of the chunked work list, and the chunk r
 //     holding a piece of it stored that piece at id r + ug * B + b.
+// The slot arithmetic is merge_slot_range (merge_slots.h), which reads only slots the
+// workspace holds whatever its header says.
 // With running max M and weights w_j = 2^(m_j - M):
 //   out = sum_j w_j acc_j / sum_j w_j l_j
 // which is the merge of kernels/paged_attn_triton.py:_merge_kernel (:250-284) and
@@ -46,10 +48,12 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
 
   // Header and this row's prefix entries are read up front, in one round trip (skipped
   // when the caller knows the partition layout was used: its slots need no header).
+  // merge_slot_range checks every word it uses and keeps the slots it names inside the
+  // workspace, whatever the header holds.
   const bool known0 = p.kind_hint == 0;
   int hv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  const int b = static_cast<int>(row / p.H);  // the sequence when q_len == 1
-  const int bh = b < p.batch ? b : p.batch - 1;  // header holds batch + 1 prefixes
+  const int64_t bq = row / p.H;  // the sequence when q_len == 1
+  const int bh = bq < p.batch ? static_cast<int>(bq) : p.batch - 1;  // batch + 1 prefixes
   int pb = 0, pe = 0;
   if (!known0) {
 #pragma unroll
@@ -57,34 +61,9 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
     pb = p.hdr[kHdrPrefix + bh];
     pe = p.hdr[kHdrPrefix + bh + 1];
   }
-
-  // Partial j of this row sits at slot base + j * stride; n bounds the count.
-  int64_t base = 0, stride = 1;
-  int64_t n = 0;
-  const bool markers = known0 || hv[kHdrKind] == 0;
-  if (markers) {
-    base = row * p.max_parts;
-    n = p.max_parts;
-  } else {
-    const int B = hv[kHdrB];
-    const int sumT = hv[kHdrSumT];
-    const int c = hv[kHdrChunk];
-    const int UG = hv[kHdrUG];
-    const int RT = hv[kHdrRT];
-    const int h = static_cast<int>(row - static_cast<int64_t>(b) * p.H);
-    const int kvh = h / p.G;
-    const int gi = h - kvh * p.G;
-    const int unit = (gi / RT) * p.KVH + kvh;
-    const int ug = unit / UG;
-    const int ul = unit - ug * UG;
-    if (pe > pb) {
-      const int64_t seg_start = static_cast<int64_t>(ug) * sumT + pb;
-      const int64_t r0 = seg_start / c;
-      n = (seg_start + (pe - pb) - 1) / c - r0 + 1;
-      base = ((r0 + static_cast<int64_t>(ug) * B + b) * UG + ul) * RT + gi % RT;
-      stride = static_cast<int64_t>(UG) * RT;
-    }
-  }
+  // Partial j of this row sits at slot base + j * stride, j < n.
+  const SlotRange sr = merge_slot_range(hv, pb, pe, row, p.batch, p.H, p.KVH, p.G, p.max_parts,
+                                        p.slots, p.kind_hint);
 
   float acc[kMergeMaxDims];
 #pragma unroll
@@ -162,10 +141,13 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(const MergeParams 
       if (end) break;
     }
   };
-  fold_source(std::integral_constant<int, kMergeBatch>{}, p.ml, p.acc, base, stride, n, markers);
-  if (p.npp > 0)
-    fold_source(std::integral_constant<int, kMergePrefixBatch>{}, p.pml, p.pacc, row * p.npp, 1,
-                p.npp, false);
+  fold_source(std::integral_constant<int, kMergeBatch>{}, p.ml, p.acc, sr.base, sr.stride, sr.n,
+              sr.markers);
+  if (p.npp > 0) {
+    const SlotRange pr = clamp_slots(SlotRange{row * p.npp, 1, p.npp, false}, p.pslots);
+    fold_source(std::integral_constant<int, kMergePrefixBatch>{}, p.pml, p.pacc, pr.base, 1,
+                pr.n, false);
+  }
 
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   QT* out = static_cast<QT*>(p.out) + row * D;

@@ -101,7 +101,33 @@ struct SplitParams {
   int* tickets;
   int mfma_waves;  // partition MFMA kernel: waves per workgroup (4, or 8 for long partitions)
   int mfma_deep;   // partition MFMA kernel, regular shape at head_dim 64: the deeper residency
+  int head_dim;    // the row's head size (the generic kernel's element mode compiles a larger
+                   // capacity and masks the dims past it)
+  int rows16;      // cache rows start on 16-byte boundaries and hold whole 16-byte chunks
 };
+
+// One 16-byte chunk of a K/V row as the generic kernel's lanes read it. Whole chunks of
+// rows on 16-byte boundaries load as one 16-byte load; otherwise the `valid` leading
+// elements (the row's last, partial chunk, or rows on 2- or 4-byte boundaries) load one
+// by one and the rest of the chunk reads as zeros.
+template <typename KT>
+__device__ __forceinline__ uint4 load_kv_chunk(const KT* src, int valid, bool vec16) {
+  constexpr int EB = Elt<KT>::kBytes;
+  constexpr int N = 16 / EB;
+  if (vec16 && valid >= N) return *reinterpret_cast<const uint4*>(src);
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    if (e < valid) {
+      uint32_t bits;
+      if constexpr (EB == 4) bits = reinterpret_cast<const uint32_t*>(src)[e];
+      else if constexpr (EB == 2) bits = reinterpret_cast<const uint16_t*>(src)[e];
+      else bits = reinterpret_cast<const uint8_t*>(src)[e];
+      w[(e * EB) / 4] |= bits << (8 * ((e * EB) % 4));
+    }
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
 
 // Position of row b's query for RoPE, clamped into the tables.
 __device__ __forceinline__ int rope_position(const SplitParams& p, int b) {
@@ -120,12 +146,17 @@ __device__ __forceinline__ float rope_mix(float q, float r, float c, float s) {
   return a + b;
 }
 
-template <typename QT, typename KT, int D, int RT>
+// ELEM = false: head_dim == D, rows read with 16-byte loads. ELEM = true: D is a capacity
+// (16, 32, 64, 128 or 256) and the row's head_dim (p.head_dim <= D) any even size; rows
+// load chunk by chunk through load_kv_chunk, dims past head_dim read as zeros and are
+// not written.
+template <typename QT, typename KT, int D, int RT, bool ELEM>
 __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams p) {
   using CK = Chunk<KT>;
   constexpr int EPL = CK::kElems;                      // KV elements per 16 B
   static_assert((D * Elt<KT>::kBytes) % 16 == 0, "row must be whole 16-byte chunks");
-  constexpr int CHUNKS = D * Elt<KT>::kBytes / 16;     // 16-byte chunks per row
+  constexpr int CHUNKS = D * Elt<KT>::kBytes / 16;     // 16-byte chunks per row (capacity)
+  const int HD = ELEM ? p.head_dim : D;                // the row's head size
   constexpr int LPR = next_pow2(CHUNKS);               // lanes per K/V row
   static_assert(LPR <= kWave, "row wider than a wave");
   constexpr int TPI = kWave / LPR;                     // tokens per wave instruction
@@ -233,7 +264,10 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
   // Query rows for this lane's chunk of dims, pre-scaled by scale*log2(e).
   const int c = lane % LPR;
   const int tg = lane / LPR;
-  const bool c_ok = c < CHUNKS;
+  // Lanes past the row's last (possibly partial) chunk hold no dims.
+  const bool c_ok = ELEM ? c * EPL < HD : c < CHUNKS;
+  const int c_valid = HD - c * EPL;  // elements of this lane's chunk inside the row
+  const bool vec16 = !ELEM || p.rows16 != 0;
   float qreg[RT][EPL];
   {
     const QT* qp = static_cast<const QT*>(p.q);
@@ -242,17 +276,19 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
 #pragma unroll
       for (int e = 0; e < EPL; ++e) qreg[r][e] = 0.0f;
       if (r < nrows && c_ok) {
-        const QT* src = qp + orow[r] * D + c * EPL;
+        const QT* src = qp + orow[r] * HD + c * EPL;
         float qv[EPL];
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) qv[e] = Elt<QT>::load(src + e);
+        for (int e = 0; e < EPL; ++e) qv[e] = (!ELEM || e < c_valid) ? Elt<QT>::load(src + e) : 0.0f;
         if (p.rope_cos != nullptr) {  // rotate-half RoPE, rounded back to QT
-          const int64_t po = static_cast<int64_t>(rope_position(p, b)) * D;
+          const int64_t po = static_cast<int64_t>(rope_position(p, b)) * HD;
 #pragma unroll
           for (int e = 0; e < EPL; ++e) {
             const int d = c * EPL + e;
-            const bool lo_half = d < D / 2;
-            const float partner = Elt<QT>::load(qp + orow[r] * D + (lo_half ? d + D / 2 : d - D / 2));
+            if (ELEM && d >= HD) continue;
+            const bool lo_half = d < HD / 2;
+            const float partner =
+                Elt<QT>::load(qp + orow[r] * HD + (lo_half ? d + HD / 2 : d - HD / 2));
             qv[e] = round_to<QT>(rope_mix(qv[e], lo_half ? -partner : partner, p.rope_cos[po + d],
                                           p.rope_sin[po + d]));
           }
@@ -279,7 +315,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
       const int64_t off = (s < nslots && t < n_tok) ? s_off[t] : -1;
       offs[u] = off;
       raw[u] = make_uint4(0u, 0u, 0u, 0u);
-      if (off >= 0 && c_ok) raw[u] = *reinterpret_cast<const uint4*>(kbase + off + c * EPL);
+      if (off >= 0 && c_ok) raw[u] = load_kv_chunk(kbase + off + c * EPL, c_valid, vec16);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -344,7 +380,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
       const int64_t off = (s < nslots && t < n_tok) ? s_off[t] : -1;
       tt[u] = off >= 0 ? t : -1;
       raw[u] = make_uint4(0u, 0u, 0u, 0u);
-      if (off >= 0 && c_ok) raw[u] = *reinterpret_cast<const uint4*>(vbase + off + c * EPL);
+      if (off >= 0 && c_ok) raw[u] = load_kv_chunk(vbase + off + c * EPL, c_valid, vec16);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -378,9 +414,9 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
   }
   __syncthreads();
 
-  for (int idx = tid; idx < nrows * D; idx += kSplitThreads) {
-    const int r = idx / D;
-    const int d = idx - r * D;
+  for (int idx = tid; idx < nrows * HD; idx += kSplitThreads) {
+    const int r = idx / HD;
+    const int d = idx - r * HD;
     float a = 0.0f;
 #pragma unroll
     for (int ww = 0; ww < kSplitWaves; ++ww) a += s_sc[(ww * RT + r) * D + d];
@@ -388,7 +424,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
 #pragma unroll
     for (int rr = 0; rr < RT; ++rr)
       if (rr == r) orr = orow[rr];
-    p.acc[(orr * p.max_parts + part) * D + d] = a;
+    p.acc[(orr * p.max_parts + part) * HD + d] = a;
   }
 #pragma unroll
   for (int r = 0; r < RT; ++r) {
@@ -406,27 +442,28 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const SplitParams 
 
 // Host-side launch for one dtype pair; defined in split_<pair>.hip.
 template <typename QT, typename KT>
-hipError_t launch_split(const SplitParams& p, int D, int RT, hipStream_t stream, bool* supported);
+hipError_t launch_split(const SplitParams& p, int D, int RT, bool rows16, hipStream_t stream,
+                        bool* supported);
 
-template <typename QT, typename KT, int D, int RT>
+template <typename QT, typename KT, int D, int RT, bool ELEM>
 hipError_t launch_split_one(const SplitParams& p, hipStream_t stream) {
   const unsigned gx = static_cast<unsigned>(p.max_parts) * static_cast<unsigned>(p.KVH) *
                       static_cast<unsigned>(p.rtiles);
   dim3 grid(gx, 1, static_cast<unsigned>(p.batch));
-  hipLaunchKernelGGL((split_kernel<QT, KT, D, RT>), grid, dim3(kSplitThreads), 0, stream, p);
+  hipLaunchKernelGGL((split_kernel<QT, KT, D, RT, ELEM>), grid, dim3(kSplitThreads), 0, stream, p);
   return hipGetLastError();
 }
 
-// One head size: row tiles of 1, 2, 4 or 8 query rows; head sizes whose K/V row is not
-// whole 16-byte chunks of the cache type are not compiled.
-template <typename QT, typename KT, int D>
+// One head size (or, ELEM, capacity): row tiles of 1, 2, 4 or 8 query rows; head sizes
+// whose K/V row is not whole 16-byte chunks of the cache type are not compiled.
+template <typename QT, typename KT, int D, bool ELEM>
 hipError_t launch_split_d(const SplitParams& p, int RT, hipStream_t stream, bool* supported) {
   if constexpr ((D * Elt<KT>::kBytes) % 16 == 0) {
     switch (RT) {
-      case 1: return launch_split_one<QT, KT, D, 1>(p, stream);
-      case 2: return launch_split_one<QT, KT, D, 2>(p, stream);
-      case 4: return launch_split_one<QT, KT, D, 4>(p, stream);
-      case 8: return launch_split_one<QT, KT, D, 8>(p, stream);
+      case 1: return launch_split_one<QT, KT, D, 1, ELEM>(p, stream);
+      case 2: return launch_split_one<QT, KT, D, 2, ELEM>(p, stream);
+      case 4: return launch_split_one<QT, KT, D, 4, ELEM>(p, stream);
+      case 8: return launch_split_one<QT, KT, D, 8, ELEM>(p, stream);
       default: break;
     }
   }
@@ -435,30 +472,39 @@ hipError_t launch_split_d(const SplitParams& p, int RT, hipStream_t stream, bool
 }
 
 // Explicit specializations, one per compiled dtype pair (split_<pair>.hip): head dims
-// 16, 24, 32, 64, 96, 128 and 256 (24 only where a row is whole 16-byte chunks).
+// 16, 24, 32, 64, 96, 128 and 256 with 16-byte rows (24 only where a row is whole 16-byte
+// chunks); any other even head_dim up to 256, or rows off 16-byte boundaries, on the
+// element mode at the next capacity of 16, 32, 64, 128 or 256.
 #define MSATTN_SPLIT_LAUNCHER(QT, KT)                                                      \
   template <>                                                                              \
-  hipError_t launch_split<QT, KT>(const SplitParams& p, int D, int RT, hipStream_t stream, \
-                                  bool* supported) {                                       \
+  hipError_t launch_split<QT, KT>(const SplitParams& p, int D, int RT, bool rows16,        \
+                                  hipStream_t stream, bool* supported) {                   \
     *supported = true;                                                                     \
-    switch (D) {                                                                           \
-      case 16: return launch_split_d<QT, KT, 16>(p, RT, stream, supported);                \
-      case 24: return launch_split_d<QT, KT, 24>(p, RT, stream, supported);                \
-      case 32: return launch_split_d<QT, KT, 32>(p, RT, stream, supported);                \
-      case 64: return launch_split_d<QT, KT, 64>(p, RT, stream, supported);                \
-      case 96: return launch_split_d<QT, KT, 96>(p, RT, stream, supported);                \
-      case 128: return launch_split_d<QT, KT, 128>(p, RT, stream, supported);              \
-      case 256: return launch_split_d<QT, KT, 256>(p, RT, stream, supported);              \
-      default: break;                                                                      \
+    if (rows16 && (D * Elt<KT>::kBytes) % 16 == 0) {                                       \
+      switch (D) {                                                                         \
+        case 16: return launch_split_d<QT, KT, 16, false>(p, RT, stream, supported);       \
+        case 24: return launch_split_d<QT, KT, 24, false>(p, RT, stream, supported);       \
+        case 32: return launch_split_d<QT, KT, 32, false>(p, RT, stream, supported);       \
+        case 64: return launch_split_d<QT, KT, 64, false>(p, RT, stream, supported);       \
+        case 96: return launch_split_d<QT, KT, 96, false>(p, RT, stream, supported);       \
+        case 128: return launch_split_d<QT, KT, 128, false>(p, RT, stream, supported);     \
+        case 256: return launch_split_d<QT, KT, 256, false>(p, RT, stream, supported);     \
+        default: break;                                                                    \
+      }                                                                                    \
     }                                                                                      \
+    if (D <= 16) return launch_split_d<QT, KT, 16, true>(p, RT, stream, supported);        \
+    if (D <= 32) return launch_split_d<QT, KT, 32, true>(p, RT, stream, supported);        \
+    if (D <= 64) return launch_split_d<QT, KT, 64, true>(p, RT, stream, supported);        \
+    if (D <= 128) return launch_split_d<QT, KT, 128, true>(p, RT, stream, supported);      \
+    if (D <= 256) return launch_split_d<QT, KT, 256, true>(p, RT, stream, supported);      \
     *supported = false;                                                                    \
     return hipSuccess;                                                                     \
   }
 
 #define MSATTN_DECLARE_SPLIT(QT, KT)                                                   \
   template <>                                                                          \
-  hipError_t launch_split<QT, KT>(const SplitParams& p, int D, int RT, hipStream_t stream, \
-                                  bool* supported);
+  hipError_t launch_split<QT, KT>(const SplitParams& p, int D, int RT, bool rows16,    \
+                                  hipStream_t stream, bool* supported);
 MSATTN_DECLARE_SPLIT(float, float)
 MSATTN_DECLARE_SPLIT(float, _Float16)
 MSATTN_DECLARE_SPLIT(float, bf16_t)

@@ -69,18 +69,30 @@ def test_partition_policy(B, q_len, H, KVH, D, ctx, part):
 def test_workspace_rejects_bad_geometry():
     lib = nat.lib()
     assert lib.msattn_workspace_bytes(1, 1, 6, 4, 64, 16) == 0     # H % KVH != 0
-    assert lib.msattn_workspace_bytes(1, 1, 4, 4, 66, 16) == 0     # head_dim % 4 != 0
+    assert lib.msattn_workspace_bytes(1, 1, 4, 4, 65, 16) == 0     # odd head_dim
+    assert lib.msattn_workspace_bytes(1, 1, 4, 4, 258, 16) == 0    # head_dim past 256
     assert lib.msattn_partition_tokens(0, 1, 4, 4, 64, 16) == -1
+
+
+@pytest.mark.parametrize("D", [2, 6, 40, 66, 80, 112, 200, 256])
+def test_every_even_head_dim_up_to_256_is_a_valid_geometry(D):
+    """miniserve/attention.py:87-88 accepts any positive even head_dim; the library takes
+    every even size up to 256 (the generic kernel's element mode for sizes it does not
+    compile exactly)."""
+    lib = nat.lib()
+    assert lib.msattn_workspace_bytes(3, 1, 8, 2, D, 1000) > 0
+    assert lib.msattn_workspace_bytes(3, 5, 8, 2, D, 1000) > 0
 
 
 def _attn_args(**over):
     buf = ctypes.create_string_buffer(1 << 16)
     p = ctypes.addressof(buf)
     p16 = (p + 15) // 16 * 16
-    args = dict(query=p16, k=p16, v=p16, bstride=16 * 2 * 64, sstride=2 * 64, hstride=64,
-                table=p16, lens=p16, out=p16, ws=p16, ws_bytes=1 << 15, batch=1, q_len=1, H=4,
-                KVH=2, D=64, bs=16, nb=4, W=1, max_ctx=16, causal=1, window=0, scale=0.125,
-                qd=nat.F32, kvd=nat.F32, stream=None)
+    k_off = over.pop("k_off", 0)
+    args = dict(query=p16, k=p16 + k_off, v=p16, bstride=16 * 2 * 64, sstride=2 * 64,
+                hstride=64, table=p16, lens=p16, out=p16, ws=p16, ws_bytes=1 << 15, batch=1,
+                q_len=1, H=4, KVH=2, D=64, bs=16, nb=4, W=1, max_ctx=16, causal=1, window=0,
+                scale=0.125, qd=nat.F32, kvd=nat.F32, stream=None)
     args.update(over)
     return buf, list(args.values())
 
@@ -92,9 +104,11 @@ def _attn_args(**over):
     (dict(qd=nat.FP8_E4M3), nat.ERR_INVALID_ARG),
     (dict(kvd=7), nat.ERR_INVALID_ARG),
     (dict(scale=float("nan")), nat.ERR_INVALID_ARG),
-    (dict(sstride=2 * 64 + 1), nat.ERR_INVALID_ARG),      # row not 16-byte aligned
+    (dict(k_off=2), nat.ERR_INVALID_ARG),                  # cache not aligned to its element
+    (dict(sstride=-1), nat.ERR_INVALID_ARG),
     (dict(ws_bytes=16), nat.ERR_WORKSPACE),
-    (dict(D=40, bstride=16 * 2 * 40, sstride=2 * 40, hstride=40), nat.ERR_UNSUPPORTED),
+    (dict(D=65, bstride=16 * 2 * 65, sstride=2 * 65, hstride=65), nat.ERR_INVALID_ARG),
+    (dict(D=258, bstride=16 * 2 * 258, sstride=2 * 258, hstride=258), nat.ERR_INVALID_ARG),
     (dict(query=1), nat.ERR_INVALID_ARG),                  # query not aligned to its element
     (dict(out=2), nat.ERR_INVALID_ARG),                    # output not aligned to its element
 ])
@@ -211,3 +225,84 @@ def test_noalloc_entry_checks_before_any_hip_call():
     big[-3] = big[-2] = nat.BF16
     assert lib.msattn_workspace_bytes(512, 1, 32, 8, 128, 16384) > 64 << 20
     assert lib.msattn_paged_attention_noalloc(*big) == nat.ERR_WORKSPACE
+
+
+# ------------------------------------------------------------------ kernel routes
+
+def route(B, q_len, H, KVH, D, ctx, qd=nat.BF16, kvd=None, ws=None, slot_stride=None,
+          bs=16, query=256, out=256):
+    """msattn_paged_attention_route for a contiguous cache [.., bs, KVH, D] (or the given
+    slot stride), with the call's own workspace size unless `ws` is given."""
+    lib = nat.lib()
+    kvd = qd if kvd is None else kvd
+    ss = KVH * D if slot_stride is None else slot_stride
+    ws = lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) if ws is None else ws
+    r = ctypes.c_int(-1)
+    st = lib.msattn_paged_attention_route(query, out, 256, 256, bs * ss, ss, D, B, q_len, H, KVH,
+                                          D, bs, ctx, qd, kvd, ws, ctypes.byref(r))
+    return st, r.value
+
+
+@pytest.mark.parametrize("shape,want", [
+    ((64, 1, 32, 8, 128, 8192), nat.ROUTE_STREAMK),            # C3
+    ((32, 1, 14, 2, 64, 2048), nat.ROUTE_PARTITION_FUSED),     # C2
+    ((16, 1, 28, 4, 128, 4608), nat.ROUTE_PARTITION_FUSED),    # C5 decode
+    ((2, 512, 28, 4, 128, 4608), nat.ROUTE_PREFILL),           # C5 prefill
+    ((8, 4, 28, 4, 128, 8192), nat.ROUTE_PARTITION_FUSED),     # speculative: 28 rows, 32 pairs
+    ((64, 6, 32, 8, 128, 8192), nat.ROUTE_PREFILL),            # 24 rows over 512 pairs
+    ((1, 512, 8, 1, 128, 8192), nat.ROUTE_PREFILL),            # 4096 rows: never re-streamed
+    ((4, 16, 32, 8, 128, 8192), nat.ROUTE_PARTITION_FUSED),    # 64 rows: the measured limit
+    ((4, 17, 32, 8, 128, 8192), nat.ROUTE_PREFILL),            # 68 rows: past it
+])
+def test_route_policy(shape, want):
+    """The routing rules in csrc/abi.hip: stream-K from 2^18 table tiles, the partition
+    kernel (merging in-kernel) below it; chunked prefill on the prefill kernel unless at
+    most 64 rows per KV head over too few (sequence, KV head) pairs to fill the device."""
+    st, r = route(*shape)
+    assert st == nat.OK and r == want, (nat.ROUTE_NAMES.get(r), shape)
+
+
+def test_route_generic_kernel_cases():
+    """Pairs and layouts outside the MFMA kernels take the generic kernel."""
+    assert route(4, 1, 8, 2, 40, 1000)[1] == nat.ROUTE_GENERIC            # head_dim 40
+    assert route(4, 1, 8, 2, 6, 1000)[1] == nat.ROUTE_GENERIC             # head_dim 6
+    assert route(4, 1, 8, 2, 128, 1000, qd=nat.F16, kvd=nat.BF16)[1] == nat.ROUTE_GENERIC
+    assert route(4, 1, 8, 2, 64, 1000, slot_stride=2 * 64 + 1)[1] == nat.ROUTE_GENERIC
+    assert route(4, 1, 8, 2, 64, 1000, bs=24)[1] == nat.ROUTE_GENERIC     # pages of 24 tokens
+    assert route(4, 1, 8, 2, 64, 1000, query=258)[1] == nat.ROUTE_GENERIC  # query off 16 B
+    # an fp32 query over any cache decodes on the MFMA partition kernel
+    assert route(4, 1, 8, 2, 64, 1000, qd=nat.F32, kvd=nat.FP8_E4M3)[1] == \
+        nat.ROUTE_PARTITION_FUSED
+
+
+def test_noalloc_route_falls_back_to_the_prefill_kernel():
+    """A chunked prefill the cost model sends to the partition kernel, whose partition
+    layout at this table capacity exceeds the no-allocation scratch, runs on the prefill
+    kernel (no scratch) instead of failing; a decode past the scratch still fails."""
+    lib = nat.lib()
+    B, q_len, H, KVH, D, ctx = 4, 8, 32, 8, 128, 131072
+    assert lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) > nat.NOALLOC_SCRATCH_BYTES
+    assert route(B, q_len, H, KVH, D, ctx) == (nat.OK, nat.ROUTE_PARTITION_FUSED)
+    assert route(B, q_len, H, KVH, D, ctx, ws=nat.NOALLOC_SCRATCH_BYTES) == \
+        (nat.OK, nat.ROUTE_PREFILL)
+    # the advisor's case: a 64-token chunk over a 131072-token table
+    assert route(1, 64, 28, 4, 128, 131072, ws=nat.NOALLOC_SCRATCH_BYTES) == \
+        (nat.OK, nat.ROUTE_PREFILL)
+    # an fp32 query has no prefill kernel: past the scratch it is refused
+    assert route(B, q_len, H, KVH, D, ctx, qd=nat.F32, ws=nat.NOALLOC_SCRATCH_BYTES)[0] == \
+        nat.ERR_WORKSPACE
+    assert route(512, 1, 32, 8, 128, 16384, ws=nat.NOALLOC_SCRATCH_BYTES)[0] == nat.ERR_WORKSPACE
+
+
+def test_route_rejects_bad_arguments():
+    lib = nat.lib()
+    r = ctypes.c_int(0)
+    args = [256, 256, 256, 256, 16 * 256, 256, 128, 2, 1, 4, 2, 128, 16, 100, nat.BF16,
+            nat.BF16, 1 << 30]
+    assert lib.msattn_paged_attention_route(*args, None) == nat.ERR_INVALID_ARG
+    bad = list(args)
+    bad[11] = 129  # odd head_dim
+    assert lib.msattn_paged_attention_route(*bad, ctypes.byref(r)) == nat.ERR_INVALID_ARG
+    bad = list(args)
+    bad[14] = nat.FP8_E4M3  # fp8 query
+    assert lib.msattn_paged_attention_route(*bad, ctypes.byref(r)) == nat.ERR_INVALID_ARG

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from miniserve_amd import PagedAttention, paged_attention
+from miniserve_amd import PagedAttention, kernel_route, paged_attention
 from oracle import dense, paged_sdpa
 
 pytestmark = pytest.mark.gpu
@@ -97,6 +97,13 @@ def test_prefill_every_pair(device, q_dtype, kv_dtype):
     lens = [24, 500, 131]
     note(f"prefill q={name(q_dtype)} kv={name(kv_dtype)}")
     q, kc, vc, table = case(H, KVH, D, lens, q_dtype, kv_dtype, q_len=q_len, seed=3)
+    on_prefill_kernel = q_dtype != torch.float32 and kv_dtype in (q_dtype, torch.float32,
+                                                                   torch.float8_e4m3fn)
+    # an fp32 query over any cache: the fp32 MFMA partition kernel at 16 rows per tile
+    want = ("prefill" if on_prefill_kernel else
+            "partition-fused" if q_dtype == torch.float32 else "generic")
+    route = kernel_route(q.to(device), kc.to(device), table, max_context=max(lens))
+    assert route == want, (route, want)
     out = paged_attention(q.to(device), kc.to(device), vc.to(device), table, lens)
     ref = dense.paged_attention_f64(q, kc, vc, table, lens, kv_cast=True)
     check(out, ref, q_dtype)

@@ -14,7 +14,8 @@ import numpy as np
 import pytest
 import torch
 
-from miniserve_amd import PagedAttention, gather_kv, paged_attention
+from miniserve_amd import PagedAttention, gather_kv, kernel_route, paged_attention
+from miniserve_amd import _native as nat
 from miniserve_amd.workloads import make_workload
 from oracle import dense, paged_sdpa, split_k
 
@@ -64,6 +65,31 @@ def scenario(h, kv_heads, d, lens, q_len=1, block_size=8, dtype=torch.float32, s
 
 def run_hip(device, q, kc, vc, table, lens, **kw):
     return paged_attention(q.to(device), kc.to(device), vc.to(device), table, lens, **kw)
+
+
+# Workspace header word 0 after a call: the layout the partials kernel recorded (0 the
+# partition kernels, 1 stream-K, 2 the partition kernel merging in-kernel); the prefill
+# kernel leaves the workspace untouched.
+_SENTINEL = 0x5EED
+_KIND_OF_ROUTE = {"prefill": _SENTINEL, "partition-fused": 2, "partition": 0, "generic": 0,
+                  "stream-K": 1}
+
+
+def run_routed(device, want, q, kc, vc, table, lens, **kw):
+    """run_hip, after checking that the call takes kernel route `want` (as the library
+    reports it for this shape, and as the workspace header shows after the call)."""
+    qd, kcd, vcd = q.to(device), kc.to(device), vc.to(device)
+    B, q_len, H, D = q.shape
+    max_ctx = kw.get("max_context") or max(lens)
+    got = kernel_route(qd, kcd, table, max_context=max_ctx)
+    assert got == want, f"route {got}, expected {want}"
+    ws_bytes = nat.lib().msattn_workspace_bytes(B, q_len, H, kc.shape[2], D, max_ctx)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=device)
+    ws[:4].view(torch.int32).fill_(_SENTINEL)
+    out = paged_attention(qd, kcd, vcd, table, lens, workspace=ws, **kw)
+    kind = int(ws[:4].view(torch.int32).item())
+    assert kind == _KIND_OF_ROUTE[want], f"header kind {kind} after route {want}"
+    return out
 
 
 # ------------------------------------------------------------------ addressing
@@ -354,6 +380,69 @@ def test_rope_in_kernel_matches_unfused(device, H, KVH, D, dtype, kv_dtype, wide
     assert torch.equal(fused, unfused)
     ref = dense.paged_attention_f64(qr, kc, vc, table, lens)
     assert rel_err(fused, ref) < (1e-4 if dtype == torch.float32 else BF16_REL)
+
+
+@pytest.mark.parametrize("D", [6, 40, 80, 112, 200, 256])
+@pytest.mark.parametrize("dtype,kv_dtype", [
+    (torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+    (torch.float16, torch.float8_e4m3fn)])
+def test_any_even_head_dim(device, D, dtype, kv_dtype):
+    """Head sizes outside the MFMA kernels' 64 / 128 (miniserve/attention.py:87-88 accepts
+    any even head_dim): decode, chunked prefill (causal, windowed) and fused RoPE on the
+    generic kernel's element mode (a capacity of 16, 64, 128 or 256 dims with the dims
+    past head_dim masked), each against the float64 oracle."""
+    H, KVH = 8, 2
+    bar = 1e-4 if dtype == torch.float32 else BF16_REL
+    err = abs_err if dtype == torch.float32 else rel_err
+    for q_len, lens, window in ((1, [1, 17, 300, 1000, 0, 64], None), (24, [24, 300, 90], None),
+                                (20, [500, 33], 64)):
+        note(f"head_dim {D}: {dtype} over {kv_dtype}, q_len={q_len} lens={lens} "
+             f"window={window}")
+        width = max((L + 15) // 16 for L in lens) + 2
+        q, kc, vc, table = paged_case(H, KVH, D, lens, dtype, 16, width, seed=D + q_len,
+                                      q_len=q_len)
+        kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+        out = run_routed(device, "generic", q, kc, vc, table, lens, window=window)
+        ref = dense.paged_attention_f64(q, kc.to(dtype), vc.to(dtype), table, lens,
+                                        window=window)
+        assert err(out, ref) < bar
+        if q_len == 1:
+            assert not out[4].any()  # context 0
+            v0 = vc[table[0, 0], 0].to(dtype)
+            for h in range(H):       # context 1: exactly V[0]
+                assert torch.equal(out[0, 0, h].cpu(), v0[h // (H // KVH)])
+    # fused RoPE on the element mode: the partner of dim d is d +- D / 2
+    lens = [1, 300, 77]
+    q, kc, vc, table = paged_case(H, KVH, D, lens, dtype, 16, 20, seed=D)
+    kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+    cos, sin = rope_tables(max(lens) + 8, D)
+    pos = torch.tensor([L - 1 for L in lens])
+    fused = paged_attention(q.to(device), kc.to(device), vc.to(device), table, lens,
+                            rope=(cos.to(device), sin.to(device), pos.to(device)))
+    qr = rope_unfused(q, cos, sin, pos)
+    unfused = paged_attention(qr.to(device), kc.to(device), vc.to(device), table, lens)
+    assert torch.equal(fused, unfused)
+
+
+def test_generic_kernel_rows_off_16_byte_boundaries(device):
+    """Cache views whose rows do not start on 16-byte boundaries (a bf16 pool padded to
+    head_dim + 3 per head, viewed as [.., KVH, 64]: 134-byte head stride) are accepted, as
+    the reference's indexing accepts any strided cache, and read element by element on
+    the generic kernel; decode and prefill against the float64 oracle."""
+    H, KVH, D, pad = 8, 2, 64, 3
+    lens = [5, 300, 1000]
+    for q_len in (1, 24):
+        note(f"padded cache rows: q_len={q_len}")
+        q, kc, vc, table = paged_case(H, KVH, D, lens, torch.bfloat16, 16, 70, seed=q_len)
+        kpad = torch.zeros(kc.shape[0], 16, KVH, D + pad, dtype=torch.bfloat16)
+        vpad = torch.zeros_like(kpad)
+        kpad[..., :D], vpad[..., :D] = kc, vc
+        kd, vd = kpad.to(device)[..., :D], vpad.to(device)[..., :D]
+        assert kd.stride(2) * 2 % 16 != 0
+        assert kernel_route(q.to(device), kd, table) == "generic"
+        out = paged_attention(q.to(device), kd, vd, table, lens)
+        ref = dense.paged_attention_f64(q, kc, vc, table, lens)
+        assert rel_err(out, ref) < BF16_REL
 
 
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
@@ -750,27 +839,36 @@ def test_streamk_graph_replays(device):
 
 # ------------------------------------------------------------------ chunked prefill (MFMA)
 
-@pytest.mark.parametrize("H,KVH,D,q_len,lens,dtype,causal,window", [
-    (28, 4, 128, 512, [4608, 4608], torch.bfloat16, True, None),   # C5 prefill shape
-    (28, 4, 128, 100, [100, 1000, 357], torch.bfloat16, True, None),
-    (32, 8, 128, 17, [17, 40, 3000], torch.bfloat16, True, None),
-    (32, 8, 128, 64, [64, 700], torch.float16, True, None),
-    (8, 8, 128, 33, [33, 90], torch.bfloat16, False, None),        # non-causal
-    (28, 4, 128, 200, [1200, 300], torch.bfloat16, True, 128),     # sliding window
-    (16, 2, 128, 80, [50, 2000], torch.bfloat16, True, None),      # context shorter than the chunk
+# Chunked prefill (more than 16 query rows per KV head). "prefill": the MFMA prefill
+# kernel; "partition-fused": the partition kernel at 16 rows per tile, which the cost
+# model picks for at most 64 rows per KV head over few (sequence, KV head) pairs.
+@pytest.mark.parametrize("H,KVH,D,q_len,lens,dtype,causal,window,route", [
+    (28, 4, 128, 512, [4608, 4608], torch.bfloat16, True, None, "prefill"),   # C5 prefill shape
+    (28, 4, 128, 100, [100, 1000, 357], torch.bfloat16, True, None, "prefill"),
+    (32, 8, 128, 17, [17, 40, 3000], torch.bfloat16, True, None, "prefill"),  # 68 rows
+    (32, 8, 128, 64, [64, 700], torch.float16, True, None, "prefill"),
+    (8, 8, 128, 80, [80, 150], torch.bfloat16, False, None, "prefill"),       # non-causal
+    (28, 4, 128, 200, [1200, 300], torch.bfloat16, True, 128, "prefill"),     # sliding window
+    (16, 2, 128, 80, [50, 2000], torch.bfloat16, True, None, "prefill"),      # context shorter than the chunk
     # head_dim 64 (Qwen2.5-0.5B geometry): a staging pass spans two 16-token tiles
-    (14, 2, 64, 512, [2560, 600], torch.bfloat16, True, None),
-    (14, 2, 64, 37, [37, 1500, 90], torch.float16, True, 100),
-    (8, 8, 64, 40, [40, 333], torch.bfloat16, False, None),
+    (14, 2, 64, 512, [2560, 600], torch.bfloat16, True, None, "prefill"),
+    (14, 2, 64, 37, [37, 1500, 90], torch.float16, True, 100, "prefill"),
+    (8, 8, 64, 72, [72, 333], torch.bfloat16, False, None, "prefill"),        # non-causal
+    (14, 2, 64, 37, [37, 1500, 90], torch.bfloat16, True, None, "prefill"),
+    # few pairs, at most 64 rows per KV head: the partition kernel's 16-row tiles
+    (8, 8, 128, 33, [33, 90], torch.bfloat16, False, None, "partition-fused"),
+    (8, 8, 64, 40, [40, 333], torch.bfloat16, False, None, "partition-fused"),
+    (32, 8, 128, 16, [16, 40, 3000], torch.float16, True, None, "partition-fused"),
+    (16, 2, 128, 8, [5, 2000], torch.bfloat16, True, 100, "partition-fused"),  # ctx < chunk
 ])
-def test_prefill_mfma(device, H, KVH, D, q_len, lens, dtype, causal, window):
+def test_prefill_mfma(device, H, KVH, D, q_len, lens, dtype, causal, window, route):
     note(f"prefill H={H} KVH={KVH} D={D} q_len={q_len} lens={lens} {dtype} causal={causal} "
-         f"window={window}")
+         f"window={window} route={route}")
     g = torch.Generator().manual_seed(q_len + H)
     width = max((L + 15) // 16 for L in lens) + 3
     q, kc, vc, table = wide_table_case(H, KVH, D, lens, dtype, width, seed=q_len)
     q = torch.randn(len(lens), q_len, H, D, generator=g).to(dtype)
-    out = run_hip(device, q, kc, vc, table, lens, causal=causal, window=window)
+    out = run_routed(device, route, q, kc, vc, table, lens, causal=causal, window=window)
     ref = dense.paged_attention_f64(q, kc, vc, table, lens, causal=causal, window=window)
     err = rel_err(out, ref)
     note(f"prefill max-rel {err:.3e}")

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 from miniserve_amd import _native as nat
+from miniserve_amd import kernel_route
 from oracle import dense
 
 pytestmark = pytest.mark.gpu
@@ -86,6 +87,8 @@ CASES = {  # name -> (H, KVH, D, dtype, q_len, first lens, second lens, width in
     "partition fp32": (14, 2, 64, torch.float32, 1, [400, 130, 512, 9], [200, 35], 32),
     "generic fp32": (14, 2, 96, torch.float32, 1, [400, 130, 512, 9], [200, 35], 32),
     "prefill": (28, 4, 128, torch.bfloat16, 64, [512, 700], [64], 48),
+    # 8 x 4 = 32 rows per KV head over 16 pairs: the partition kernel's 16-row tiles
+    "partition prefill": (32, 8, 128, torch.bfloat16, 8, [900, 3000], [100], 256),
 }
 
 
@@ -117,3 +120,25 @@ def test_noalloc_refuses_geometry_past_scratch(device):
         table.data_ptr(), lens.data_ptr(), out.data_ptr(), B, 1, H, KVH, D, 16, 4, W, W * 16, 1, 0,
         0.1, nat.BF16, nat.BF16, nat.stream_handle(device))
     assert st == nat.ERR_WORKSPACE
+
+
+def test_noalloc_long_table_prefill_takes_the_prefill_kernel(device):
+    """A short chunked prefill over a long-capacity table (131072 tokens): the workspace
+    entry runs it on the partition kernel, whose layout at that capacity exceeds the
+    scratch; the no-allocation entry runs it on the prefill kernel (which needs none)
+    instead of refusing it. Both within the oracle's bar, and within two output ulps of
+    each other (different kernels sum in different orders); two calls in a row, the
+    second smaller."""
+    H, KVH, D, q_len, width = 32, 8, 128, 8, 8192
+    assert nat.lib().msattn_workspace_bytes(4, q_len, H, KVH, D, width * 16) > SCRATCH
+    for i, lens in enumerate(([300, 2000, 9, 1200], [40, 700])):
+        note(f"noalloc long table call {i + 1}: lens={lens}")
+        q, kc, vc, table = make(H, KVH, D, lens, q_len, torch.bfloat16, width, seed=31 + i)
+        qd, kcd, td = q.to(device), kc.to(device), table.to(device)
+        assert kernel_route(qd, kcd, td) == "partition-fused"
+        assert kernel_route(qd, kcd, td, workspace_bytes=SCRATCH) == "prefill"
+        out_ws, out_na = call_both(device, q, kc, vc, table, lens, width * 16)
+        check_oracle(out_ws, q, kc, vc, table, lens)
+        check_oracle(out_na, q, kc, vc, table, lens)
+        diff = (out_ws.float() - out_na.float()).abs().max().item()
+        assert diff <= 2 * 2.0 ** -7 * out_ws.float().abs().max().item()
