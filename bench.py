@@ -76,6 +76,11 @@ def parse():
                          "reference runner calls them (model_runner.py:72-76: transposed q/k/v "
                          "views, an int64 device table, Python-list starts and lengths), "
                          "against the kernel's own time")
+    ap.add_argument("--decode-sweep", action="store_true",
+                    help="time decodes of the shapes around the stream-K threshold (table "
+                         "capacities of 49k-261k tiles), one line per shape with the route "
+                         "the library took; compare builds made with --define overrides of "
+                         "MSATTN_STREAMK_MIN_TILES*")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--stream-probe", action="store_true",
@@ -182,6 +187,9 @@ def main():
         return
     if args.runner:
         runner_bench(args)
+        return
+    if args.decode_sweep:
+        decode_sweep()
         return
     if args.eager:
         eager_bench(args)
@@ -654,6 +662,116 @@ def cpu_baseline(w, target_s: float):
         "cpu_model": cpu_model(),
         "torch": torch.__version__,
     }
+
+
+# (batch, H, KVH, D, lo, hi, log-uniform, max_context or None for hi, cache, query)
+SWEEP_SHAPES = [
+    (64, 32, 8, 128, 1024, 8192, True, 8158, "bf16", "bf16"),
+    (64, 32, 8, 128, 1024, 8192, True, 6144, "bf16", "bf16"),
+    (48, 32, 8, 128, 1024, 8192, True, None, "bf16", "bf16"),
+    (40, 32, 8, 128, 2048, 8192, False, None, "bf16", "bf16"),
+    (32, 32, 8, 128, 1024, 8192, False, None, "bf16", "bf16"),
+    (64, 32, 8, 128, 512, 4096, False, None, "bf16", "bf16"),
+    (24, 32, 8, 128, 4096, 16384, False, None, "bf16", "bf16"),
+    (12, 32, 8, 128, 8192, 32768, False, None, "bf16", "bf16"),
+    (192, 14, 2, 64, 2048, 8192, False, None, "bf16", "bf16"),
+    (240, 14, 2, 64, 1024, 8192, False, None, "bf16", "bf16"),
+    (128, 14, 2, 64, 1024, 8192, False, None, "bf16", "bf16"),
+    (96, 28, 4, 128, 1024, 8192, False, None, "bf16", "bf16"),
+    (120, 28, 4, 128, 1024, 8192, False, None, "bf16", "bf16"),
+    (64, 28, 4, 128, 2048, 8192, False, None, "bf16", "bf16"),
+    (64, 32, 8, 128, 1024, 8192, True, 8158, "fp8", "bf16"),
+    (48, 32, 8, 128, 1024, 8192, True, None, "fp8", "bf16"),
+    (40, 32, 8, 128, 2048, 8192, False, None, "fp8", "bf16"),
+    (64, 32, 8, 128, 1024, 8192, True, 8158, "fp32", "fp32"),
+    (48, 32, 8, 128, 1024, 8192, True, None, "fp32", "fp32"),
+    (16, 32, 8, 128, 1024, 8192, False, None, "bf16", "bf16"),
+    (16, 32, 8, 128, 1024, 8192, True, None, "bf16", "bf16"),
+    (8, 32, 8, 128, 8192, 16384, False, None, "bf16", "bf16"),
+    (4, 32, 8, 128, 16384, 32768, False, None, "bf16", "bf16"),
+    (24, 32, 8, 128, 1024, 8192, False, None, "bf16", "bf16"),
+    (24, 32, 8, 128, 1024, 8192, True, None, "bf16", "bf16"),
+    (12, 32, 8, 128, 4096, 16384, False, None, "bf16", "bf16"),
+    (48, 32, 8, 128, 512, 4096, False, None, "bf16", "bf16"),
+    (28, 32, 8, 128, 1024, 8192, True, None, "bf16", "bf16"),
+    (12, 32, 8, 128, 1024, 8192, False, None, "bf16", "bf16"),
+    (128, 14, 2, 64, 1024, 4096, False, None, "bf16", "bf16"),
+    (64, 14, 2, 64, 2048, 8192, False, None, "bf16", "bf16"),
+    (96, 14, 2, 64, 1024, 8192, False, None, "bf16", "bf16"),
+    (96, 14, 2, 64, 1024, 8192, True, None, "bf16", "bf16"),
+    (32, 28, 4, 128, 1024, 8192, False, None, "bf16", "bf16"),
+    (48, 28, 4, 128, 1024, 8192, False, None, "bf16", "bf16"),
+    (48, 28, 4, 128, 1024, 8192, True, None, "bf16", "bf16"),
+    (16, 32, 8, 128, 1024, 8192, False, None, "fp8", "bf16"),
+    (24, 32, 8, 128, 1024, 8192, False, None, "fp8", "bf16"),
+    (16, 32, 8, 128, 1024, 8192, False, None, "fp32", "fp32"),
+    (24, 32, 8, 128, 1024, 8192, False, None, "fp32", "fp32"),
+    (24, 32, 8, 128, 1024, 8192, False, None, "fp32", "bf16"),
+]
+
+
+def decode_sweep():
+    """Per-call time of each SWEEP_SHAPES decode (ten calls per hipGraph, 20 replays after
+    5), with the route the library took."""
+    import torch
+
+    from miniserve_amd.attention import kernel_route, paged_attention
+
+    dev = torch.device("cuda:0")
+    types = {"bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn, "fp32": torch.float32}
+    for i, (B, H, KVH, D, lo, hi, logu, cap, kvn, qn) in enumerate(SWEEP_SHAPES):
+        g = torch.Generator().manual_seed(i)
+        if logu:
+            lens = torch.exp(torch.empty(B).uniform_(math.log(lo), math.log(hi), generator=g))
+            lens = lens.floor().long()
+        else:
+            lens = torch.randint(lo, hi + 1, (B,), generator=g)
+        cap = cap or hi
+        lens = lens.clamp(max=cap)
+        W = -(-cap // 16)
+        pool = int(sum(-(-int(L) // 16) for L in lens)) + 8
+        kc = torch.randn(pool, 16, KVH, D, device=dev).to(types[kvn])
+        vc = torch.randn(pool, 16, KVH, D, device=dev).to(types[kvn])
+        perm = torch.randperm(pool, generator=g).int().to(dev)
+        table = torch.zeros(B, W, dtype=torch.int32, device=dev)
+        cur = 0
+        for b in range(B):
+            n = -(-int(lens[b]) // 16)
+            table[b, :n] = perm[cur:cur + n]
+            cur += n
+        q = torch.randn(B, 1, H, D, device=dev).to(types[qn])
+        ln = lens.int().to(dev)
+        out = torch.empty_like(q)
+        ws = torch.zeros(256 << 20, dtype=torch.uint8, device=dev)
+        step = lambda: paged_attention(q, kc, vc, table, ln, max_context=cap, workspace=ws,
+                                       out=out)
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(10):
+                step()
+        for _ in range(MIN_WARMUP_REPLAYS):
+            graph.replay()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(20):
+            graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        print(json.dumps({"batch": B, "geometry": f"H{H}/KVH{KVH}/D{D}",
+                          "contexts": f"{lo}..{hi} {'log-U' if logu else 'U'}",
+                          "max_context": cap, "table_tiles": B * KVH * W,
+                          "query": qn, "cache": kvn,
+                          "route": kernel_route(q, kc, table, max_context=cap, out=out),
+                          "us_per_call": round(start.elapsed_time(stop) * 1e3 / 200, 2)}),
+              flush=True)
+        del kc, vc, ws
+        torch.cuda.empty_cache()
 
 
 def _decode_inputs(w, dev):

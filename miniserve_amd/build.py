@@ -1,10 +1,12 @@
 """Build libmsattn.so (gfx950) in-tree with hipcc.
 
-Usage: ``python -m miniserve_amd.build`` (or ``__graft_entry__.build()``).
-Every ``csrc/*.hip`` file is compiled to an object under ``_build/`` in
-parallel, then linked into ``miniserve_amd/libmsattn.so``, which the Python
-package loads with ctypes. A build always recompiles: nothing is cached
-across calls.
+Usage: ``python -m miniserve_amd.build [--define NAME=VALUE ...]`` (or
+``__graft_entry__.build()``). Every ``csrc/*.hip`` file is compiled to an object
+under ``_build/`` in parallel, then linked into ``miniserve_amd/libmsattn.so``,
+which the Python package loads with ctypes. A build always recompiles: nothing
+is cached across calls. ``--define`` overrides one of the compile-time tuning
+knobs (the ``MSATTN_*`` macros of csrc/) for a measurement build; rebuild
+without it to restore the defaults.
 """
 from __future__ import annotations
 
@@ -59,8 +61,16 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
-def build(verbose: bool = True, jobs: int | None = None) -> Path:
-    """Compile every csrc/*.hip for gfx950 and link libmsattn.so; returns its path."""
+def build(verbose: bool = True, jobs: int | None = None,
+          defines: list[str] | None = None) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libmsattn.so; returns its path.
+    `defines`: NAME=VALUE overrides of MSATTN_* tuning macros."""
+    extra = []
+    for d in defines or []:
+        name = d.split("=", 1)[0]
+        if not name.startswith("MSATTN_") or not name.replace("_", "").isalnum():
+            raise ValueError(f"--define takes MSATTN_* tuning macros, not {d!r}")
+        extra.append(f"-D{d}")
     if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
         raise RuntimeError("hipcc not found; the msattn library needs ROCm's hipcc")
     hipcc = HIPCC if Path(HIPCC).exists() else shutil.which("hipcc")
@@ -73,7 +83,8 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
         src, obj = pair
         if verbose:
             print(f"[msattn build] hipcc {src.name}", flush=True)
-        _run([hipcc, *COMMON_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)])
+        _run([hipcc, *COMMON_FLAGS, *extra, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o",
+              str(obj)])
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(compile_one, zip(sources, objs)))
@@ -86,4 +97,9 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    import argparse
+
+    ap = argparse.ArgumentParser(description="build libmsattn.so for gfx950")
+    ap.add_argument("--define", action="append", default=[], metavar="MSATTN_NAME=VALUE",
+                    help="override a compile-time tuning macro (measurement builds)")
+    build(defines=ap.parse_args().define)

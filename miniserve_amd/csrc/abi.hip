@@ -29,12 +29,20 @@ static_assert(kPartMax / 8 >= 16 * kMfmaWaves && (kPartMax / 8) % (16 * kMfmaWav
 #endif
 constexpr int64_t kTargetSlots = MSATTN_TARGET_SLOTS;  // workgroup slots wanted in a launch
 #ifndef MSATTN_STREAMK_MIN_TILES
-#define MSATTN_STREAMK_MIN_TILES 262144
+#define MSATTN_STREAMK_MIN_TILES 65536
 #endif
-// Decode launches whose (batch x KV heads x table tiles) reach this use stream-K; below it
-// the partition kernel was measured as fast or faster (3-12 % at 65,536 tiles, even at
-// 131,072 with long contexts), above it stream-K (11 % at 64 sequences of 1-8k tokens).
+#ifndef MSATTN_STREAMK_MIN_TILES_D64
+#define MSATTN_STREAMK_MIN_TILES_D64 131072
+#endif
+// Decode launches whose (batch x KV heads x table tiles) reach this use stream-K, below it
+// the partition kernel. Measured on 40 shapes (graph steps, both kernels on each): at
+// head_dim 128, stream-K was 12-25 % faster from 65,536 tiles up (bf16, fp8, fp32 caches;
+// H32/KVH8 and H28/KVH4), level or 10 % slower only where the contexts fill little of
+// the table (16 log-uniform 1-8k contexts: 41.3 against 37.3 us); at head_dim 64
+// (H14/KVH2) the partition kernel stays 9-14 % faster up to 98,304 tiles and stream-K
+// wins from 131,072 (5-14 %). At 49,152 tiles the two are level.
 constexpr int64_t kStreamKMinTiles = MSATTN_STREAMK_MIN_TILES;
+constexpr int64_t kStreamKMinTilesD64 = MSATTN_STREAMK_MIN_TILES_D64;
 // The same for a 16-bit query over an fp8 cache at 8 rows per tile (G = 5..8), where
 // stream-K's two waves per SIMD win from 65,536 tiles (37.0 against 44.3 us for 64 x
 // H14/KVH2 at 2-8k tokens); below it the partition kernel does (11.8 against 20.4 us).
@@ -411,7 +419,9 @@ PartialsPlan plan_partials(const void* query, int q_dtype, int kv_dtype, int hea
       static_cast<int64_t>(batch) * num_kv_heads * ceil_div(max_context, 16);
   const bool kv_fp8 = kv_dtype == MSATTN_FP8_E4M3;
   const int64_t sk_min_tiles =
-      kv_fp8 && q_dtype != MSATTN_F32 && pl.RT == 8 ? kStreamKMinTilesFp8Rt8 : kStreamKMinTiles;
+      kv_fp8 && q_dtype != MSATTN_F32 && pl.RT == 8 ? kStreamKMinTilesFp8Rt8
+      : head_dim == 64                               ? kStreamKMinTilesD64
+                                                     : kStreamKMinTiles;
   const int64_t triples = static_cast<int64_t>(batch) * num_kv_heads * ceil_div(rows, pl.RT);
   if (pl.use_mfma && q_len == 1 && batch <= kSkMaxBatch && tile_capacity >= sk_min_tiles)
     pl.kind = 1;

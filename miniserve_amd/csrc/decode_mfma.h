@@ -222,6 +222,9 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 // between workgroups inside one launch go through these, so publishing them needs only
 // their completion (s_waitcnt vmcnt(0)), not a writeback of the whole L2.
 constexpr int kWaitVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt and lgkmcnt not waited
+#ifndef MSATTN_MERGE_ACQREL
+#define MSATTN_MERGE_ACQREL 0
+#endif
 
 __device__ __forceinline__ void store2_device(float* p, float a, float b) {  // p: 8-byte aligned
   const uint64_t v = static_cast<uint64_t>(__float_as_uint(a)) |
@@ -733,7 +736,16 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
     __syncthreads();
     if (tid == 0) {
       int* t = p.tickets + ((static_cast<int64_t>(b) * p.KVH + kvh) * p.rtiles + rtile);
-      const int old = __hip_atomic_fetch_add(t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // MSATTN_MERGE_ACQREL = 0 (default): a relaxed ticket. The partials were stored
+      // through with agent-scope (sc1) stores, whose completion the s_waitcnt above
+      // awaits in every thread before the barrier, and the last workgroup reads them with
+      // agent-scope (sc1) loads issued after its barrier, which follows the ticket's
+      // return: on gfx950 no L2 writeback or invalidation is needed. 1: the same exchange
+      // as a release / acquire pair under the HIP memory model (the compiler then writes
+      // back and invalidates this XCD's L2 around the ticket), for comparison.
+      const int old = __hip_atomic_fetch_add(t, 1, MSATTN_MERGE_ACQREL ? __ATOMIC_ACQ_REL
+                                                                       : __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
       const int last = old == nparts - 1;
       if (last) __hip_atomic_store(t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_last = last;

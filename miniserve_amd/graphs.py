@@ -25,12 +25,41 @@ Differences, deliberate:
 """
 from __future__ import annotations
 
+from itertools import chain
 from typing import List, Sequence
 
+import numpy as np
 import torch
 
 from . import _native as nat
 from .attention import PagedAttention, paged_attention
+
+
+def fill_table(tab: np.ndarray, tables, batch: int) -> None:
+    """Write the page ids of `batch` rows into the int32 array tab [rows >= batch, width]:
+    row b's pages from column 0, every other entry -1 (a hole). `tables` is a sequence of
+    per-row page-id sequences, or a 2-D array / tensor of page ids padded with -1. Ragged
+    lists are placed with one scatter (no per-row arrays)."""
+    width = tab.shape[1]
+    tab.fill(-1)
+    if isinstance(tables, (torch.Tensor, np.ndarray)):
+        arr = tables.cpu().numpy() if isinstance(tables, torch.Tensor) else tables
+        if arr.ndim != 2 or arr.shape[0] != batch or arr.shape[1] > width:
+            raise ValueError(f"tables must be [{batch}, <= {width}] page ids")
+        tab[:batch, : arr.shape[1]] = arr
+        return
+    rows = [r if isinstance(r, (list, tuple)) else list(r) for r in tables]
+    if len(rows) != batch:
+        raise ValueError(f"{len(rows)} table rows for a batch of {batch}")
+    counts = np.fromiter((len(r) for r in rows), dtype=np.int64, count=batch)
+    if batch and int(counts.max()) > width:
+        b = int(counts.argmax())
+        raise ValueError(f"row {b}: {int(counts[b])} pages > table width {width}")
+    total = int(counts.sum())
+    flat = np.fromiter(chain.from_iterable(rows), dtype=np.int32, count=total)
+    row_of = np.repeat(np.arange(batch), counts)
+    first = np.repeat(np.cumsum(counts) - counts, counts)
+    tab[row_of, np.arange(total) - first] = flat
 
 
 class DecodeLayer:
@@ -76,17 +105,30 @@ class GraphedDecodeRunner:
                             self.num_kv_heads, self.head_dim)
         dev = self._device
 
+        Wt = self.table_width
+
         def input_set():
+            # table, write positions and lengths share one int32 buffer, so a step's
+            # integer inputs go to the device in one copy from one pinned staging buffer
+            ints = torch.zeros(Bm * Wt + 2 * Bm, dtype=torch.int32, device=dev)
+            ints[: Bm * Wt].fill_(-1)
             return {
                 "q": torch.zeros((L, Bm, 1, H, D), dtype=self.dtype, device=dev),
                 "k": torch.zeros((L, Bm, 1, KVH, D), dtype=self.dtype, device=dev),
                 "v": torch.zeros((L, Bm, 1, KVH, D), dtype=self.dtype, device=dev),
-                "table": torch.full((Bm, self.table_width), -1, dtype=torch.int32, device=dev),
-                "start": torch.zeros((Bm,), dtype=torch.int32, device=dev),
-                "lens": torch.zeros((Bm,), dtype=torch.int32, device=dev),
+                "ints": ints,
+                "table": ints[: Bm * Wt].view(Bm, Wt),
+                "start": ints[Bm * Wt: Bm * Wt + Bm],
+                "lens": ints[Bm * Wt + Bm:],
             }
 
         self._in = [input_set() for _ in range(2)]
+        # Host staging per input set (pinned; refilled only once that set's previous copy
+        # has run, which its event records).
+        self._stage = [torch.empty(Bm * Wt + 2 * Bm, dtype=torch.int32, pin_memory=True)
+                       for _ in range(2)]
+        self._stage_np = [t.numpy() for t in self._stage]
+        self._stage_ev: list = [None, None]
         self._out = torch.zeros((L, Bm, 1, H, D), dtype=self.dtype, device=dev)
         self.max_context = self.table_width * self.block_size
         ws_bytes = max(nat.lib().msattn_workspace_bytes(b, 1, H, KVH, D, self.max_context)
@@ -136,10 +178,11 @@ class GraphedDecodeRunner:
         """One decode step for len(ctx) real rows.
 
         q [L, B, 1, H, D], k/v [L, B, 1, KVH, D]: the new token of every row and layer;
-        tables: page ids per row; ctx: tokens already cached per row. Row b's new k/v
-        land at position ctx[b] and it attends over ctx[b] + 1 tokens. Returns the
-        attention output [L, B, 1, H, D]. Pad rows are padded to the bucket with
-        table -1 and ctx 0 and produce nothing.
+        tables: page ids per row (lists, or a 2-D int array / tensor whose rows are padded
+        with -1); ctx: tokens already cached per row. Row b's new k/v land at position
+        ctx[b] and it attends over ctx[b] + 1 tokens. Returns the attention output
+        [L, B, 1, H, D]. Pad rows are padded to the bucket with table -1 and ctx 0 and
+        produce nothing.
         """
         B = len(ctx)
         if B > self.max_batch:
@@ -152,24 +195,10 @@ class GraphedDecodeRunner:
         idx = self._buf_idx
         self._buf_idx = 1 - self._buf_idx
         buf = self._in[idx]
+        self._stage_inputs(idx, tables, ctx)
         buf["q"][:, :B].copy_(q)
         buf["k"][:, :B].copy_(k)
         buf["v"][:, :B].copy_(v)
-        host_table = torch.full((self.max_batch, self.table_width), -1, dtype=torch.int32)
-        for b, row in enumerate(tables):
-            row = list(row)
-            if len(row) > self.table_width:
-                raise ValueError(f"row {b}: {len(row)} pages > table width {self.table_width}")
-            host_table[b, : len(row)] = torch.tensor(row, dtype=torch.int32)
-        start = torch.zeros(self.max_batch, dtype=torch.int32)
-        start[:B] = torch.tensor([int(c) for c in ctx], dtype=torch.int32)
-        lens = torch.zeros(self.max_batch, dtype=torch.int32)
-        lens[:B] = start[:B] + 1
-        if int(lens.max()) > self.max_context:
-            raise ValueError(f"context {int(lens.max())} > table capacity {self.max_context}")
-        buf["table"].copy_(host_table)
-        buf["start"].copy_(start)
-        buf["lens"].copy_(lens)
         if use_graph:
             self._graphs[bucket][idx]()
         else:
@@ -177,11 +206,36 @@ class GraphedDecodeRunner:
         self.replay_log.append((len(self.replay_log), idx))
         return self._out[:, :B].clone()
 
+    def _stage_inputs(self, idx: int, tables, ctx: Sequence[int]) -> None:
+        """Block tables, write positions and lengths of a step into input set idx: filled
+        in its pinned staging buffer (vectorised, no per-row tensors) and sent in one
+        asynchronous copy on the current stream."""
+        Bm, Wt = self.max_batch, self.table_width
+        B = len(ctx)
+        ev = self._stage_ev[idx]
+        if ev is not None:
+            ev.synchronize()  # the staging buffer's previous copy has run
+        st = self._stage_np[idx]
+        fill_table(st[: Bm * Wt].reshape(Bm, Wt), tables, B)
+        start = st[Bm * Wt: Bm * Wt + Bm]
+        lens = st[Bm * Wt + Bm:]
+        start.fill(0)
+        start[:B] = np.fromiter((int(c) for c in ctx), dtype=np.int32, count=B)
+        lens.fill(0)
+        lens[:B] = start[:B] + 1
+        top = int(lens[:B].max())
+        if top > self.max_context:
+            raise ValueError(f"context {top} > table capacity {self.max_context}")
+        self._in[idx]["ints"].copy_(self._stage[idx], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._stage_ev[idx] = ev
+
     def memory_report(self) -> dict:
         """Static footprint: inputs are max-bucket-sized and shared by every bucket's
         graphs, so the total tracks the largest bucket, not the number of buckets."""
         nb = lambda t: t.element_size() * t.numel()
-        per_set = sum(nb(t) for t in self._in[0].values())
+        per_set = sum(nb(self._in[0][name]) for name in ("q", "k", "v", "ints"))
         out_b = nb(self._out) + nb(self._ws)
         max_fp = per_set + out_b
         total = 2 * per_set + out_b

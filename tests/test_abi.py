@@ -253,11 +253,18 @@ def route(B, q_len, H, KVH, D, ctx, qd=nat.BF16, kvd=None, ws=None, slot_stride=
     ((1, 512, 8, 1, 128, 8192), nat.ROUTE_PREFILL),            # 4096 rows: never re-streamed
     ((4, 16, 32, 8, 128, 8192), nat.ROUTE_PARTITION_FUSED),    # 64 rows: the measured limit
     ((4, 17, 32, 8, 128, 8192), nat.ROUTE_PREFILL),            # 68 rows: past it
+    # stream-K thresholds: 2^16 table tiles at head_dim 128, 2^17 at head_dim 64
+    ((64, 1, 32, 8, 128, 8158), nat.ROUTE_STREAMK),            # C3 called with max(lens)
+    ((16, 1, 32, 8, 128, 8192), nat.ROUTE_STREAMK),            # 65,536 tiles
+    ((15, 1, 32, 8, 128, 8192), nat.ROUTE_PARTITION_FUSED),    # 61,440
+    ((64, 1, 14, 2, 64, 8192), nat.ROUTE_PARTITION_FUSED),     # 65,536 at head_dim 64
+    ((128, 1, 14, 2, 64, 8192), nat.ROUTE_STREAMK),            # 131,072 at head_dim 64
 ])
 def test_route_policy(shape, want):
-    """The routing rules in csrc/abi.hip: stream-K from 2^18 table tiles, the partition
-    kernel (merging in-kernel) below it; chunked prefill on the prefill kernel unless at
-    most 64 rows per KV head over too few (sequence, KV head) pairs to fill the device."""
+    """The routing rules in csrc/abi.hip: stream-K from 2^16 table tiles at head_dim 128
+    (2^17 at head_dim 64), the partition kernel (merging in-kernel) below; chunked prefill
+    on the prefill kernel unless at most 64 rows per KV head over too few (sequence, KV
+    head) pairs to fill the device."""
     st, r = route(*shape)
     assert st == nat.OK and r == want, (nat.ROUTE_NAMES.get(r), shape)
 

@@ -129,3 +129,39 @@ def test_apply_rope_closed_form(pos_shape, with_k):
     bad = q * cos[pos].unsqueeze(1 if pos.ndim == 2 else 0) + \
         torch.cat([q[..., D // 2:], q[..., :D // 2]], -1) * sin[pos].unsqueeze(1 if pos.ndim == 2 else 0)
     assert not torch.allclose(bad, closed(q), atol=1e-3)
+
+
+def test_runner_table_fill_matches_row_by_row():
+    """GraphedDecodeRunner's host staging places ragged per-row page lists with one
+    scatter (graphs.fill_table); it must equal the row-by-row fill, for lists, tuples,
+    generators, arrays and tensors, and refuse rows wider than the table."""
+    import numpy as np
+
+    from miniserve_amd.graphs import fill_table
+
+    rng = np.random.default_rng(3)
+    for trial in range(50):
+        rows, width, batch = int(rng.integers(1, 70)), int(rng.integers(1, 40)), 0
+        batch = int(rng.integers(1, rows + 1))
+        lists = [list(rng.integers(0, 10_000, int(rng.integers(0, width + 1))))
+                 for _ in range(batch)]
+        want = np.full((rows, width), -1, dtype=np.int32)
+        for b, r in enumerate(lists):
+            want[b, : len(r)] = r
+        got = np.zeros((rows, width), dtype=np.int32)
+        fill_table(got, lists, batch)
+        assert np.array_equal(got, want), trial
+        got[:] = 7
+        fill_table(got, [tuple(r) for r in lists], batch)
+        assert np.array_equal(got, want)
+        got[:] = 7
+        fill_table(got, [iter(r) for r in lists], batch)
+        assert np.array_equal(got, want)
+        dense = want[:batch]
+        got[:] = 7
+        fill_table(got, torch.from_numpy(dense.copy()), batch)
+        assert np.array_equal(got, want)
+    with pytest.raises(ValueError):
+        fill_table(np.zeros((2, 3), dtype=np.int32), [[1, 2, 3, 4]], 1)
+    with pytest.raises(ValueError):
+        fill_table(np.zeros((2, 3), dtype=np.int32), [[1]], 2)

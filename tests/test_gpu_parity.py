@@ -797,6 +797,55 @@ def test_streamk_large_batch(device, batch, max_ctx, width):
         assert torch.equal(out[1, 0, h].cpu(), vc[table[1, 0], 0, h // (H // KVH)])
 
 
+@pytest.mark.parametrize("other", ["another batch", "same batch, other heads"])
+def test_merge_reads_only_its_workspace_after_another_geometry(device, other):
+    """msattn_merge_partials over a workspace last written by a stream-K call of another
+    geometry: the header describes a layout that is not this call's. The merge checks every
+    header word and clamps the slots it reads to the workspace (merge_slot_range), so the
+    call returns MSATTN_OK with a finite output (zeros where the header names no slot of
+    this row) and the next regular call on the workspace is correct again."""
+    lib = nat.lib()
+    H, KVH, D = 32, 8, 128
+    lens = [3000, 17, 5000, 0, 800, 4096, 1, 2500] * 8
+    width = SK_MIN_TILES // (len(lens) * KVH) + 1
+    note(f"stale header ({other}): stream-K over {len(lens)} sequences")
+    q, kc, vc, table = wide_table_case(H, KVH, D, lens, torch.bfloat16, width, seed=404)
+    kd, vd = kc.to(device), vc.to(device)
+    td = table.to(device=device, dtype=torch.int32)
+    ld = torch.tensor(lens, dtype=torch.int32, device=device)
+    cap = width * 16
+    ws = torch.zeros(256 << 20, dtype=torch.uint8, device=device)
+    stream = nat.stream_handle(device)
+    st = lib.msattn_paged_attention_partials(
+        q.to(device).data_ptr(), kd.data_ptr(), vd.data_ptr(), kd.stride(0), kd.stride(1),
+        kd.stride(2), td.data_ptr(), ld.data_ptr(), ws.data_ptr(), ws.numel(), len(lens), 1, H,
+        KVH, D, 16, kd.shape[0], width, cap, 1, 0, 1 / D ** 0.5, nat.BF16, nat.BF16, stream)
+    assert st == nat.OK
+    torch.cuda.synchronize()
+    assert int(ws[:4].view(torch.int32).item()) == 1  # a stream-K header
+    if other == "another batch":
+        B2, H2, KVH2, D2, ctx2 = 5, 14, 2, 64, 1000
+    else:  # the header's batch matches, so its stream-K words are used, for other heads
+        B2, H2, KVH2, D2, ctx2 = len(lens), 8, 8, 64, 4096
+    need = lib.msattn_workspace_bytes(B2, 1, H2, KVH2, D2, ctx2)
+    assert need <= ws.numel()
+    lens2 = torch.randint(0, ctx2 + 1, (B2,), dtype=torch.int32, device=device)
+    out = torch.full((B2, 1, H2, D2), float("nan"), dtype=torch.bfloat16, device=device)
+    st = lib.msattn_merge_partials(ws.data_ptr(), need, lens2.data_ptr(), out.data_ptr(), B2, 1,
+                                   H2, KVH2, D2, ctx2, nat.BF16, stream)
+    assert st == nat.OK
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    # the workspace still serves a regular call of the second geometry
+    q2, kc2, vc2, table2 = wide_table_case(H2, KVH2, D2, [min(int(x), ctx2) for x in lens2],
+                                           torch.bfloat16, ctx2 // 16, seed=405)
+    lens2l = [int(x) for x in lens2]
+    got = paged_attention(q2.to(device), kc2.to(device), vc2.to(device), table2, lens2l,
+                          max_context=ctx2, workspace=ws)
+    ref = dense.paged_attention_f64(q2, kc2, vc2, table2, lens2l)
+    assert rel_err(got, ref) < BF16_REL
+
+
 def test_streamk_graph_replays(device):
     """Stream-K decode captured in a graph: replays with new lengths match eager bit-exactly."""
     note("stream-K graph")
