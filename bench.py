@@ -81,6 +81,14 @@ def parse():
                          "capacities of 49k-261k tiles), one line per shape with the route "
                          "the library took; compare builds made with --define overrides of "
                          "MSATTN_STREAMK_MIN_TILES*")
+    ap.add_argument("--prefill-sweep", action="store_true",
+                    help="time chunked prefills of 16-224 tasks (sequence x KV head x 128-row "
+                         "block) on the prefill kernel, one line per shape; compare builds "
+                         "made with --define MSATTN_PF_STREAMK=0 / 1")
+    ap.add_argument("--warm-ms", type=float, default=200.0,
+                    help="untimed graph replays before each timed loop last at least this "
+                         "long (and at least --warmup steps), so timing starts at steady "
+                         "clocks")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--stream-probe", action="store_true",
@@ -154,6 +162,23 @@ def stream_read_gbs(dev, launches: int = 20) -> float:
     return nbytes / (ms * 1e-3) / 1e9
 
 
+def warm(replay, warm_ms: float, min_replays: int) -> None:
+    """Replay a captured graph at least `min_replays` times and for at least `warm_ms` of
+    wall time, then synchronise. Under sustained load the MFMA-bound prefill kernel runs
+    ~10 % faster after the first ~20 ms (its time falls from ~91 to ~81 us per launch over
+    the first ~150 launches of a run, while a decode kernel's stays flat): timing starts
+    in that steady state."""
+    import torch
+
+    t0 = time.perf_counter()
+    done = 0
+    while done < min_replays or (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(8):
+            replay()
+        done += 8
+        torch.cuda.synchronize()
+
+
 def warmup_replays(warmup: int, steps_per_graph: int) -> int:
     """Untimed replays of a captured graph before the timed ones: the --warmup steps'
     worth, and never fewer than MIN_WARMUP_REPLAYS (the first replays of a new graph run
@@ -190,6 +215,9 @@ def main():
         return
     if args.decode_sweep:
         decode_sweep()
+        return
+    if args.prefill_sweep:
+        prefill_sweep(args)
         return
     if args.eager:
         eager_bench(args)
@@ -259,9 +287,7 @@ def main():
             for _ in range(n_in_graph):
                 step()
         torch.cuda.synchronize()
-        for _ in range(warmup_replays(args.warmup, n_in_graph)):
-            graph.replay()
-        torch.cuda.synchronize()
+        warm(graph.replay, args.warm_ms, warmup_replays(args.warmup, n_in_graph))
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(args.steps // n_in_graph):
@@ -476,9 +502,7 @@ def prefill_bench(args):
         with torch.cuda.graph(graph):
             for _ in range(n_in_graph):
                 step()
-        for _ in range(warmup_replays(args.warmup, n_in_graph)):
-            graph.replay()
-        torch.cuda.synchronize()
+        warm(graph.replay, args.warm_ms, warmup_replays(args.warmup, n_in_graph))
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(args.steps // n_in_graph):
@@ -522,6 +546,7 @@ def prefill_bench(args):
     # MI355X dense matrix peaks: bf16 2.5 PFLOP/s, fp32 157.3 TFLOP/s.
     peak = 157.3 if fp32 else 2500.0
     kernel = {"prefill": "msattn::prefill_mfma_kernel",
+              "prefill stream-K": "msattn::prefill_mfma_kernel (stream-K schedule)",
               "partition-fused": "msattn::decode_mfma_kernel (16-row tiles, merged in-kernel)"
               }.get(route, route)
     result = {
@@ -770,6 +795,72 @@ def decode_sweep():
                           "route": kernel_route(q, kc, table, max_context=cap, out=out),
                           "us_per_call": round(start.elapsed_time(stop) * 1e3 / 200, 2)}),
               flush=True)
+        del kc, vc, ws
+        torch.cuda.empty_cache()
+
+
+# (batch, H, KVH, q_len, context): causal bf16 chunks at the end of the context, D = 128
+PREFILL_SWEEP_SHAPES = [
+    (1, 32, 8, 64, 16384),     # 16 tasks
+    (1, 32, 8, 128, 8192),     # 32
+    (1, 8, 8, 512, 32768),     # 32
+    (1, 32, 8, 256, 8192),     # 64
+    (2, 32, 8, 192, 6144),     # 96
+    (1, 28, 4, 512, 4608),     # 112
+    (1, 32, 8, 512, 8192),     # 128
+    (4, 32, 8, 128, 2048),     # 128
+    (2, 32, 8, 384, 4096),     # 192
+    (2, 28, 4, 512, 4608),     # 224 (C5)
+]
+
+
+def prefill_sweep(args):
+    """Graph-step time of each PREFILL_SWEEP_SHAPES call (ten per graph, 20 replays after
+    the warm-up) with its task count and TFLOP/s."""
+    import torch
+
+    from miniserve_amd.attention import kernel_route, paged_attention
+
+    dev = torch.device("cuda:0")
+    for i, (B, H, KVH, T, L) in enumerate(PREFILL_SWEEP_SHAPES):
+        g = torch.Generator(device=dev).manual_seed(i)
+        D, bs = 128, 16
+        pages = -(-L // bs)
+        pool = B * pages + 4
+        kc = torch.randn(pool, bs, KVH, D, generator=g, device=dev).to(torch.bfloat16)
+        vc = torch.randn(pool, bs, KVH, D, generator=g, device=dev).to(torch.bfloat16)
+        table = torch.randperm(pool, device=dev)[: B * pages].view(B, pages).int()
+        q = torch.randn(B, T, H, D, generator=g, device=dev).to(torch.bfloat16)
+        lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+        out = torch.empty_like(q)
+        ws = torch.zeros(256 << 20, dtype=torch.uint8, device=dev)
+        step = lambda: paged_attention(q, kc, vc, table, lens, max_context=L, workspace=ws,
+                                       out=out)
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(10):
+                step()
+        warm(graph.replay, args.warm_ms, MIN_WARMUP_REPLAYS)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(20):
+            graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(stop) * 1e3 / 200
+        rows = T * (H // KVH)
+        tasks = -(-rows // 128) * KVH * B
+        flops = B * sum(4 * D * H * (L - T + j + 1) for j in range(T))
+        print(json.dumps({"batch": B, "geometry": f"H{H}/KVH{KVH}/D{D}", "q_len": T,
+                          "context": L, "tasks": tasks,
+                          "route": kernel_route(q, kc, table, max_context=L, out=out),
+                          "us_per_call": round(us, 2),
+                          "tflops": round(flops / (us * 1e-6) / 1e12, 1)}), flush=True)
         del kc, vc, ws
         torch.cuda.empty_cache()
 

@@ -56,6 +56,7 @@ typedef enum msattn_route {
   MSATTN_ROUTE_PARTITION = 3,        /* MFMA partition kernel, then the merge kernel */
   MSATTN_ROUTE_STREAMK = 4,          /* MFMA stream-K decode kernel, then the merge kernel */
   MSATTN_ROUTE_GENERIC = 5,          /* generic VALU kernel, then the merge kernel */
+  MSATTN_ROUTE_PREFILL_STREAMK = 6,  /* prefill kernel, stream-K schedule (merge in-kernel) */
 } msattn_route;
 
 /* ABI version (MSATTN_ABI_VERSION). No reference counterpart. */
@@ -120,6 +121,12 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
  * (sequence, KV head, row tile) to finish folds the others' partials into `out`, and a
  * sequence of one partition writes `out` directly. The partials kernel's rounding and
  * the fold are those of the two-launch path, with the fold's sums in another order.
+ * A prefill-kernel launch whose tasks (row blocks of 128 x KV heads x sequences) would
+ * leave CUs idle in one-task-per-workgroup rounds runs stream-K when a cost model in sizes
+ * only predicts it faster and the workspace is msattn_workspace_bytes() or more: one
+ * workgroup per CU, each an equal share of all tasks' key steps, a task split between
+ * workgroups folded by the last of them (tickets in the workspace header, which every call
+ * leaves at zero); the fold sums the pieces in another order than one workgroup would.
  */
 int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
                            int64_t cache_block_stride, int64_t cache_slot_stride,

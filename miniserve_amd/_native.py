@@ -25,9 +25,10 @@ OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_HIP = 0, 1, 2, 3, 4
 
 # msattn_route codes: the kernel msattn_paged_attention runs for a call's shape.
 ROUTE_PREFILL, ROUTE_PARTITION_FUSED, ROUTE_PARTITION, ROUTE_STREAMK, ROUTE_GENERIC = 1, 2, 3, 4, 5
+ROUTE_PREFILL_STREAMK = 6
 ROUTE_NAMES = {ROUTE_PREFILL: "prefill", ROUTE_PARTITION_FUSED: "partition-fused",
                ROUTE_PARTITION: "partition", ROUTE_STREAMK: "stream-K",
-               ROUTE_GENERIC: "generic"}
+               ROUTE_GENERIC: "generic", ROUTE_PREFILL_STREAMK: "prefill stream-K"}
 NOALLOC_SCRATCH_BYTES = 64 << 20
 MAX_HEAD_DIM = 256
 

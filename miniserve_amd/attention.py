@@ -442,8 +442,9 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
 def kernel_route(query: torch.Tensor, k_cache: torch.Tensor, block_table,
                  max_context: int | None = None, out: torch.Tensor | None = None,
                  workspace_bytes: int | None = None) -> str:
-    """Name of the kernel ``paged_attention`` runs for this call: "prefill",
-    "partition-fused", "partition", "stream-K" or "generic" (msattn_paged_attention_route).
+    """Name of the kernel ``paged_attention`` runs for this call: "prefill", "prefill
+    stream-K" (the prefill kernel's stream-K schedule), "partition-fused", "partition",
+    "stream-K" (the stream-K decode kernel) or "generic" (msattn_paged_attention_route).
 
     The choice depends on shapes, types and alignment, not on context-length values;
     ``max_context`` defaults to the table capacity, ``workspace_bytes`` to the call's own

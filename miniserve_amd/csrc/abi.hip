@@ -81,6 +81,50 @@ constexpr bool kWideFp8Uncapped = MSATTN_WIDE_FP8_UNCAPPED != 0;
 // Workgroups per CU from which a head_dim-64 partition launch takes the deeper residency.
 constexpr int kDeepMinPerCu = MSATTN_DEEP_MIN_PER_CU;
 
+// Stream-K scheduling of the prefill kernel's tasks: 1 where the cost model below prefers
+// it, 2 always (where it fits), 0 never (one task per workgroup).
+#ifndef MSATTN_PF_STREAMK
+#define MSATTN_PF_STREAMK 1
+#endif
+constexpr int kPfStreamK = MSATTN_PF_STREAMK;
+static_assert(kPfSkMaxTasks <= kMaxTickets, "a ticket per stream-K prefill task");
+// The cost model, in units of one task's key-step pair (about 2.2 us on MI355X), fitted on
+// ten chunked-prefill shapes of 16-224 tasks timed both ways: one task per workgroup costs
+// P x rounds (P: key-step pairs of a task, rounds: of one task per CU); stream-K costs
+// P x tasks / G + kPfSkFixedPairs (two task starts, two partials and a ticket per share)
+// + kPfSkMergePairs x G / tasks (a task's contributors merged by the last), in tenths of
+// a pair. Stream-K is taken when it costs under 90 % of the other.
+#ifndef MSATTN_PF_SK_FIXED_TENTHS
+#define MSATTN_PF_SK_FIXED_TENTHS 100
+#endif
+#ifndef MSATTN_PF_SK_MERGE_TENTHS
+#define MSATTN_PF_SK_MERGE_TENTHS 12
+#endif
+constexpr int64_t kPfSkFixedTenths = MSATTN_PF_SK_FIXED_TENTHS;
+constexpr int64_t kPfSkMergeTenths = MSATTN_PF_SK_MERGE_TENTHS;
+#ifndef MSATTN_PF_SK_MIN_PAIRS
+#define MSATTN_PF_SK_MIN_PAIRS 4
+#endif
+constexpr int64_t kPfSkMinPairs = MSATTN_PF_SK_MIN_PAIRS;  // key-step pairs a share holds at least
+constexpr int64_t kPfSkMaxGroups = 256;  // workgroups of a stream-K prefill launch, at most
+
+// Workgroups of a stream-K prefill launch on a device of `cus` CUs for this geometry (a
+// multiple of 8 when it has at least 8, so that shares are dealt to the XCDs evenly; no
+// more than kPfSkMaxGroups; each share at least kPfSkMinPairs of the work list's key-step
+// pairs at the table capacity), or 0 where the geometry cannot take stream-K: not a
+// prefill the MFMA kernel's head sizes allow, or more tasks than tickets.
+int64_t prefill_sk_groups(int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                          int max_context, int64_t cus) {
+  if (kPfStreamK == 0 || q_len <= 1 || (head_dim != 64 && head_dim != 128)) return 0;
+  const int64_t rows = static_cast<int64_t>(q_len) * (num_heads / num_kv_heads);
+  const int64_t tasks = (rows + kPfRows - 1) / kPfRows * num_kv_heads * batch;
+  if (tasks > kPfSkMaxTasks) return 0;
+  const int64_t pairs_max = std::max<int64_t>(1, ceil_div(ceil_div(max_context, kPfStep), 2));
+  int64_t G = std::min<int64_t>(cus, kPfSkMaxGroups);
+  if (G >= kXcds) G = G / kXcds * kXcds;
+  return std::min<int64_t>(G, std::max<int64_t>(1, tasks * pairs_max / kPfSkMinPairs));
+}
+
 bool dtype_ok(int d) { return d >= MSATTN_F32 && d <= MSATTN_FP8_E4M3; }
 int dtype_bytes(int d) { return d == MSATTN_F32 ? 4 : (d == MSATTN_FP8_E4M3 ? 1 : 2); }
 bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
@@ -174,10 +218,55 @@ Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, i
       if (sk > L.slots) L.slots = sk;
     }
   }
+  // A chunked prefill on the prefill kernel's stream-K schedule keeps two partials of
+  // kPfRows rows per workgroup in the same regions: sized for the largest launch any
+  // device takes, so that a call with this workspace and the no-allocation entry point
+  // (whose scratch holds it) take the same schedule.
+  const int64_t pf_groups = prefill_sk_groups(batch, q_len, num_heads, num_kv_heads, head_dim,
+                                              max_context, kPfSkMaxGroups);
+  if (2 * pf_groups * kPfRows > L.slots) L.slots = 2 * pf_groups * kPfRows;
   L.hdr_bytes = round256(sizeof(int) * (kHdrPrefix + static_cast<size_t>(batch) + 1));
   L.ml_bytes = round256(static_cast<size_t>(L.slots) * 2 * sizeof(float));
   L.acc_bytes = static_cast<size_t>(L.slots) * head_dim * sizeof(float);
   return L;
+}
+
+// The prefill launch's schedule: stream-K over `groups` workgroups (partials at the given
+// workspace offsets), or groups = 0 for one task per workgroup. Stream-K is taken where
+// prefill_sk_groups allows it, the cost model prefers it (MSATTN_PF_STREAMK 1; 2 takes it
+// wherever it fits) and the workspace holds its partials.
+int device_cus();
+
+struct PfSkPlan {
+  int64_t groups = 0;
+  size_t ml_offset = 0;
+  size_t acc_offset = 0;
+};
+
+PfSkPlan prefill_sk_plan(int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                         int max_context, size_t workspace_bytes) {
+  PfSkPlan plan;
+  const int64_t cus = device_cus();
+  const int64_t G = prefill_sk_groups(batch, q_len, num_heads, num_kv_heads, head_dim,
+                                      max_context, cus);
+  if (G < 2) return plan;
+  const int64_t rows = static_cast<int64_t>(q_len) * (num_heads / num_kv_heads);
+  const int64_t tasks = (rows + kPfRows - 1) / kPfRows * num_kv_heads * batch;
+  const int64_t rounds = (tasks + cus - 1) / cus;
+  const int64_t P = std::max<int64_t>(1, ceil_div(ceil_div(max_context, kPfStep), 2));
+  // costs in tenths of a pair, times `tasks` (which divides the stream-K terms)
+  const int64_t one_cost = 10 * P * rounds * tasks;
+  const int64_t sk_cost = 10 * P * tasks * tasks / G + kPfSkFixedTenths * tasks +
+                          kPfSkMergeTenths * G;
+  if (kPfStreamK != 2 && 10 * sk_cost >= 9 * one_cost) return plan;
+  const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
+  const size_t ml_bytes = round256(static_cast<size_t>(2 * G * kPfRows) * 2 * sizeof(float));
+  const size_t acc_bytes = static_cast<size_t>(2 * G * kPfRows) * head_dim * sizeof(float);
+  if (workspace_bytes < L.hdr_bytes + ml_bytes + acc_bytes) return plan;
+  plan.groups = G;
+  plan.ml_offset = L.hdr_bytes;
+  plan.acc_offset = L.hdr_bytes + ml_bytes;
+  return plan;
 }
 
 // Cascade decode: the shared-prefix pass splits the prefix into npart key partitions
@@ -701,6 +790,7 @@ constexpr int64_t kPrefillSplitPct = MSATTN_PREFILL_SPLIT_PCT;
 #endif
 constexpr int64_t kPrefillSplitMaxRows = MSATTN_PREFILL_SPLIT_MAX_ROWS;
 
+
 // Whether the chunked-prefill kernel can run this call: a multi-token bf16/fp16 query
 // with more than kPrefillMinRows rows per KV head on the MFMA route's types and layouts.
 bool prefill_kernel_ok(const void* query, const void* out, int64_t cache_slot_stride,
@@ -807,6 +897,21 @@ int attention_impl(const void* query, const void* k_cache, const void* v_cache,
     const int64_t tasks = static_cast<int64_t>(pp.rblocks) * num_kv_heads * batch;
     if (tasks >= (int64_t(1) << 31) - kXcds) return MSATTN_ERR_UNSUPPORTED;
     pp.xcd_per = static_cast<int>((tasks + kXcds - 1) / kXcds);
+    // Stream-K scheduling where the cost model prefers it (prefill_sk_plan): one workgroup
+    // per CU, each taking an equal share of all tasks' key-step pairs, a task split
+    // between shares merged by its last share; a ticket per task in the workspace header
+    // and two partial slots per workgroup after it.
+    pp.sk_groups = 0;
+    const PfSkPlan sk = prefill_sk_plan(batch, q_len, num_heads, num_kv_heads, head_dim,
+                                        max_context, workspace_bytes);
+    if (sk.groups > 0) {
+      char* ws = static_cast<char*>(workspace);
+      pp.sk_groups = static_cast<int>(sk.groups);
+      pp.ntasks = static_cast<int>(tasks);
+      pp.sk_ml = reinterpret_cast<float*>(ws + sk.ml_offset);
+      pp.sk_acc = reinterpret_cast<float*>(ws + sk.acc_offset);
+      pp.tickets = reinterpret_cast<int*>(ws) + kHdrTickets;
+    }
     bool sup = false;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const hipError_t e = with_mfma_types(q_dtype, kv_dtype, [&](auto t, auto kt) {
@@ -925,7 +1030,11 @@ int msattn_paged_attention_route(const void* query, const void* out, const void*
       workspace_bytes < workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim,
                                          max_context).total())
     return MSATTN_ERR_WORKSPACE;
-  *route = r;
+  *route = r == MSATTN_ROUTE_PREFILL &&
+                   prefill_sk_plan(batch, q_len, num_heads, num_kv_heads, head_dim, max_context,
+                                   workspace_bytes).groups > 0
+               ? MSATTN_ROUTE_PREFILL_STREAMK
+               : r;
   return MSATTN_OK;
 }
 

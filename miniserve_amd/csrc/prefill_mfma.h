@@ -33,6 +33,7 @@
 #pragma once
 
 #include "decode_mfma.h"
+#include "pf_streamk.h"
 
 #ifndef MSATTN_PF_RB
 #define MSATTN_PF_RB 2
@@ -154,7 +155,57 @@ struct PrefillParams {
   float* pml;
   float* pacc;
   int key_part, npart;
+  // Stream-K mode (sk_groups > 0, prefill only): the grid is sk_groups workgroups, which
+  // take equal contiguous shares of the work list (every task's key-step pairs, tasks in
+  // order). A task split between workgroups has each share store an unnormalised partial
+  // (m, l, acc) per row at slot 2 * share + (0: the share's first task, 1: its last);
+  // the last share to take the task's ticket folds them into the output.
+  int sk_groups;
+  int ntasks;         // rblocks * KVH * batch
+  float* sk_ml;       // [2 * sk_groups][kPfRows][2]
+  float* sk_acc;      // [2 * sk_groups][kPfRows][D]
+  int* tickets;       // one per task, zero before and after every launch
 };
+
+// Largest task count of a stream-K prefill launch (its work-list prefix sums sit in LDS).
+constexpr int kPfSkMaxTasks = 2048;
+// Cache-policy operand of a buffer load / store with SC1 set (gfx950: bit 4), the bit the
+// compiler sets on agent-scope atomic loads and stores.
+constexpr int kAuxSc1 = 16;
+
+// Geometry of one prefill task (sequence b, KV head, 128-row block; not the cascade's
+// PX tasks): its rows, context and the key range [lo_all, hi_all) its rows see, and the
+// 64-key steps covering that range.
+struct PfTask {
+  int b, kvh, rblock, ctx, row0, rows_here, i_first, i_last, lo_all, hi_all;
+  int step_first, step_end;
+  __device__ int iterations() const {  // key-step pairs, at least one (rows without keys)
+    const int n = (step_end - step_first + 1) / 2;
+    return n > 0 ? n : 1;
+  }
+};
+
+template <int BROWS>
+__device__ __forceinline__ PfTask pf_task(const PrefillParams& p, unsigned task) {
+  PfTask t;
+  const unsigned per_b = static_cast<unsigned>(p.rblocks) * static_cast<unsigned>(p.KVH);
+  t.b = static_cast<int>(task / per_b);
+  const unsigned bx = task - static_cast<unsigned>(t.b) * per_b;
+  // larger (later) row blocks first: they see the most keys under a causal mask
+  t.rblock = p.rblocks - 1 - static_cast<int>(bx % static_cast<unsigned>(p.rblocks));
+  t.kvh = static_cast<int>(bx / static_cast<unsigned>(p.rblocks));
+  int ctx = p.lens[t.b];
+  t.ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
+  t.row0 = t.rblock * BROWS;
+  t.rows_here = min(BROWS, p.rows_per_kvh - t.row0);
+  t.i_first = t.row0 / p.G;
+  t.i_last = (t.row0 + t.rows_here - 1) / p.G;
+  t.lo_all = p.window > 0 ? max(0, t.ctx - p.q_len + t.i_first - p.window + 1) : 0;
+  t.hi_all = p.causal ? min(t.ctx, t.ctx - p.q_len + t.i_last + 1) : t.ctx;
+  t.step_first = t.hi_all > t.lo_all ? t.lo_all / kPfStep : 0;
+  t.step_end = t.hi_all > t.lo_all ? ceil_div(t.hi_all, kPfStep) : 0;
+  return t;
+}
 
 template <typename T, typename KT, int D, int RB, bool PX>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillParams p) {
@@ -191,17 +242,104 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int w = wg - grp * kPfWaves;  // wave within the group: its query rows
   const int g = lane >> 4;
   const int n = lane & 15;
+  // Stream-K mode: the work list is every task's key-step pairs (PfTask::iterations),
+  // tasks in order; s_skpre[t] = pairs of tasks 0 .. t - 1 (an exclusive scan over the
+  // tasks' counts, computed here from the context lengths, so the launch is capture-safe),
+  // and this workgroup's share is [r_begin, r_end) of the list.
+  __shared__ int s_skpre[PX ? 1 : kPfSkMaxTasks + 1];
+  __shared__ int s_last;
+  const bool sk = !PX && p.sk_groups > 0;
+  int r_begin = 0, r_end = 0, sk_task = 0, sk_share = 0;
+  if constexpr (!PX) {
+    if (sk) {
+      constexpr int kPer = (kPfSkMaxTasks + kPfThreads - 1) / kPfThreads;
+      int cnt[kPer];
+      int sum = 0;
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int t = tid * kPer + k;
+        cnt[k] = t < p.ntasks ? pf_task<BROWS>(p, static_cast<unsigned>(t)).iterations() : 0;
+        sum += cnt[k];
+      }
+      const int incl = wave_inclusive_sum(sum);
+      if (lane == kWave - 1) s_pg[wg] = incl;  // the page window is free before the tasks
+      __syncthreads();
+      int excl = incl - sum;
+      for (int k = 0; k < wg; ++k) excl += s_pg[k];
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int t = tid * kPer + k;
+        if (t < p.ntasks) s_skpre[t] = excl;
+        excl += cnt[k];
+      }
+      if (tid == kPfThreads - 1) s_skpre[p.ntasks] = excl;  // the list's length
+      __syncthreads();
+      const unsigned i = blockIdx.x;
+      // shares dealt to the XCDs in contiguous runs, as tasks are without stream-K
+      sk_share = (MSATTN_PF_XCD && p.sk_groups % kXcds == 0)
+                     ? static_cast<int>((i % kXcds) * static_cast<unsigned>(p.sk_groups / kXcds) +
+                                        i / kXcds)
+                     : static_cast<int>(i);
+      // (values read from LDS are the same in every lane: readfirstlane keeps them, and
+      // all the task arithmetic that follows, in scalar registers)
+      const int total = __builtin_amdgcn_readfirstlane(s_skpre[p.ntasks]);
+      // Shares: no more than the list's length, so that every share holds work (a task's
+      // contributors are then consecutive shares, each taking its ticket); workgroups
+      // past them have none.
+      pf_sk_range(sk_share, total, pf_sk_shares(p.sk_groups, total), &r_begin, &r_end);
+      int lo = 0, hi = p.ntasks;  // the task holding r_begin: s_skpre[lo] <= r_begin < s_skpre[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (__builtin_amdgcn_readfirstlane(s_skpre[mid]) <= r_begin) lo = mid;
+        else hi = mid;
+      }
+      sk_task = lo;
+    }
+  }
+
+  // One task at a time: without stream-K the workgroup's one task; with it, the tasks its
+  // share touches, each over the part [it_lo, it_hi) of its key-step pairs in the share.
+  for (int seg = 0;; ++seg) {
+  // The lane's constants are derived again in each task from an opaque copy of the thread
+  // index, so the compiler does not hoist the task's lane arithmetic out of this loop and
+  // hold it across the key loop.
+  int tid_opaque = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(tid_opaque));
+  const int tid = tid_opaque;
+  const int lane = tid & (kWave - 1);
+  const int wg = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int grp = wg / kPfWaves;
+  const int w = wg - grp * kPfWaves;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  int it_lo = 0, it_hi = 1 << 28;
+  bool full = true;  // the whole task: normalised output; else a partial
+  unsigned task = 0;
   // Task = (sequence, KV head) pair-major, then row block; larger (later) row blocks
   // first: they see the most keys under a causal mask.
   unsigned bx = blockIdx.x;
   int b = 0;
   if constexpr (!PX) {
-    const unsigned i = blockIdx.x;
-    const unsigned task = MSATTN_PF_XCD ? (i % kXcds) * static_cast<unsigned>(p.xcd_per) + i / kXcds : i;
     const unsigned per_b = static_cast<unsigned>(p.rblocks) * static_cast<unsigned>(p.KVH);
-    if (task >= per_b * static_cast<unsigned>(p.batch)) return;  // the grid's tail
+    if (sk) {
+      if (sk_task >= p.ntasks || r_begin >= r_end) break;
+      const int p0 = __builtin_amdgcn_readfirstlane(s_skpre[sk_task]);
+      const int p1 = __builtin_amdgcn_readfirstlane(s_skpre[sk_task + 1]);
+      if (p0 >= r_end) break;
+      it_lo = r_begin > p0 ? r_begin - p0 : 0;
+      it_hi = (r_end < p1 ? r_end : p1) - p0;
+      full = it_lo == 0 && it_hi == p1 - p0;
+      task = static_cast<unsigned>(sk_task++);
+    } else {
+      if (seg > 0) break;
+      const unsigned i = blockIdx.x;
+      task = MSATTN_PF_XCD ? (i % kXcds) * static_cast<unsigned>(p.xcd_per) + i / kXcds : i;
+      if (task >= per_b * static_cast<unsigned>(p.batch)) break;  // the grid's tail
+    }
     b = static_cast<int>(task / per_b);
     bx = task - static_cast<unsigned>(b) * per_b;
+  } else {
+    if (seg > 0) break;
   }
   const int rblock = p.rblocks - 1 - static_cast<int>(bx % static_cast<unsigned>(p.rblocks));
   const int kvh = static_cast<int>(bx / static_cast<unsigned>(p.rblocks));
@@ -298,8 +436,13 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
 
   const KT* kbase = static_cast<const KT*>(p.k);
   const KT* vbase = static_cast<const KT*>(p.v);
-  const int step_first = hi_all > lo_all ? lo_all / kPfStep : 0;
-  const int step_end = hi_all > lo_all ? ceil_div(hi_all, kPfStep) : 0;
+  // The task's steps (pf_task's rule), then this share's part of them: pairs it_lo ..
+  // it_hi - 1 (group 0 takes the pair's first step, group 1 its second, as without
+  // stream-K).
+  const int step_first0 = hi_all > lo_all ? lo_all / kPfStep : 0;
+  const int step_end0 = hi_all > lo_all ? ceil_div(hi_all, kPfStep) : 0;
+  const int step_first = step_first0 + 2 * it_lo;
+  const int step_end = min(step_end0, step_first0 + 2 * it_hi);
 
   int pg_base = -(1 << 30);  // s_pg[i] = physical page of logical page pg_base + i
   auto page_of = [&](int tok) { return p.bs_shift >= 0 ? tok >> p.bs_shift : tok / p.bs; };
@@ -904,6 +1047,26 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
         }
         continue;
       }
+      if (!full) {  // stream-K share of a split task: its unnormalised partial, device scope
+        if (row_ok[rb]) {
+          const int rs = (2 * sk_share + (seg == 0 ? 0 : 1)) * kPfRows + (w * WROWS + rb * 16 + n);
+          if (g == 0) store2_device(p.sk_ml + static_cast<int64_t>(rs) * 2, M, l);
+          // 16-byte stores with cache policy SC1 (written through to the memory every XCD
+          // reads, as the agent-scope atomic stores are; half their transactions)
+          const __amdgpu_buffer_rsrc_t racc = tile_rsrc(p.sk_acc, 2 * p.sk_groups * kPfRows * D * 4);
+#pragma unroll
+          for (int t = 0; t < ND; ++t) {
+            const float4 o1 = s_acc[(w * ND + t) * kWave + lane];
+            const mf_u32x4 v = {__float_as_uint(acc[rb][t][0] * a0 + o1.x * a1),
+                                __float_as_uint(acc[rb][t][1] * a0 + o1.y * a1),
+                                __float_as_uint(acc[rb][t][2] * a0 + o1.z * a1),
+                                __float_as_uint(acc[rb][t][3] * a0 + o1.w * a1)};
+            __builtin_amdgcn_raw_buffer_store_b128(v, racc, (rs * D + 16 * t + 4 * g) * 4, 0,
+                                                   kAuxSc1);
+          }
+        }
+        continue;
+      }
       if (row_ok[rb]) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         T* op = static_cast<T*>(p.out) + out_row(rb) * D;
@@ -920,13 +1083,88 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       }
     }
   }
+  if constexpr (!PX) {
+    if (!full) {
+      // The share's partial is stored through to the memory every XCD reads (agent-scope
+      // stores, SC1) and acknowledged (s_waitcnt) in every thread before the barrier; then
+      // the task's ticket. The last of its shares to arrive reads every share's partial
+      // with agent-scope loads (after a barrier that follows the ticket's return), folds
+      // them (log-sum-exp, base 2) into the normalised output, and leaves the ticket at
+      // zero. The ordering argument is the partition decode's in-kernel merge's.
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+      const int p0 = __builtin_amdgcn_readfirstlane(s_skpre[task]);
+      const int p1 = __builtin_amdgcn_readfirstlane(s_skpre[task + 1]);
+      const int total = __builtin_amdgcn_readfirstlane(s_skpre[p.ntasks]);
+      const int G = pf_sk_shares(p.sk_groups, total);
+      const int l_lo = pf_sk_owner(p0, total, G), l_hi = pf_sk_owner(p1 - 1, total, G);
+      if (tid == 0) {
+        int* t = p.tickets + task;
+        const int old = __hip_atomic_fetch_add(t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == l_hi - l_lo;
+        if (last) __hip_atomic_store(t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+      }
+      __syncthreads();
+      if (s_last) {
+        constexpr int DPT = D / 4;  // dims per thread: 4 threads a row, 128 rows
+        static_assert(kPfThreads == 4 * kPfRows, "four threads per row of the task block");
+        const int r = tid >> 2;
+        const int d0 = (tid & 3) * DPT;
+        if (r < rows_here) {
+          float M = -INFINITY, L = 0.0f;
+          float a[DPT];
+#pragma unroll
+          for (int k = 0; k < DPT; ++k) a[k] = 0.0f;
+          // each contributor's (m, l) and acc slice requested together (one round trip per
+          // contributor), with agent-scope loads: SC1, which do not take a line from this
+          // XCD's L2 or this CU's L1
+          const __amdgpu_buffer_rsrc_t racc = tile_rsrc(p.sk_acc, 2 * p.sk_groups * kPfRows * D * 4);
+          for (int l = l_lo; l <= l_hi; ++l) {
+            const int rs = pf_sk_partial_slot(l, p0, total, G) * kPfRows + r;
+            const float2 ml = load2_device(p.sk_ml + static_cast<int64_t>(rs) * 2);
+            mf_u32x4 v[DPT / 4];
+#pragma unroll
+            for (int k = 0; k < DPT / 4; ++k)
+              v[k] = __builtin_amdgcn_raw_buffer_load_b128(racc, (rs * D + d0 + 4 * k) * 4, 0,
+                                                          kAuxSc1);
+            if (ml.x == -INFINITY) continue;  // no key of this row in that share
+            const float Mn = fmaxf(M, ml.x);
+            const float alpha = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M = -inf
+            const float beta = __builtin_amdgcn_exp2f(ml.x - Mn);
+            L = L * alpha + ml.y * beta;
+#pragma unroll
+            for (int k = 0; k < DPT / 4; ++k) {
+              a[4 * k] = a[4 * k] * alpha + __uint_as_float(v[k].x) * beta;
+              a[4 * k + 1] = a[4 * k + 1] * alpha + __uint_as_float(v[k].y) * beta;
+              a[4 * k + 2] = a[4 * k + 2] * alpha + __uint_as_float(v[k].z) * beta;
+              a[4 * k + 3] = a[4 * k + 3] * alpha + __uint_as_float(v[k].w) * beta;
+            }
+            M = Mn;
+          }
+          const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+          const int row = row0 + r;
+          const int i = row / p.G;
+          const int64_t orow =
+              (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
+          T* op = static_cast<T*>(p.out) + orow * D + d0;
+#pragma unroll
+          for (int k = 0; k < DPT; k += 4)
+            *reinterpret_cast<uint2*>(op + k) = make_uint2(Pack2<T>::pack(a[k] * inv, a[k + 1] * inv),
+                                                           Pack2<T>::pack(a[k + 2] * inv, a[k + 3] * inv));
+        }
+      }
+    }
+  }
+  __syncthreads();  // this task's LDS reads are done before the next task's copies
+  }  // task loop
 }
 template <typename T, typename KT>
 hipError_t launch_prefill_mfma_impl(const PrefillParams& p, int D, hipStream_t stream,
                                     bool* supported) {
   *supported = D == 64 || D == 128;
   if (!*supported) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>(kXcds * p.xcd_per));
+  const dim3 grid(static_cast<unsigned>(p.sk_groups > 0 ? p.sk_groups : kXcds * p.xcd_per));
   if (D == 128)
     hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 128, kPfRB, false>), grid, dim3(kPfThreads), 0,
                        stream, p);

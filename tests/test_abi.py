@@ -250,9 +250,13 @@ def route(B, q_len, H, KVH, D, ctx, qd=nat.BF16, kvd=None, ws=None, slot_stride=
     ((2, 512, 28, 4, 128, 4608), nat.ROUTE_PREFILL),           # C5 prefill
     ((8, 4, 28, 4, 128, 8192), nat.ROUTE_PARTITION_FUSED),     # speculative: 28 rows, 32 pairs
     ((64, 6, 32, 8, 128, 8192), nat.ROUTE_PREFILL),            # 24 rows over 512 pairs
-    ((1, 512, 8, 1, 128, 8192), nat.ROUTE_PREFILL),            # 4096 rows: never re-streamed
+    ((1, 512, 8, 1, 128, 8192), nat.ROUTE_PREFILL_STREAMK),    # 4096 rows: 32 tasks, stream-K
     ((4, 16, 32, 8, 128, 8192), nat.ROUTE_PARTITION_FUSED),    # 64 rows: the measured limit
-    ((4, 17, 32, 8, 128, 8192), nat.ROUTE_PREFILL),            # 68 rows: past it
+    ((4, 17, 32, 8, 128, 8192), nat.ROUTE_PREFILL_STREAMK),    # 68 rows: past it (32 tasks)
+    # prefill tasks scheduled stream-K where one task per CU leaves CUs idle long enough
+    ((1, 128, 32, 8, 128, 8192), nat.ROUTE_PREFILL_STREAMK),   # 32 tasks of 64 key-step pairs
+    ((2, 384, 32, 8, 128, 4096), nat.ROUTE_PREFILL),           # 192 tasks: one round
+    ((4, 128, 32, 8, 128, 2048), nat.ROUTE_PREFILL),           # 128 tasks of 16 pairs
     # stream-K thresholds: 2^16 table tiles at head_dim 128, 2^17 at head_dim 64
     ((64, 1, 32, 8, 128, 8158), nat.ROUTE_STREAMK),            # C3 called with max(lens)
     ((16, 1, 32, 8, 128, 8192), nat.ROUTE_STREAMK),            # 65,536 tiles
@@ -264,7 +268,8 @@ def test_route_policy(shape, want):
     """The routing rules in csrc/abi.hip: stream-K from 2^16 table tiles at head_dim 128
     (2^17 at head_dim 64), the partition kernel (merging in-kernel) below; chunked prefill
     on the prefill kernel unless at most 64 rows per KV head over too few (sequence, KV
-    head) pairs to fill the device."""
+    head) pairs to fill the device, stream-K scheduled where the cost model prefers it
+    (sizes from the measured prefill sweep)."""
     st, r = route(*shape)
     assert st == nat.OK and r == want, (nat.ROUTE_NAMES.get(r), shape)
 
@@ -291,10 +296,12 @@ def test_noalloc_route_falls_back_to_the_prefill_kernel():
     assert lib.msattn_workspace_bytes(B, q_len, H, KVH, D, ctx) > nat.NOALLOC_SCRATCH_BYTES
     assert route(B, q_len, H, KVH, D, ctx) == (nat.OK, nat.ROUTE_PARTITION_FUSED)
     assert route(B, q_len, H, KVH, D, ctx, ws=nat.NOALLOC_SCRATCH_BYTES) == \
-        (nat.OK, nat.ROUTE_PREFILL)
-    # the advisor's case: a 64-token chunk over a 131072-token table
+        (nat.OK, nat.ROUTE_PREFILL_STREAMK)
+    # a 64-token chunk over a 131072-token table
     assert route(1, 64, 28, 4, 128, 131072, ws=nat.NOALLOC_SCRATCH_BYTES) == \
-        (nat.OK, nat.ROUTE_PREFILL)
+        (nat.OK, nat.ROUTE_PREFILL_STREAMK)
+    # a workspace too small for the stream-K partials: one task per workgroup
+    assert route(1, 64, 28, 4, 128, 131072, ws=4096) == (nat.OK, nat.ROUTE_PREFILL)
     # an fp32 query has no prefill kernel: past the scratch it is refused
     assert route(B, q_len, H, KVH, D, ctx, qd=nat.F32, ws=nat.NOALLOC_SCRATCH_BYTES)[0] == \
         nat.ERR_WORKSPACE

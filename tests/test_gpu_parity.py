@@ -69,10 +69,10 @@ def run_hip(device, q, kc, vc, table, lens, **kw):
 
 # Workspace header word 0 after a call: the layout the partials kernel recorded (0 the
 # partition kernels, 1 stream-K, 2 the partition kernel merging in-kernel); the prefill
-# kernel leaves the workspace untouched.
+# kernel leaves it untouched (its stream-K schedule uses only the tickets and partials).
 _SENTINEL = 0x5EED
-_KIND_OF_ROUTE = {"prefill": _SENTINEL, "partition-fused": 2, "partition": 0, "generic": 0,
-                  "stream-K": 1}
+_KIND_OF_ROUTE = {"prefill": _SENTINEL, "prefill stream-K": _SENTINEL, "partition-fused": 2,
+                  "partition": 0, "generic": 0, "stream-K": 1}
 
 
 def run_routed(device, want, q, kc, vc, table, lens, **kw):
@@ -894,7 +894,7 @@ def test_streamk_graph_replays(device):
 @pytest.mark.parametrize("H,KVH,D,q_len,lens,dtype,causal,window,route", [
     (28, 4, 128, 512, [4608, 4608], torch.bfloat16, True, None, "prefill"),   # C5 prefill shape
     (28, 4, 128, 100, [100, 1000, 357], torch.bfloat16, True, None, "prefill"),
-    (32, 8, 128, 17, [17, 40, 3000], torch.bfloat16, True, None, "prefill"),  # 68 rows
+    (32, 8, 128, 17, [17, 40, 3000], torch.bfloat16, True, None, "prefill stream-K"),  # 68 rows
     (32, 8, 128, 64, [64, 700], torch.float16, True, None, "prefill"),
     (8, 8, 128, 80, [80, 150], torch.bfloat16, False, None, "prefill"),       # non-causal
     (28, 4, 128, 200, [1200, 300], torch.bfloat16, True, 128, "prefill"),     # sliding window
@@ -926,6 +926,58 @@ def test_prefill_mfma(device, H, KVH, D, q_len, lens, dtype, causal, window, rou
     for b, L in enumerate(lens):
         if causal and L < q_len:
             assert not out[b, : q_len - L].any()
+
+
+_SK = "prefill stream-K"
+
+
+@pytest.mark.parametrize("B,H,KVH,D,q_len,lo,hi,dtype,kv_dtype,want", [
+    # 16 tasks of ~94 key-step pairs over 256 workgroups: every task split over ~16 shares
+    (1, 8, 8, 128, 200, 12000, 12000, torch.bfloat16, torch.bfloat16, _SK),
+    # 96 tasks: ~2.7 shares each
+    (2, 32, 8, 128, 192, 6000, 6144, torch.bfloat16, torch.bfloat16, _SK),
+    # 300 tasks (two rounds of 256 otherwise): shares of 1.2 tasks, spanning two
+    (75, 4, 4, 64, 32, 500, 4000, torch.bfloat16, torch.bfloat16, _SK),
+    # head_dim 64, fp16, and fp8 and fp32 caches (register staging) in stream-K mode
+    (2, 14, 2, 64, 200, 200, 5000, torch.float16, torch.float16, _SK),
+    (3, 32, 8, 128, 100, 100, 6000, torch.bfloat16, torch.float8_e4m3fn, _SK),
+    (2, 28, 4, 128, 160, 160, 7000, torch.bfloat16, torch.float32, _SK),
+    # 256 short tasks: one per workgroup (the cost model keeps stream-K off)
+    (16, 32, 8, 128, 64, 64, 1000, torch.bfloat16, torch.bfloat16, "prefill"),
+])
+def test_prefill_stream_k_schedule(device, B, H, KVH, D, q_len, lo, hi, dtype, kv_dtype,
+                                   want):
+    """The prefill kernel's stream-K schedule (one workgroup per CU, each an equal share of
+    all tasks' key-step pairs; a task split between shares merged in-kernel by the last to
+    take its ticket), which the cost model picks for launches that would leave CUs idle,
+    against the float64 oracle: tasks over many shares, shares over two tasks, the staged
+    (fp8) path, and a launch of one task per CU (no stream-K); three calls in a row on one
+    workspace (the tickets must come back to zero)."""
+    g = torch.Generator().manual_seed(B * q_len + H)
+    lens = [int(x) for x in torch.randint(lo, hi + 1, (B,), generator=g)]
+    lens = [max(L, q_len) for L in lens]
+    width = (max(lens) + 15) // 16 + 1
+    ws = None
+    for call in range(3):
+        note(f"prefill stream-K B={B} H={H}/{KVH} D={D} q_len={q_len} lens={lens[:6]} "
+             f"{dtype}/{kv_dtype} call {call}")
+        q, kc, vc, table = paged_case(H, KVH, D, lens, dtype, 16, width, seed=call + q_len,
+                                      q_len=q_len)
+        kc, vc = kc.to(kv_dtype), vc.to(kv_dtype)
+        qd = q.to(device)
+        assert kernel_route(qd, kc.to(device), table) == want
+        if ws is None:
+            nbytes = nat.lib().msattn_workspace_bytes(B, q_len, H, KVH, D, width * 16)
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        out = paged_attention(qd, kc.to(device), vc.to(device), table, lens,
+                              max_context=width * 16, workspace=ws)
+        torch.cuda.synchronize()
+        assert not ws[:(64 + 4096) * 4].view(torch.int32)[64:].any(), "tickets not back at zero"
+        ref = dense.paged_attention_f64(q, kc, vc, table, lens, kv_cast=True)
+        err = rel_err(out, ref)
+        note(f"stream-K prefill max-rel {err:.3e}")
+        assert err < BF16_REL
+        lens = [max(q_len, L - 7 * (call + 1)) for L in lens]
 
 
 def paged_case(H, KVH, D, lens, dtype, bs, width_pages, seed, q_len=1):

@@ -125,8 +125,8 @@ def test_noalloc_refuses_geometry_past_scratch(device):
 def test_noalloc_long_table_prefill_takes_the_prefill_kernel(device):
     """A short chunked prefill over a long-capacity table (131072 tokens): the workspace
     entry runs it on the partition kernel, whose layout at that capacity exceeds the
-    scratch; the no-allocation entry runs it on the prefill kernel (which needs none)
-    instead of refusing it. Both within the oracle's bar, and within two output ulps of
+    scratch; the no-allocation entry runs it on the prefill kernel (whose stream-K
+    tickets and partials fit the scratch) instead of refusing it. Both within the oracle's bar, and within two output ulps of
     each other (different kernels sum in different orders); two calls in a row, the
     second smaller."""
     H, KVH, D, q_len, width = 32, 8, 128, 8, 8192
@@ -136,7 +136,7 @@ def test_noalloc_long_table_prefill_takes_the_prefill_kernel(device):
         q, kc, vc, table = make(H, KVH, D, lens, q_len, torch.bfloat16, width, seed=31 + i)
         qd, kcd, td = q.to(device), kc.to(device), table.to(device)
         assert kernel_route(qd, kcd, td) == "partition-fused"
-        assert kernel_route(qd, kcd, td, workspace_bytes=SCRATCH) == "prefill"
+        assert kernel_route(qd, kcd, td, workspace_bytes=SCRATCH) == "prefill stream-K"
         out_ws, out_na = call_both(device, q, kc, vc, table, lens, width * 16)
         check_oracle(out_ws, q, kc, vc, table, lens)
         check_oracle(out_na, q, kc, vc, table, lens)
