@@ -79,9 +79,16 @@ constexpr int kXcds = 8;
 #ifndef MSATTN_PF_PRIO
 #define MSATTN_PF_PRIO 1
 #endif
-constexpr float kPfRescaleSlack = 8.0f;
+constexpr float kPfRescaleSlack = 8.0f;  // base-2 headroom before the max moves
+constexpr float kPfSumBound = 256.0f;      // 2^kPfRescaleSlack
+// l's increment as the sum of the rounded weights (v_dot2), which is also the fast path's
+// test for a weight over the bound (no per-score max); 0: fp32 sum and a per-lane max.
+#ifndef MSATTN_PF_SUM_CHECK
+#define MSATTN_PF_SUM_CHECK 1
+#endif
+constexpr bool kPfSumCheck = MSATTN_PF_SUM_CHECK != 0;
 // s_waitcnt immediate (gfx9 encoding) waiting for every vector memory operation only.
-constexpr int kWaitVm0 = 0x0F70;         // base-2 headroom before the max moves
+constexpr int kWaitVm0 = 0x0F70;
 
 typedef short pf_s4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) pf_s4 lds_s4;  // an LDS pointer target
@@ -513,47 +520,66 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   };
   // Online softmax of one row block over one half-step (32 keys, slices 2 ks, 2 ks + 1).
   // The weights are exp2(s * scale_log2 - m) for the row's running max m (base 2; the row
-  // max is taken on raw scores, scale_log2 > 0 keeps the order). m only moves when a row's
-  // max exceeds it by more than kPfRescaleSlack: the weights then stay below
-  // 2^kPfRescaleSlack, which fp32 sums and the bf16/fp16 P operand hold, and the
-  // normalisation by l is exact whatever reference max the sums share.
-  // Fast path (almost every half-step): each lane tests its own scores against m +
-  // kPfRescaleSlack (max over lanes and the positive scale commute, so no lane over means
-  // no row over) and the weights are taken with the current m, with no cross-lane
-  // reduction. When any lane is over, softmax_redo moves m (the row max over the 4 lane
-  // groups), rescales l and acc, and takes the weights again.
+  // max is taken on raw scores, scale_log2 > 0 keeps the order). m moves only when some
+  // weight would exceed 2^kPfRescaleSlack: the weights stay within what fp32 sums and the
+  // bf16/fp16 P operand hold, and the normalisation by l is exact whatever reference max
+  // the sums share.
+  // Fast path (almost every half-step): the weights are taken with the current m, with no
+  // cross-lane reduction, and l's increment is the sum of the rounded weights the P.V
+  // MFMAs take (v_dot2 of each packed pair with (1, 1)). Every weight is at most that
+  // sum, so a lane whose sum is within 2^kPfRescaleSlack holds no weight over it: the
+  // sum is the test, and the scores' max is taken only on the slow path. A row whose m
+  // is still -inf (no key seen yet) takes the slow path too. softmax_redo moves m to the
+  // row max (over the 4 lane groups) when it is above m, rescales l and acc, and takes
+  // the weights again. (MSATTN_PF_SUM_CHECK=0: each lane tests its scores' max against
+  // m + kPfRescaleSlack instead, l's increment summed in fp32 before rounding.)
   uint4 pb[RB][2];
   float psum[RB];
   float lmax[RB];
   auto softmax_exp = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) __attribute__((always_inline)) {
     const float m_use = m_run[rb] != -INFINITY ? m_run[rb] : 0.0f;
     float pr[8];
-    psum[rb] = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < 4; ++r)
         pr[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(sv[rb][2 * ks + h][r], p.scale_log2, -m_use));
-        psum[rb] += pr[4 * h + r];
-      }
     pb[rb][ks] = make_uint4(Pack2<T>::pack(pr[0], pr[1]), Pack2<T>::pack(pr[2], pr[3]),
                             Pack2<T>::pack(pr[4], pr[5]), Pack2<T>::pack(pr[6], pr[7]));
+    if constexpr (kPfSumCheck) {
+      const uint32_t one2 = Pack2<T>::pack(1.0f, 1.0f);
+      const uint4 w = pb[rb][ks];
+      psum[rb] = Dot2<T>::dot(w.w, one2, Dot2<T>::dot(w.z, one2, Dot2<T>::dot(w.y, one2,
+                 Dot2<T>::dot(w.x, one2, 0.0f))));
+    } else {
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += pr[i];
+      psum[rb] = s;
+    }
   };
-  // The lane's max and whether it is over the bound, then the weights with the current m.
-  auto softmax_fast = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) __attribute__((always_inline)) {
+  // The lane's scores' max over the half-step.
+  auto lane_max = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) __attribute__((always_inline)) {
     float lm = -INFINITY;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) lm = fmaxf(lm, sv[rb][2 * ks + h][r]);
-    lmax[rb] = lm;
+    return lm;
+  };
+  // The weights with the current m (and, without the sum test, the lane's max).
+  auto softmax_fast = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) __attribute__((always_inline)) {
+    if constexpr (!kPfSumCheck) lmax[rb] = lane_max(sv, rb, ks);
     softmax_exp(sv, rb, ks);
   };
   auto over_bound = [&]() __attribute__((always_inline)) {
     bool over = false;
     static_for<RB>([&](auto rc) {
       constexpr int rb = decltype(rc)::value;
-      over |= lmax[rb] * p.scale_log2 > m_run[rb] + kPfRescaleSlack;
+      if constexpr (kPfSumCheck)
+        over |= psum[rb] > kPfSumBound || m_run[rb] == -INFINITY;
+      else
+        over |= lmax[rb] * p.scale_log2 > m_run[rb] + kPfRescaleSlack;
     });
     return __any(over);
   };
@@ -562,8 +588,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     // (static_for: every array index stays a constant, the arrays stay in registers)
     static_for<RB>([&](auto rc) {
       constexpr int rb = decltype(rc)::value;
+      if constexpr (kPfSumCheck) lmax[rb] = lane_max(sv, rb, ks);
       const float mt = rows4_max(lmax[rb]) * p.scale_log2;  // the row max, base-2 units
-      const float m_new = mt > m_run[rb] + kPfRescaleSlack ? mt : m_run[rb];
+      const float m_new = mt > m_run[rb] + (kPfSumCheck ? 0.0f : kPfRescaleSlack) ? mt : m_run[rb];
       const float alpha = m_new != -INFINITY ? __builtin_amdgcn_exp2f(m_run[rb] - m_new) : 1.0f;
       l_run[rb] *= alpha;
       m_run[rb] = m_new;
