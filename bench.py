@@ -381,27 +381,8 @@ def main():
 
     read_ceiling = stream_read_gbs(dev)
 
-    # HBM traffic per launch of the dominant kernel comes from rocprofv3 counter runs
-    # (FETCH_SIZE, WRITE_SIZE) recorded in profiles/; it is reported only when that record
-    # was taken on the library this run loaded (same sha256), else null with the reason.
-    traffic, traffic_note = None, None
-    tname = (f"traffic_{w.name}{'' if args.kv_dtype == 'same' else '-' + args.kv_dtype}"
-             f"{'' if args.q_dtype == 'same' else '-q' + args.q_dtype}.json")
-    tfile = PROFILES / tname
+    traffic, traffic_note = traffic_record(w.name, args)
     lib_sha = library_sha256()
-    if tfile.exists():
-        try:
-            rec = json.loads(tfile.read_text())
-        except (ValueError, OSError):
-            rec = {}
-        if rec.get("library_sha256") == lib_sha:
-            traffic = rec.get("hbm_bytes_per_launch")
-            traffic_note = f"profiles/{tname}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this library"
-        else:
-            traffic_note = (f"profiles/{tname} was measured on library "
-                            f"{rec.get('library_sha256')}, not on this one ({lib_sha})")
-    else:
-        traffic_note = f"no profiles/{tname} for this workload"
 
     result = {
         "metric": METRIC,
@@ -545,6 +526,7 @@ def prefill_bench(args):
     fp32 = w.query.dtype == torch.float32
     # MI355X dense matrix peaks: bf16 2.5 PFLOP/s, fp32 157.3 TFLOP/s.
     peak = 157.3 if fp32 else 2500.0
+    traffic, traffic_note = traffic_record(w.name, args)
     kernel = {"prefill": "msattn::prefill_mfma_kernel",
               "prefill stream-K": "msattn::prefill_mfma_kernel (stream-K schedule)",
               "partition-fused": "msattn::decode_mfma_kernel (16-row tiles, merged in-kernel)"
@@ -565,7 +547,8 @@ def prefill_bench(args):
                    "us_per_step_one_per_graph": round(ms_single * 1e3, 2)},
         "roofline": {"kernel": kernel, "bound": "mfma",
                      "achieved": round(k_tflops, 1), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(k_tflops / peak, 4), "traffic": None,
+                     "frac": round(k_tflops / peak, 4), "traffic": traffic,
+                     "traffic_source": traffic_note,
                      "kernel_avg_us": round(k_avg * 1e3, 2),
                      "kernel_median_us": round(k_ms[len(k_ms) // 2] * 1e3, 2),
                      "kernel_min_us": round(k_ms[0] * 1e3, 2),
@@ -618,6 +601,28 @@ def reference_forward_us(w, table, lens, T) -> dict:
     return {"us": round(start.elapsed_time(stop) / n * 1e3, 1),
             "what": "the reference's forward (block-table gather, GQA expand, masked SDPA) "
                     "restated in torch, eager, on this GPU"}
+
+
+def traffic_record(workload: str, args):
+    """HBM bytes per launch of the dominant kernel from rocprofv3 counter runs (FETCH_SIZE,
+    WRITE_SIZE) recorded in profiles/traffic_<workload>[-<kv dtype>][-q<q dtype>].json,
+    reported only when the record was taken on the library this run loaded (same sha256);
+    else None, with the reason."""
+    tname = (f"traffic_{workload}{'' if args.kv_dtype == 'same' else '-' + args.kv_dtype}"
+             f"{'' if args.q_dtype == 'same' else '-q' + args.q_dtype}.json")
+    tfile = PROFILES / tname
+    lib_sha = library_sha256()
+    if not tfile.exists():
+        return None, f"no profiles/{tname} for this workload"
+    try:
+        rec = json.loads(tfile.read_text())
+    except (ValueError, OSError):
+        rec = {}
+    if rec.get("library_sha256") == lib_sha:
+        return (rec.get("hbm_bytes_per_launch"),
+                f"profiles/{tname}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this library")
+    return None, (f"profiles/{tname} was measured on library {rec.get('library_sha256')}, "
+                  f"not on this one ({lib_sha})")
 
 
 def library_sha256() -> str:
