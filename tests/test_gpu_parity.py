@@ -1170,6 +1170,50 @@ def test_cascade_graph_replays(device):
         assert torch.equal(replayed, eager), f"replay {rep}"
 
 
+def test_prefill_stream_k_graph_replays(device):
+    """A chunked prefill on the stream-K schedule (32 tasks over a 16,384-token table)
+    captured in a hipGraph: replays with new context lengths each time match eager calls
+    bit for bit (the tickets come back to zero between replays, and the fold order is the
+    shares' order whichever share arrives last)."""
+    note("prefill stream-K graph")
+    H, KVH, D, q_len, width = 32, 8, 128, 128, 1024
+    cap = width * 16
+    lens = [cap]
+    q, kc, vc, table = paged_case(H, KVH, D, lens, torch.bfloat16, 16, width, seed=77,
+                                  q_len=q_len)
+    kc, vc = kc.to(device), vc.to(device)
+    sq = q.to(device)
+    stable = table.to(device=device, dtype=torch.int32)
+    assert kernel_route(sq, kc, stable, max_context=cap) == "prefill stream-K"
+    slens = torch.tensor(lens, dtype=torch.int32, device=device)
+    nbytes = nat.lib().msattn_workspace_bytes(1, q_len, H, KVH, D, cap)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    out = torch.empty_like(sq)
+
+    def step():
+        paged_attention(sq, kc, vc, stable, slens, max_context=cap, workspace=ws, out=out)
+
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream(device).wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    g = torch.Generator().manual_seed(78)
+    for rep in range(4):
+        new = [int(torch.randint(q_len, cap + 1, (1,), generator=g))]
+        slens.copy_(torch.tensor(new, dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        assert not ws[:(64 + 4096) * 4].view(torch.int32)[64:].any(), "tickets not back at zero"
+        eager = paged_attention(sq, kc, vc, stable, new, max_context=cap)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay {rep}: lens {new}"
+
+
 # ------------------------------------------------------------------ benchmark configs
 
 @pytest.fixture(scope="module")
