@@ -281,6 +281,31 @@ int msattn_write_kv(void* k_cache, void* v_cache, int64_t cache_block_stride,
                     void* stream);
 
 /*
+ * Decode with the new token appended: msattn_write_kv of k_new / v_new at position
+ * context_lens[b] - 1 of each row (rows with context_lens[b] <= 0 write nothing; holes
+ * are skipped), followed by msattn_paged_attention (q_len 1, causal) over context_lens.
+ * k_new / v_new are contiguous [batch, 1, num_kv_heads, head_dim] in the query dtype,
+ * the token each row appends this step; context_lens already count it. Where the call
+ * takes the partition kernel merging in-kernel (MSATTN_ROUTE_PARTITION_FUSED) with a
+ * bf16/fp16 query, at most 8 query rows per KV head and k_new and v_new 16-byte aligned,
+ * both run in that one launch: the workgroup whose partition holds the new
+ * position writes the rows (cast to the cache type as msattn_write_kv casts them) and
+ * uses the same values in place of the cache's row, so the output and the caches equal
+ * those of the two calls bit for bit. Other routes run the two calls. No reference
+ * counterpart as one call: the reference runner makes these two calls per layer
+ * (miniserve/model_runner.py:70-76, attention.py:111-133 and 205-250); this entry
+ * point is for callers, such as a bucketed decode graph, that want one launch per layer.
+ */
+int msattn_paged_attention_append(const void* query, const void* k_new, const void* v_new,
+                                  void* k_cache, void* v_cache, int64_t cache_block_stride,
+                                  int64_t cache_slot_stride, int64_t cache_head_stride,
+                                  const int32_t* block_table, const int32_t* context_lens,
+                                  void* out, void* workspace, size_t workspace_bytes, int batch,
+                                  int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                  int num_blocks, int table_width, int max_context, int window,
+                                  float scale, int q_dtype, int kv_dtype, void* stream);
+
+/*
  * Block-table gather: out[b, p] = cache[table[b, p / block_size], p % block_size]
  * for p < context_lens[b]; positions p >= context_lens[b] read page 0 (as the
  * reference does), holes give zero rows. out is [batch, max_context,

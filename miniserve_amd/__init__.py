@@ -4,6 +4,8 @@
 and runs on hand-written gfx950 HIP kernels (libmsattn.so, C ABI in
 include/msattn.h).
 """
-from .attention import PagedAttention, apply_rope, gather_kv, kernel_route, paged_attention
+from .attention import (PagedAttention, apply_rope, gather_kv, kernel_route, paged_attention,
+                        paged_attention_append)
 
-__all__ = ["PagedAttention", "apply_rope", "gather_kv", "kernel_route", "paged_attention"]
+__all__ = ["PagedAttention", "apply_rope", "gather_kv", "kernel_route", "paged_attention",
+           "paged_attention_append"]

@@ -70,6 +70,10 @@ SIGNATURES = {
     "msattn_write_kv": (c_int, [
         c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp,
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    "msattn_paged_attention_append": (c_int, [
+        c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_size,
+        c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+        c_float, c_int, c_int, c_vp]),
     "msattn_gather_kv": (c_int, [
         c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp,
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),

@@ -439,6 +439,78 @@ def paged_attention(query: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     return out
 
 
+def paged_attention_append(query: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                           k_cache: torch.Tensor, v_cache: torch.Tensor, block_table,
+                           context_lens, *, window: int | None = None,
+                           scale: float | None = None, max_context: int | None = None,
+                           workspace: torch.Tensor | None = None,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode step with the new token appended: ``write_kv`` of k_new / v_new
+    ([batch, 1, kv_heads, head_dim], the query's dtype) at position context_lens[b] - 1
+    of each row, then the causal decode over ``context_lens`` (which count the new
+    token), as msattn_paged_attention_append. Rows with context_lens[b] <= 0 write
+    nothing. On the partition kernel (small decodes, bf16/fp16 query, at most 8 query rows
+    per KV head) both happen in one launch; the caches and the output equal those of
+    ``write_kv`` followed by ``paged_attention`` bit for bit.
+    """
+    _require_gpu(query, "query")
+    _require_gpu(k_cache, "k_cache")
+    _require_gpu(v_cache, "v_cache")
+    if query.ndim != 4 or query.shape[1] != 1:
+        raise ValueError("query must be [batch, 1, heads, head_dim] (decode)")
+    if k_cache.ndim != 4 or k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype \
+            or k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share a [num_blocks, block_size, kv_heads, "
+                         "head_dim] shape, dtype and strides")
+    B, _, H, D = query.shape
+    nb, bs, KVH, Dk = k_cache.shape
+    if Dk != D or H % KVH:
+        raise ValueError("head_dim and kv_heads must match the query")
+    if D > nat.MAX_HEAD_DIM or D % 2:
+        raise ValueError(f"head_dim {D}: the kernels take even head sizes up to "
+                         f"{nat.MAX_HEAD_DIM}")
+    if k_cache.stride(3) != 1:
+        raise ValueError("cache head_dim must be contiguous")
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        if tuple(t.shape) != (B, 1, KVH, D) or t.dtype != query.dtype:
+            raise ValueError(f"{name} must be [{B}, 1, {KVH}, {D}] in the query dtype")
+    if window is not None and window <= 0:
+        raise ValueError("window must be positive")
+    dev = query.device
+    q = query.contiguous()
+    kn = k_new.contiguous()
+    vn = v_new.contiguous()
+    table = block_table_i32(block_table, dev)
+    if table.shape[0] != B:
+        raise ValueError(f"block_table has {table.shape[0]} rows for a batch of {B}")
+    lens, host_max = context_lens_i32(context_lens, dev, B)
+    W = table.shape[1]
+    cap = W * bs
+    if max_context is None:
+        max_context = cap if host_max is None else host_max
+    if host_max is not None and host_max > cap:
+        raise ValueError(f"context length {host_max} exceeds the block table capacity {cap}")
+    max_context = max(0, min(int(max_context), cap))
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    L = nat.lib()
+    ws_bytes = L.msattn_workspace_bytes(B, 1, H, KVH, D, max_context)
+    if ws_bytes == 0:
+        raise ValueError("unsupported attention geometry")
+    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
+        workspace = _workspace(dev, ws_bytes)
+    if out is None:
+        out = torch.empty((B, 1, H, D), dtype=query.dtype, device=dev)
+    status = L.msattn_paged_attention_append(
+        q.data_ptr(), kn.data_ptr(), vn.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), table.data_ptr(),
+        lens.data_ptr(), out.data_ptr(), workspace.data_ptr(), ws_bytes, B, H, KVH, D, bs, nb,
+        W, max_context, int(window or 0), float(scale), nat.dtype_code(query.dtype),
+        nat.dtype_code(k_cache.dtype), nat.stream_handle(dev))
+    nat.check("msattn_paged_attention_append", status)
+    return out
+
+
 def kernel_route(query: torch.Tensor, k_cache: torch.Tensor, block_table,
                  max_context: int | None = None, out: torch.Tensor | None = None,
                  workspace_bytes: int | None = None) -> str:

@@ -55,6 +55,19 @@ constexpr int64_t kStreamKMinTilesFp8Rt8 = MSATTN_STREAMK_MIN_TILES_FP8_RT8;
 #endif
 // 1: msattn_paged_attention's partition-kernel decodes merge in-kernel (no merge launch).
 constexpr bool kFusedMerge = MSATTN_FUSED_MERGE != 0;
+#ifndef MSATTN_FUSED_APPEND
+#define MSATTN_FUSED_APPEND 1
+#endif
+// 1: msattn_paged_attention_append writes the new K/V rows inside the partition decode
+// launch; 0: always a write_kv launch, then the decode.
+constexpr bool kFusedAppend = MSATTN_FUSED_APPEND != 0;
+
+int write_kv_impl(void* k_cache, void* v_cache, int64_t cache_block_stride,
+                  int64_t cache_slot_stride, int64_t cache_head_stride, const void* k,
+                  const void* v, const int32_t* block_table, const int32_t* starts,
+                  int start_offset, int batch, int tokens, int num_kv_heads, int head_dim,
+                  int block_size, int num_blocks, int table_width, int src_dtype, int kv_dtype,
+                  void* stream);
 #ifndef MSATTN_WIDE_ROUTE
 #define MSATTN_WIDE_ROUTE 1
 #endif
@@ -531,7 +544,8 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
                   int q_len, int num_heads, int num_kv_heads, int head_dim, int block_size,
                   int num_blocks, int table_width, int max_context, int causal, int window,
                   float scale, int q_dtype, int kv_dtype, const RopeArgs& rope, int key_lo,
-                  int* kind, void* stream, void* fused_out = nullptr) {
+                  int* kind, void* stream, void* fused_out = nullptr,
+                  const void* k_new = nullptr, const void* v_new = nullptr) {
   *kind = -1;
   if (!query || !block_table || !context_lens || !workspace) return MSATTN_ERR_INVALID_ARG;
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
@@ -599,6 +613,8 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   p.rope_max_pos = rope.max_pos;
   p.out = nullptr;
   p.tickets = nullptr;
+  p.k_new = nullptr;
+  p.v_new = nullptr;
   p.head_dim = head_dim;
   p.rows16 = rows16 ? 1 : 0;
   const int64_t gx = static_cast<int64_t>(p.max_parts) * num_kv_heads * p.rtiles;
@@ -625,6 +641,10 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
     *kind = 2;
     p.out = fused_out;
     p.tickets = p.hdr + kHdrTickets;
+    if (k_new != nullptr) {  // fused append: the caller checked append_fusable
+      p.k_new = k_new;
+      p.v_new = v_new;
+    }
     // The fp32 16-row route (P.V on the matrix core; its kernel unrolls kPartLongF32
     // tokens per workgroup) takes partitions of up to kPartLongF32 tokens when the grid
     // still reaches kTargetSlots: chunked prefill. Only the in-kernel merge reads these
@@ -853,7 +873,8 @@ int attention_impl(const void* query, const void* k_cache, const void* v_cache,
                    size_t workspace_bytes, int batch, int q_len, int num_heads,
                    int num_kv_heads, int head_dim, int block_size, int num_blocks,
                    int table_width, int max_context, int causal, int window, float scale,
-                   int q_dtype, int kv_dtype, bool prefill_needs_ws, void* stream) {
+                   int q_dtype, int kv_dtype, bool prefill_needs_ws, void* stream,
+                   const void* k_new = nullptr, const void* v_new = nullptr) {
   if (!out) return MSATTN_ERR_INVALID_ARG;
   if (!dtype_ok(q_dtype) || !aligned(out, dtype_bytes(q_dtype))) return MSATTN_ERR_INVALID_ARG;
   if (!geometry_ok(batch, q_len, num_heads, num_kv_heads, head_dim, max_context))
@@ -925,7 +946,8 @@ int attention_impl(const void* query, const void* k_cache, const void* v_cache,
       query, k_cache, v_cache, cache_block_stride, cache_slot_stride, cache_head_stride,
       block_table, context_lens, workspace, workspace_bytes, batch, q_len, num_heads,
       num_kv_heads, head_dim, block_size, num_blocks, table_width, max_context, causal, window,
-      scale, q_dtype, kv_dtype, RopeArgs{nullptr, nullptr, nullptr, 0}, 0, &kind, stream, out);
+      scale, q_dtype, kv_dtype, RopeArgs{nullptr, nullptr, nullptr, 0}, 0, &kind, stream, out,
+      k_new, v_new);
   if (rc != MSATTN_OK) return rc;
   if (kind == 2) return MSATTN_OK;  // merged in-kernel
   return merge_impl(workspace, workspace_bytes, context_lens, out, batch, q_len, num_heads,
@@ -1177,6 +1199,65 @@ int msattn_write_kv(void* k_cache, void* v_cache, int64_t cache_block_stride,
                     const void* v, const int32_t* block_table, const int32_t* starts, int batch,
                     int tokens, int num_kv_heads, int head_dim, int block_size, int num_blocks,
                     int table_width, int src_dtype, int kv_dtype, void* stream) {
+  return write_kv_impl(k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                       cache_head_stride, k, v, block_table, starts, 0, batch, tokens,
+                       num_kv_heads, head_dim, block_size, num_blocks, table_width, src_dtype,
+                       kv_dtype, stream);
+}
+
+int msattn_paged_attention_append(const void* query, const void* k_new, const void* v_new,
+                                  void* k_cache, void* v_cache, int64_t cache_block_stride,
+                                  int64_t cache_slot_stride, int64_t cache_head_stride,
+                                  const int32_t* block_table, const int32_t* context_lens,
+                                  void* out, void* workspace, size_t workspace_bytes, int batch,
+                                  int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                  int num_blocks, int table_width, int max_context, int window,
+                                  float scale, int q_dtype, int kv_dtype, void* stream) {
+  if (!k_new || !v_new || !k_cache || !v_cache || !context_lens || !out)
+    return MSATTN_ERR_INVALID_ARG;
+  if (!dtype_ok(q_dtype) || q_dtype == MSATTN_FP8_E4M3 || !dtype_ok(kv_dtype))
+    return MSATTN_ERR_INVALID_ARG;
+  if (!geometry_ok(batch, 1, num_heads, num_kv_heads, head_dim, max_context))
+    return MSATTN_ERR_INVALID_ARG;
+  const int route = choose_route(query, out, k_cache, v_cache, cache_block_stride,
+                                 cache_slot_stride, cache_head_stride, batch, 1, num_heads,
+                                 num_kv_heads, head_dim, block_size, max_context, q_dtype,
+                                 kv_dtype, workspace_bytes);
+  // The partition kernels built with the append: a bf16/fp16 query at up to 8 query rows
+  // per KV head (more would cost the kernels their second wave per SIMD).
+  const bool append_kernel = (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
+                             mfma_rows_per_tile(num_heads / num_kv_heads) <= 8;
+  if (kFusedAppend && route == MSATTN_ROUTE_PARTITION_FUSED && append_kernel &&
+      aligned(k_new, 16) && aligned(v_new, 16)) {
+    return attention_impl(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                          cache_head_stride, block_table, context_lens, out, workspace,
+                          workspace_bytes, batch, 1, num_heads, num_kv_heads, head_dim,
+                          block_size, num_blocks, table_width, max_context, 1, window, scale,
+                          q_dtype, kv_dtype, true, stream, k_new, v_new);
+  }
+  // Other routes: the write, then the decode (two launches, the same result).
+  const int rc = write_kv_impl(k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                               cache_head_stride, k_new, v_new, block_table, context_lens, -1,
+                               batch, 1, num_kv_heads, head_dim, block_size, num_blocks,
+                               table_width, q_dtype, kv_dtype, stream);
+  if (rc != MSATTN_OK) return rc;
+  return msattn_paged_attention(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
+                                cache_head_stride, block_table, context_lens, out, workspace,
+                                workspace_bytes, batch, 1, num_heads, num_kv_heads, head_dim,
+                                block_size, num_blocks, table_width, max_context, 1, window,
+                                scale, q_dtype, kv_dtype, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int write_kv_impl(void* k_cache, void* v_cache, int64_t cache_block_stride,
+                  int64_t cache_slot_stride, int64_t cache_head_stride, const void* k,
+                  const void* v, const int32_t* block_table, const int32_t* starts,
+                  int start_offset, int batch, int tokens, int num_kv_heads, int head_dim,
+                  int block_size, int num_blocks, int table_width, int src_dtype, int kv_dtype,
+                  void* stream) {
   if (!k_cache || !v_cache || !k || !v || !block_table || !starts) return MSATTN_ERR_INVALID_ARG;
   if (batch <= 0 || tokens < 0 || num_kv_heads <= 0 || head_dim <= 0) return MSATTN_ERR_INVALID_ARG;
   if (block_size <= 0 || num_blocks <= 0 || table_width <= 0) return MSATTN_ERR_INVALID_ARG;
@@ -1205,11 +1286,16 @@ int msattn_write_kv(void* k_cache, void* v_cache, int64_t cache_block_stride,
   p.bs = block_size;
   p.num_blocks = num_blocks;
   p.W = table_width;
+  p.start_offset = start_offset;
   bool sup = false;
   const hipError_t e = launch_write_kv(p, src_dtype, kv_dtype, static_cast<hipStream_t>(stream), &sup);
   if (!sup) return MSATTN_ERR_UNSUPPORTED;
   return hip_status(e);
 }
+
+}  // namespace
+
+extern "C" {
 
 int msattn_gather_kv(const void* cache, int64_t cache_block_stride, int64_t cache_slot_stride,
                      int64_t cache_head_stride, const int32_t* block_table,

@@ -440,6 +440,28 @@ template <> struct Kv8<float, float> {
   }
 };
 
+// A new K/V row's eight elements (type ST) as loaded for the fused append, and the raw
+// chunk a cache of KT holds for them: each element cast as msattn_write_kv casts it
+// (through fp32 with the cache type's rounding; the same type keeps its bits).
+template <typename ST> struct alignas(16) SrcChunk {
+  ST v[8];
+};
+template <typename KT> struct alignas(sizeof(KT) * 8 >= 16 ? 16 : 8) CacheChunk {
+  KT v[8];
+};
+template <typename KT, typename ST, typename RAW>
+__device__ __forceinline__ RAW append_raw(const SrcChunk<ST>& x) {
+  static_assert(sizeof(RAW) == 8 * sizeof(KT), "a raw chunk holds eight cache elements");
+  if constexpr (std::is_same<KT, ST>::value) {
+    return __builtin_bit_cast(RAW, x);
+  } else {
+    CacheChunk<KT> c;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) Elt<KT>::store(&c.v[e], Elt<ST>::load(&x.v[e]));
+    return __builtin_bit_cast(RAW, c);
+  }
+}
+
 #ifndef MSATTN_PV_DOT2
 #define MSATTN_PV_DOT2 1
 #endif
@@ -619,7 +641,8 @@ __device__ __forceinline__ void rope_chunks(typename QChunk<T>::type (&qb)[D / 3
   }
 }
 
-template <typename T, typename KT, int D, int RT, int W = kMfmaWaves, int WPC = kMfmaWgPerCu>
+template <typename T, typename KT, int D, int RT, int W = kMfmaWaves, int WPC = kMfmaWgPerCu,
+          bool APPEND = false>
 __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParams p) {
   constexpr int kWaves = W;               // waves per workgroup
   constexpr int kThreads = W * kWave;
@@ -1020,6 +1043,54 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
     pv_tile<T, KT, D, RTA>(acc, pr, vm, va);
   };
 
+  // Fused append (p.k_new set): the new
+  // token's K/V rows go to cache position ctx - 1. The wave whose run holds that position
+  // requests them with its tiles, writes them to the cache (cast to the cache type) and
+  // puts the same values into the tile's registers in place of the row it loaded, so
+  // this launch reads what msattn_write_kv followed by a decode would read. No other
+  // workgroup reads that position (it lies in the last partition), so nothing waits for
+  // the store.
+  // (Built as its own instantiation, APPEND, for 2-byte queries at up to 8 rows per tile:
+  // the chunks held for it take 16-36 registers, which cost the decode without it 0.5-2.6 %.)
+  constexpr bool kAppendOk = APPEND && !kPvMfma && sizeof(T) == 2 && RT <= 8;
+  const bool app = kAppendOk && p.k_new != nullptr && ctx > 0;
+  const int k_app = app ? (ctx - 1) / 16 - tw0 : -1;  // run index of the new token's tile
+  const bool app_here = k_app >= 0 && k_app < nt;      // wave-uniform
+  const int r_new = (ctx - 1) & 15;                    // its row in the tile
+  const bool k_lane = tile_token<D>(n) == r_new;       // lanes holding its K chunks
+  const bool v_lane = va <= r_new && (r_new - va) % TPI == 0;  // and one of its V chunks
+  SrcChunk<T> kn[JD], vn;
+  if (app_here) {
+    const int64_t row = (static_cast<int64_t>(b) * p.KVH + kvh) * D;
+    if (k_lane) {
+#pragma unroll
+      for (int j = 0; j < JD; ++j)
+        kn[j] = *reinterpret_cast<const SrcChunk<T>*>(static_cast<const T*>(p.k_new) + row +
+                                                      KV::qk_dim0(j, g, JD));
+    }
+    if (v_lane)
+      vn = *reinterpret_cast<const SrcChunk<T>*>(static_cast<const T*>(p.v_new) + row + vc * 8);
+  }
+  auto append_patch = [&](raw_t (&kb)[JD], raw_t (&vb)[NJ], int64_t base) __attribute__((always_inline)) {
+    if (base < 0) return;  // a hole: write_kv writes nothing there either
+    const int64_t rowoff = base + static_cast<int64_t>(r_new) * p.slot_stride;
+    if (k_lane) {
+#pragma unroll
+      for (int j = 0; j < JD; ++j) {
+        const raw_t x = append_raw<KT, T, raw_t>(kn[j]);
+        kb[j] = x;
+        *reinterpret_cast<raw_t*>(const_cast<KT*>(kbase) + rowoff + KV::qk_dim0(j, g, JD)) = x;
+      }
+    }
+    if (v_lane) {
+      const raw_t x = append_raw<KT, T, raw_t>(vn);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (TPI * j + va == r_new) vb[j] = x;
+      *reinterpret_cast<raw_t*>(const_cast<KT*>(vbase) + rowoff + vc * 8) = x;
+    }
+  };
+
   // A ring of DEPTH tiles: the loads of DEPTH - 1 tiles are in flight while one is
   // consumed. The sequence is fully unrolled (a wave owns at most kMaxT tiles) so
   // every wait for a tile's loads is exact; loads for tiles at or past nt read
@@ -1039,6 +1110,9 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
     if constexpr (nx < kMaxT) {
       br[nx % DEPTH] = tile_base(nx);
       issue(br[nx % DEPTH], kr[nx % DEPTH], vr[nx % DEPTH]);
+    }
+    if constexpr (kAppendOk) {
+      if (app_here && k == k_app) append_patch(kr[k % DEPTH], vr[k % DEPTH], br[k % DEPTH]);
     }
     consume(k, kr[k % DEPTH], vr[k % DEPTH], br[k % DEPTH]);
   });
@@ -1143,8 +1217,17 @@ template <typename T, typename KT, int D, int RT, int W = kMfmaWaves, int WPC = 
 hipError_t launch_decode_mfma_one(const SplitParams& p, hipStream_t stream) {
   const unsigned gx = static_cast<unsigned>(p.max_parts) * static_cast<unsigned>(p.KVH) *
                       static_cast<unsigned>(p.rtiles);
-  hipLaunchKernelGGL((decode_mfma_kernel<T, KT, D, RT, W, WPC>),
-                     dim3(gx, 1, static_cast<unsigned>(p.batch)), dim3(W * kWave), 0, stream, p);
+  const dim3 grid(gx, 1, static_cast<unsigned>(p.batch));
+  // the fused append's instantiation (the host sets k_new only where it is built)
+  if constexpr (sizeof(T) == 2 && RT <= 8) {
+    if (p.k_new != nullptr) {
+      hipLaunchKernelGGL((decode_mfma_kernel<T, KT, D, RT, W, WPC, true>), grid, dim3(W * kWave),
+                         0, stream, p);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((decode_mfma_kernel<T, KT, D, RT, W, WPC>), grid, dim3(W * kWave), 0,
+                     stream, p);
   return hipGetLastError();
 }
 

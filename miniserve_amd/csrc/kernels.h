@@ -37,6 +37,7 @@ struct WriteKVParams {
   const int32_t* starts;
   int64_t blk_stride, slot_stride, head_stride;
   int batch, tokens, KVH, D, bs, num_blocks, W;
+  int start_offset;  // added to starts[b] (-1: starts are context lengths after the append)
 };
 
 hipError_t launch_write_kv(const WriteKVParams& p, int src_dtype, int dst_dtype,

@@ -31,7 +31,7 @@ __global__ __launch_bounds__(kOpsThreads) void write_kv_kernel(const WriteKVPara
     rest /= p.KVH;
     const int t = static_cast<int>(rest % p.tokens);
     const int b = static_cast<int>(rest / p.tokens);
-    const int64_t off = token_offset(p.table, b, p.starts[b] + t, p.bs, p.W, p.num_blocks,
+    const int64_t off = token_offset(p.table, b, p.starts[b] + p.start_offset + t, p.bs, p.W, p.num_blocks,
                                      p.blk_stride, p.slot_stride);
     if (off < 0) continue;
     const int64_t dst = off + static_cast<int64_t>(h) * p.head_stride + d;
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kOpsThreads) void write_kv_copy_kernel(const WriteK
     rest /= p.KVH;
     const int t = static_cast<int>(rest % p.tokens);
     const int b = static_cast<int>(rest / p.tokens);
-    const int64_t off = token_offset(p.table, b, p.starts[b] + t, p.bs, p.W, p.num_blocks,
+    const int64_t off = token_offset(p.table, b, p.starts[b] + p.start_offset + t, p.bs, p.W, p.num_blocks,
                                      p.blk_stride, p.slot_stride);
     if (off < 0) continue;
     const int64_t dst = off + static_cast<int64_t>(h) * p.head_stride + d;
@@ -83,7 +83,7 @@ __global__ __launch_bounds__(kOpsThreads) void write_kv_vec_kernel(const WriteKV
     rest /= p.KVH;
     const int t = static_cast<int>(rest % p.tokens);
     const int b = static_cast<int>(rest / p.tokens);
-    const int64_t off = token_offset(p.table, b, p.starts[b] + t, p.bs, p.W, p.num_blocks,
+    const int64_t off = token_offset(p.table, b, p.starts[b] + p.start_offset + t, p.bs, p.W, p.num_blocks,
                                      p.blk_stride, p.slot_stride);
     if (off < 0) continue;
     const int64_t src = idx * E;  // [b, t, h, c * E] of the contiguous source

@@ -104,6 +104,11 @@ struct SplitParams {
   int head_dim;    // the row's head size (the generic kernel's element mode compiles a larger
                    // capacity and masks the dims past it)
   int rows16;      // cache rows start on 16-byte boundaries and hold whole 16-byte chunks
+  // Fused append (partition MFMA kernel, q_len 1): non-null k_new / v_new, contiguous
+  // [batch, KVH, D] rows of the query type, 16-byte aligned: row (b, kvh) goes to cache
+  // position lens[b] - 1 (cast to the cache type) before the decode reads it.
+  const void* k_new;
+  const void* v_new;
 };
 
 // One 16-byte chunk of a K/V row as the generic kernel's lanes read it. Whole chunks of

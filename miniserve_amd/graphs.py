@@ -4,7 +4,9 @@ Restates GraphedDecodeRunner (miniserve/model_runner.py:224-336) for the attenti
 path alone. A decode step over L layers is, per layer:
     write_kv(new k, v at position ctx[b])    (miniserve/attention.py:111-133)
     forward(q, caches, table, ctx + 1)       (miniserve/attention.py:205-250)
-captured once per (bucket, input set) as a hipGraph through torch.cuda.CUDAGraph.
+captured once per (bucket, input set) as a hipGraph through torch.cuda.CUDAGraph. The two
+calls go through one msattn_paged_attention_append per layer (one launch where the
+partition kernel takes the decode; `fused_append=False` keeps them apart).
 Batches that are not a bucket size replay the next larger bucket with pad rows.
 
 Kept from the reference: sorted buckets starting at 1 (ValueError otherwise), two
@@ -32,7 +34,7 @@ import numpy as np
 import torch
 
 from . import _native as nat
-from .attention import PagedAttention, paged_attention
+from .attention import PagedAttention, paged_attention, paged_attention_append
 
 
 def fill_table(tab: np.ndarray, tables, batch: int) -> None:
@@ -77,13 +79,17 @@ class GraphedDecodeRunner:
 
     def __init__(self, layers: Sequence[DecodeLayer], table_width: int,
                  buckets: Sequence[int] = (1, 2, 4, 8, 16, 32, 64),
-                 dtype: torch.dtype | None = None) -> None:
+                 dtype: torch.dtype | None = None, fused_append: bool = True) -> None:
+        """fused_append: each layer's write_kv and decode through one
+        msattn_paged_attention_append call (one launch where the partition kernel takes
+        it, the same caches and output bit for bit); False keeps the two calls."""
         buckets = list(buckets)
         if not buckets or sorted(buckets) != buckets or buckets[0] < 1:
             raise ValueError("buckets must be sorted, start at 1")
         if not layers:
             raise ValueError("at least one layer is needed")
         self.layers = list(layers)
+        self.fused_append = bool(fused_append)
         self.buckets = tuple(buckets)
         self.max_batch = self.buckets[-1]
         self.table_width = int(table_width)
@@ -142,6 +148,16 @@ class GraphedDecodeRunner:
         start = buf["start"][:bucket]
         lens = buf["lens"][:bucket]
         for li, layer in enumerate(self.layers):
+            if self.fused_append and buf["k"].dtype == buf["q"].dtype:
+                # write_kv at lens - 1 (= start for real rows; pad rows have lens 0 and
+                # write nothing) and the decode, in one launch where the partition
+                # kernel takes the call
+                paged_attention_append(buf["q"][li, :bucket], buf["k"][li, :bucket],
+                                       buf["v"][li, :bucket], layer.k_cache, layer.v_cache,
+                                       table, lens, window=layer.pa.window,
+                                       max_context=self.max_context, workspace=self._ws,
+                                       out=self._out[li, :bucket])
+                continue
             layer.pa.write_kv(layer.k_cache, layer.v_cache, buf["k"][li, :bucket],
                               buf["v"][li, :bucket], table, start=start)
             paged_attention(buf["q"][li, :bucket], layer.k_cache, layer.v_cache, table, lens,

@@ -320,3 +320,26 @@ def test_route_rejects_bad_arguments():
     bad = list(args)
     bad[14] = nat.FP8_E4M3  # fp8 query
     assert lib.msattn_paged_attention_route(*bad, ctypes.byref(r)) == nat.ERR_INVALID_ARG
+
+
+def test_append_rejects_bad_arguments():
+    """msattn_paged_attention_append checks its pointers, types and geometry before it
+    launches anything (these calls never reach a device)."""
+    lib = nat.lib()
+    # query, k_new, v_new, k_cache, v_cache, strides x3, table, lens, out, ws, ws_bytes,
+    # batch, H, KVH, D, bs, num_blocks, W, max_context, window, scale, q/kv dtype, stream
+    args = [256, 512, 768, 1024, 2048, 16 * 256, 256, 128, 4096, 8192, 16384, 32768, 1 << 20,
+            2, 4, 2, 128, 16, 100, 4, 64, 0, 0.1, nat.BF16, nat.BF16, None]
+    for i in (1, 2, 3, 4, 9, 10):  # k_new, v_new, k_cache, v_cache, lens, out
+        bad = list(args)
+        bad[i] = None
+        assert lib.msattn_paged_attention_append(*bad) == nat.ERR_INVALID_ARG, i
+    bad = list(args)
+    bad[23] = nat.FP8_E4M3  # fp8 query
+    assert lib.msattn_paged_attention_append(*bad) == nat.ERR_INVALID_ARG
+    bad = list(args)
+    bad[16] = 129  # odd head_dim
+    assert lib.msattn_paged_attention_append(*bad) == nat.ERR_INVALID_ARG
+    bad = list(args)
+    bad[14] = 3  # heads not a multiple of KV heads
+    assert lib.msattn_paged_attention_append(*bad) == nat.ERR_INVALID_ARG
