@@ -285,13 +285,14 @@ int msattn_write_kv(void* k_cache, void* v_cache, int64_t cache_block_stride,
  * context_lens[b] - 1 of each row (rows with context_lens[b] <= 0 write nothing; holes
  * are skipped), followed by msattn_paged_attention (q_len 1, causal) over context_lens.
  * k_new / v_new are contiguous [batch, 1, num_kv_heads, head_dim] in the query dtype,
- * the token each row appends this step; context_lens already count it. Where the call
- * takes the partition kernel merging in-kernel (MSATTN_ROUTE_PARTITION_FUSED) with a
- * bf16/fp16 query, at most 8 query rows per KV head and k_new and v_new 16-byte aligned,
- * both run in that one launch: the workgroup whose partition holds the new
- * position writes the rows (cast to the cache type as msattn_write_kv casts them) and
- * uses the same values in place of the cache's row, so the output and the caches equal
- * those of the two calls bit for bit. Other routes run the two calls. No reference
+ * the token each row appends this step; context_lens already count it. With a bf16/fp16
+ * query, at most 8 query rows per KV head and k_new and v_new 16-byte aligned, the append
+ * runs inside the decode launch where the call takes the partition kernel merging
+ * in-kernel (MSATTN_ROUTE_PARTITION_FUSED) or the stream-K kernel over a cache of 2 or 4
+ * byte elements (MSATTN_ROUTE_STREAMK): the wave whose work holds the new position writes
+ * the rows (cast to the cache type as msattn_write_kv casts them) and uses the same values
+ * in place of the cache's row, so the output and the caches equal those of the two calls
+ * bit for bit. Other routes run the two calls. No reference
  * counterpart as one call: the reference runner makes these two calls per layer
  * (miniserve/model_runner.py:70-76, attention.py:111-133 and 205-250); this entry
  * point is for callers, such as a bucketed decode graph, that want one launch per layer.

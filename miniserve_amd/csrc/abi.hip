@@ -625,6 +625,10 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (plan.kind == 1) {  // stream-K
     *kind = 1;
+    if (k_new != nullptr) {  // fused append: the caller checked the route and types
+      p.k_new = k_new;
+      p.v_new = v_new;
+    }
     const int units = num_kv_heads * p.rtiles;
     p.sk_group = largest_pow2_divisor_upto(
         units, sk_waves(kv_fp8 ? 1 : 2, q_dtype == MSATTN_F32 ? 4 : 2));
@@ -1223,12 +1227,13 @@ int msattn_paged_attention_append(const void* query, const void* k_new, const vo
                                  cache_slot_stride, cache_head_stride, batch, 1, num_heads,
                                  num_kv_heads, head_dim, block_size, max_context, q_dtype,
                                  kv_dtype, workspace_bytes);
-  // The partition kernels built with the append: a bf16/fp16 query at up to 8 query rows
-  // per KV head (more would cost the kernels their second wave per SIMD).
+  // The partition and stream-K kernels built with the append: a bf16/fp16 query at up to
+  // 8 query rows per KV head (stream-K: not over an fp8 cache).
   const bool append_kernel = (q_dtype == MSATTN_BF16 || q_dtype == MSATTN_F16) &&
                              mfma_rows_per_tile(num_heads / num_kv_heads) <= 8;
-  if (kFusedAppend && route == MSATTN_ROUTE_PARTITION_FUSED && append_kernel &&
-      aligned(k_new, 16) && aligned(v_new, 16)) {
+  if (kFusedAppend && append_kernel && aligned(k_new, 16) && aligned(v_new, 16) &&
+      (route == MSATTN_ROUTE_PARTITION_FUSED ||
+       (route == MSATTN_ROUTE_STREAMK && kv_dtype != MSATTN_FP8_E4M3))) {
     return attention_impl(query, k_cache, v_cache, cache_block_stride, cache_slot_stride,
                           cache_head_stride, block_table, context_lens, out, workspace,
                           workspace_bytes, batch, 1, num_heads, num_kv_heads, head_dim,

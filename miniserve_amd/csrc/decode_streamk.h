@@ -86,7 +86,7 @@ __host__ __device__ constexpr int64_t streamk_pieces(int64_t n_chunks, int64_t n
   return n_chunks + n_segments;
 }
 
-template <typename T, typename KT, int D, int RT>
+template <typename T, typename KT, int D, int RT, bool APPEND = false>
 __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decode_streamk_kernel(
     const SplitParams p) {
   constexpr int kSkWaves = sk_waves(sizeof(KT), sizeof(T));
@@ -350,6 +350,55 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decod
   // on across runs: a run is rounded up to whole ring turns (the extra tiles read
   // nothing), and its last turn already issues the next run's first tiles, whose loads
   // are in flight while the piece's partial is written.
+  // Fused append (APPEND instantiation, p.k_new set): the new token's K/V rows go to
+  // cache position ctx - 1 of each sequence, in the last tile of its segment. The wave
+  // whose piece holds that tile (one per KV head) requests the rows when the piece
+  // starts, writes them to the cache (cast as msattn_write_kv casts them) and puts the
+  // same values into the tile's registers in place of the row it loaded. No other piece
+  // reads that position, so nothing waits for the store.
+  // (Not over an fp8 cache: its 8-wave workgroups keep two waves a SIMD, where the held
+  // chunks would spill.)
+  constexpr bool kAppendOk = APPEND && sizeof(T) == 2 && sizeof(KT) != 1 && RT <= 8;
+  int app_t = -1;  // absolute tile index of the current piece to patch, or -1
+  int app_r = 0;   // the new token's row in that tile
+  SrcChunk<T> kn[JD], vn;
+  auto app_setup = [&](const Piece& pc) __attribute__((always_inline)) {
+    const int ctx = s_ctx[pc.b];
+    const int t_new = (ctx - 1) / 16;
+    app_t = ctx > 0 && t_new >= pc.t_first && t_new < pc.t_first + pc.ntiles ? t_new : -1;
+    if (app_t < 0) return;
+    app_r = (ctx - 1) & 15;
+    const int64_t row = (static_cast<int64_t>(pc.b) * p.KVH + pc.kvh) * D;
+    if (tile_token<D>(n) == app_r) {
+#pragma unroll
+      for (int j = 0; j < JD; ++j)
+        kn[j] = *reinterpret_cast<const SrcChunk<T>*>(static_cast<const T*>(p.k_new) + row +
+                                                      KV::qk_dim0(j, g, JD));
+    }
+    if (va <= app_r && (app_r - va) % TPI == 0)
+      vn = *reinterpret_cast<const SrcChunk<T>*>(static_cast<const T*>(p.v_new) + row + vc * 8);
+  };
+  auto app_patch = [&](raw_t (&kb)[JD], raw_t (&vb)[NJ], int64_t base) __attribute__((always_inline)) {
+    if (base < 0) return;  // a hole: write_kv writes nothing there either
+    const int64_t rowoff = base + static_cast<int64_t>(app_r) * p.slot_stride;
+    if (tile_token<D>(n) == app_r) {
+#pragma unroll
+      for (int j = 0; j < JD; ++j) {
+        const raw_t x = append_raw<KT, T, raw_t>(kn[j]);
+        kb[j] = x;
+        *reinterpret_cast<raw_t*>(const_cast<KT*>(kbase) + rowoff + KV::qk_dim0(j, g, JD)) = x;
+      }
+    }
+    if (va <= app_r && (app_r - va) % TPI == 0) {
+      const raw_t x = append_raw<KT, T, raw_t>(vn);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (TPI * j + va == app_r) vb[j] = x;
+      *reinterpret_cast<raw_t*>(const_cast<KT*>(vbase) + rowoff + vc * 8) = x;
+    }
+  };
+  if constexpr (kAppendOk) app_setup(cur);
+
   raw_t kq[DEPTH][JD], vq[DEPTH][NJ];
   int64_t bq[DEPTH];
   bool primed = false;  // the ring holds the run's first DEPTH - 1 tiles
@@ -488,6 +537,10 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decod
           constexpr int nx = (d + DEPTH - 1) % DEPTH;
           bq[nx] = tile_base(k + d + DEPTH - 1);
           issue(bq[nx], kq[nx], vq[nx]);
+          if constexpr (kAppendOk) {
+            if (k + d < nt && cur.t_first + run0 + k + d == app_t)
+              app_patch(kq[cu], vq[cu], bq[cu]);
+          }
           consume(k + d, kq[cu], vq[cu], bq[cu]);
         });
         if constexpr (MSATTN_SK_LATE_IDS) {
@@ -545,11 +598,23 @@ __global__ __launch_bounds__(sk_waves(sizeof(KT), sizeof(T)) * kWave) void decod
     cur = nxt;
     run0 = run_n;
     my_base = base_n;
+    if constexpr (kAppendOk) {
+      if (run0 == 0) app_setup(cur);  // a new piece
+    }
   }
 }
 
 template <typename T, typename KT, int D, int RT>
 hipError_t launch_decode_streamk_one(const SplitParams& p, int grid, hipStream_t stream) {
+  // the fused append's instantiation (the host sets k_new only where it is built)
+  if constexpr (sizeof(T) == 2 && sizeof(KT) != 1 && RT <= 8) {
+    if (p.k_new != nullptr) {
+      hipLaunchKernelGGL((decode_streamk_kernel<T, KT, D, RT, true>),
+                         dim3(static_cast<unsigned>(grid)),
+                         dim3(sk_waves(sizeof(KT), sizeof(T)) * kWave), 0, stream, p);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((decode_streamk_kernel<T, KT, D, RT>), dim3(static_cast<unsigned>(grid)),
                      dim3(sk_waves(sizeof(KT), sizeof(T)) * kWave), 0, stream, p);
   return hipGetLastError();

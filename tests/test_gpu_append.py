@@ -1,7 +1,7 @@
 """GPU parity of msattn_paged_attention_append: write_kv of the new token at position
-context_lens[b] - 1 followed by the decode, in one launch where the partition kernel
-takes the call (bf16/fp16 query, at most 8 query rows per KV head), as two launches
-elsewhere.
+context_lens[b] - 1 followed by the decode, inside the decode launch where the partition
+or stream-K kernel takes the call (bf16/fp16 query, at most 8 query rows per KV head), as
+two launches elsewhere.
 
 The reference pair is the library's own two calls on a copy of the caches:
 msattn_write_kv at starts = context_lens - 1, then paged_attention. The fused call must
@@ -58,8 +58,14 @@ CASES = {
                                   "partition-fused"),
     "G16 (two launches)": (32, 2, 128, torch.bfloat16, torch.bfloat16, 8, 64, 0,
                            "partition-fused"),
-    "stream-K table (two launches)": (32, 8, 128, torch.bfloat16, torch.bfloat16, 16, 512, 0,
-                                      "stream-K"),
+    # stream-K (then the merge kernel): the append in the stream-K launch
+    "stream-K table": (32, 8, 128, torch.bfloat16, torch.bfloat16, 16, 512, 0, "stream-K"),
+    "stream-K table, fp8 cache (two launches)": (32, 8, 128, torch.bfloat16,
+                                                 torch.float8_e4m3fn, 16, 512, 0, "stream-K"),
+    "stream-K table, bf16 over fp32": (32, 8, 128, torch.bfloat16, torch.float32, 16, 512, 0,
+                                       "stream-K"),
+    "stream-K table, fp16 D64 G7 window": (14, 2, 64, torch.float16, torch.float16, 64, 1024,
+                                           1000, "stream-K"),
     "head_dim 80, generic kernel (two launches)": (8, 2, 80, torch.bfloat16, torch.bfloat16, 8,
                                                    64, 0, "generic"),
 }
