@@ -55,6 +55,12 @@
 #ifndef MSATTN_PF_G1PRIO
 #define MSATTN_PF_G1PRIO 1
 #endif
+// Wave priority of the copy path's MFMA-only blocks (the first half-step's scores and the
+// second half-step's P.V), above both groups' loop priorities, so that a SIMD's matrix core
+// is fed first when both waves are ready; 0 leaves them at the group's priority.
+#ifndef MSATTN_PF_MPRIO
+#define MSATTN_PF_MPRIO 2
+#endif
 
 namespace msattn {
 
@@ -751,9 +757,21 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     // The scores sv and weights pb of a step live across blocks (and, for group 1, across
     // an iteration's barrier). `copies` issues copy instructions among the block's MFMAs.
     mf_f32x4 sv[RB][4];
+    // The MFMA-only blocks run at MSATTN_PF_MPRIO and return to the group's priority.
+    auto prio_up = [] {
+      if constexpr (MSATTN_PF_MPRIO > 0) __builtin_amdgcn_s_setprio(MSATTN_PF_MPRIO);
+    };
+    auto prio_down = [&] {
+      if constexpr (MSATTN_PF_MPRIO > 0) {
+        if (grp) __builtin_amdgcn_s_setprio(MSATTN_PF_G1PRIO);
+        else __builtin_amdgcn_s_setprio(0);
+      }
+    };
     auto r0 = [&](uint16_t* kc, int step, bool full, auto&& side) {
+      prio_up();
       scores(k_from(kc), sv, I0{}, I2{});
       side();
+      prio_down();
       if (!full) mask_scores(step, sv, 0, 2);
     };
     auto r1 = [&](uint16_t* kc, int step, bool full, auto&& copies) {
@@ -779,7 +797,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][1]);
       softmax_end(sv, 1);
     };
-    auto r3 = [&](uint16_t* vc) { pv(v_from(vc), 1); };
+    auto r3 = [&](uint16_t* vc) {
+      prio_up();
+      pv(v_from(vc), 1);
+      prio_down();
+    };
     auto no_copies = [] {};
 
     // Group grp takes steps s_first + 2 i; the K and V of its i-th step go to slots
