@@ -357,6 +357,28 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int rblock = p.rblocks - 1 - static_cast<int>(bx % static_cast<unsigned>(p.rblocks));
   const int kvh = static_cast<int>(bx / static_cast<unsigned>(p.rblocks));
 
+  // Copy path: the task's first window of tile offsets starts at tile pre_t whenever no
+  // sliding window moves its first key (the task's steps then start at step 0, or at the
+  // prefix partition's first step, and a share's part at its first pair): that window's
+  // table entries are requested here, before the context length is known, so that their
+  // round trip overlaps the length's and the query's instead of following them.
+  int pre_t = -1, pre_phys = -1;
+  if constexpr (DMA) {
+    static_assert(kPfPageChunk == kPfThreads, "one window entry per thread");
+    int s0 = -1;
+    if constexpr (PX) {
+      const int lo = static_cast<int>(blockIdx.y) * p.key_part;
+      s0 = lo < p.max_ctx ? lo / kPfStep : 0;
+    } else if (p.window <= 0) {
+      s0 = 2 * it_lo;
+    }
+    if (s0 >= 0) {
+      pre_t = s0 * (kPfStep / 16);
+      const int tok = (pre_t + tid) * 16;
+      const int pg = p.bs_shift >= 0 ? tok >> p.bs_shift : tok / p.bs;
+      if (pg < p.W) pre_phys = p.table[static_cast<int64_t>(b) * p.W + pg];
+    }
+  }
   int ctx = PX ? p.max_ctx : p.lens[b];
   ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
   const int row0 = rblock * BROWS;
@@ -676,7 +698,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     // Reloaded (between barriers, by every thread) when a step leaves it.
     int64_t* const s_tile = reinterpret_cast<int64_t*>(s_pg);
     int tb_base = -(1 << 30);
-    auto ensure_tiles = [&](int s_lo, int s_hi) {
+    // first: the prologue's call, which may take the entries requested at the task's start
+    auto ensure_tiles = [&](int s_lo, int s_hi, auto first_c) {
+      constexpr bool first = decltype(first_c)::value;
       const int t_lo = s_lo * (kPfStep / 16);
       const int t_hi = s_hi * (kPfStep / 16) + kPfStep / 16 - 1;
       if (t_lo < tb_base || t_hi >= tb_base + kPfPageChunk) {
@@ -686,7 +710,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
           const int pg = page_of(tok);
           int64_t off = -1;
           if (pg < p.W) {
-            const int phys = p.table[static_cast<int64_t>(b) * p.W + pg];
+            const int phys = first && t_lo == pre_t ? pre_phys
+                                                    : p.table[static_cast<int64_t>(b) * p.W + pg];
             if (phys >= 0 && phys < p.num_blocks)
               off = static_cast<int64_t>(phys) * p.blk_stride +
                     static_cast<int64_t>(tok - pg * p.bs) * p.slot_stride +
@@ -815,7 +840,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     const int n_it = ceil_div(step_end - step_first, 2);
     TileCopy ck = plan_tile(0, false), cv = ck;  // this iteration's copies: K, V
     if (n_it > 0) {
-      ensure_tiles(step_first, min(step_first + 5, step_end - 1));
+      ensure_tiles(step_first, min(step_first + 5, step_end - 1), std::true_type{});
       const TileCopy c = plan_tile(s_first, s_first < step_end);
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
@@ -841,7 +866,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       uint16_t* const v_nxt = cur ? v0 : v1;  // V of step i + 1 goes here
       const int step = s_first + 2 * i;
       const int pn = step_first + 2 * i + 2;
-      if (pn < step_end) ensure_tiles(pn, min(pn + 3, step_end - 1));
+      if (pn < step_end) ensure_tiles(pn, min(pn + 3, step_end - 1), std::false_type{});
       if (step < step_end) {
         const bool full = step_full(step);
         TileCopy cn;  // the next iteration's copies (step + 4)
@@ -868,7 +893,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       uint16_t* const v_prv = cur ? v0 : v1;  // V of step i - 1
       const int step = s_first + 2 * i;
       const int pn = step_first + 2 * i + 2;
-      if (pn < step_end) ensure_tiles(pn, min(pn + 3, step_end - 1));
+      if (pn < step_end) ensure_tiles(pn, min(pn + 3, step_end - 1), std::false_type{});
       if (i > 0 && step - 2 < step_end) {  // the second half of step i - 1
         r2(v_prv, [&] {
 #pragma unroll
