@@ -124,9 +124,9 @@ size_t msattn_workspace_bytes(int batch, int q_len, int num_heads, int num_kv_he
  * A prefill-kernel launch whose tasks (row blocks of 128 x KV heads x sequences) would
  * leave CUs idle in one-task-per-workgroup rounds runs stream-K when a cost model in sizes
  * only predicts it faster and the workspace is msattn_workspace_bytes() or more: one
- * workgroup per CU, each an equal share of all tasks' key steps, a task split between
- * workgroups folded by the last of them (tickets in the workspace header, which every call
- * leaves at zero); the fold sums the pieces in another order than one workgroup would.
+ * workgroup per CU, each an equal share of all tasks' key steps, then a fold launch that
+ * merges each task split between workgroups (its rows spread over many workgroups); the
+ * fold sums the pieces in another order than one workgroup would.
  */
 int msattn_paged_attention(const void* query, const void* k_cache, const void* v_cache,
                            int64_t cache_block_stride, int64_t cache_slot_stride,

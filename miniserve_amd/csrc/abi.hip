@@ -100,21 +100,20 @@ constexpr int kDeepMinPerCu = MSATTN_DEEP_MIN_PER_CU;
 #define MSATTN_PF_STREAMK 1
 #endif
 constexpr int kPfStreamK = MSATTN_PF_STREAMK;
-static_assert(kPfSkMaxTasks <= kMaxTickets, "a ticket per stream-K prefill task");
-// The cost model, in units of one task's key-step pair (about 2.2 us on MI355X), fitted on
+// The cost model, in units of one task's key-step pair (about 2 us on MI355X), fitted on
 // ten chunked-prefill shapes of 16-224 tasks timed both ways: one task per workgroup costs
-// P x rounds (P: key-step pairs of a task, rounds: of one task per CU); stream-K costs
-// P x tasks / G + kPfSkFixedPairs (two task starts, two partials and a ticket per share)
-// + kPfSkMergePairs x G / tasks (a task's contributors merged by the last), in tenths of
-// a pair. Stream-K is taken when it costs under 90 % of the other.
+// P x rounds + kPfOneFixed (P: key-step pairs of a task, rounds: of one task per CU; the
+// fixed part: a task's start and end); stream-K costs P x tasks / G + kPfSkFixed (a share's
+// starts and ends, its partials and the fold launch), in tenths of a pair. Stream-K is
+// taken when it costs under 90 % of the other.
 #ifndef MSATTN_PF_SK_FIXED_TENTHS
-#define MSATTN_PF_SK_FIXED_TENTHS 100
+#define MSATTN_PF_SK_FIXED_TENTHS 90
 #endif
-#ifndef MSATTN_PF_SK_MERGE_TENTHS
-#define MSATTN_PF_SK_MERGE_TENTHS 12
+#ifndef MSATTN_PF_ONE_FIXED_TENTHS
+#define MSATTN_PF_ONE_FIXED_TENTHS 40
 #endif
 constexpr int64_t kPfSkFixedTenths = MSATTN_PF_SK_FIXED_TENTHS;
-constexpr int64_t kPfSkMergeTenths = MSATTN_PF_SK_MERGE_TENTHS;
+constexpr int64_t kPfOneFixedTenths = MSATTN_PF_ONE_FIXED_TENTHS;
 #ifndef MSATTN_PF_SK_MIN_PAIRS
 #define MSATTN_PF_SK_MIN_PAIRS 4
 #endif
@@ -125,7 +124,7 @@ constexpr int64_t kPfSkMaxGroups = 256;  // workgroups of a stream-K prefill lau
 // multiple of 8 when it has at least 8, so that shares are dealt to the XCDs evenly; no
 // more than kPfSkMaxGroups; each share at least kPfSkMinPairs of the work list's key-step
 // pairs at the table capacity), or 0 where the geometry cannot take stream-K: not a
-// prefill the MFMA kernel's head sizes allow, or more tasks than tickets.
+// prefill the MFMA kernel's head sizes allow, or more tasks than its work-list table holds.
 int64_t prefill_sk_groups(int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
                           int max_context, int64_t cus) {
   if (kPfStreamK == 0 || q_len <= 1 || (head_dim != 64 && head_dim != 128)) return 0;
@@ -238,7 +237,15 @@ Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, i
   const int64_t pf_groups = prefill_sk_groups(batch, q_len, num_heads, num_kv_heads, head_dim,
                                               max_context, kPfSkMaxGroups);
   if (2 * pf_groups * kPfRows > L.slots) L.slots = 2 * pf_groups * kPfRows;
-  L.hdr_bytes = round256(sizeof(int) * (kHdrPrefix + static_cast<size_t>(batch) + 1));
+  // The header's prefix area: a stream-K decode's tiles per sequence (batch + 1 words), or a
+  // stream-K prefill's task offsets for its fold launch (tasks + 1).
+  size_t prefix_words = static_cast<size_t>(batch) + 1;
+  if (pf_groups > 0) {
+    const int64_t rows = static_cast<int64_t>(q_len) * (num_heads / num_kv_heads);
+    const size_t tasks = static_cast<size_t>((rows + kPfRows - 1) / kPfRows * num_kv_heads * batch);
+    if (tasks + 1 > prefix_words) prefix_words = tasks + 1;
+  }
+  L.hdr_bytes = round256(sizeof(int) * (kHdrPrefix + prefix_words));
   L.ml_bytes = round256(static_cast<size_t>(L.slots) * 2 * sizeof(float));
   L.acc_bytes = static_cast<size_t>(L.slots) * head_dim * sizeof(float);
   return L;
@@ -267,10 +274,9 @@ PfSkPlan prefill_sk_plan(int batch, int q_len, int num_heads, int num_kv_heads, 
   const int64_t tasks = (rows + kPfRows - 1) / kPfRows * num_kv_heads * batch;
   const int64_t rounds = (tasks + cus - 1) / cus;
   const int64_t P = std::max<int64_t>(1, ceil_div(ceil_div(max_context, kPfStep), 2));
-  // costs in tenths of a pair, times `tasks` (which divides the stream-K terms)
-  const int64_t one_cost = 10 * P * rounds * tasks;
-  const int64_t sk_cost = 10 * P * tasks * tasks / G + kPfSkFixedTenths * tasks +
-                          kPfSkMergeTenths * G;
+  // costs in tenths of a pair, times `tasks` (which divides the stream-K work term)
+  const int64_t one_cost = (10 * P * rounds + kPfOneFixedTenths) * tasks;
+  const int64_t sk_cost = 10 * P * tasks * tasks / G + kPfSkFixedTenths * tasks;
   if (kPfStreamK != 2 && 10 * sk_cost >= 9 * one_cost) return plan;
   const Layout L = workspace_layout(batch, q_len, num_heads, num_kv_heads, head_dim, max_context);
   const size_t ml_bytes = round256(static_cast<size_t>(2 * G * kPfRows) * 2 * sizeof(float));
@@ -923,9 +929,9 @@ int attention_impl(const void* query, const void* k_cache, const void* v_cache,
     if (tasks >= (int64_t(1) << 31) - kXcds) return MSATTN_ERR_UNSUPPORTED;
     pp.xcd_per = static_cast<int>((tasks + kXcds - 1) / kXcds);
     // Stream-K scheduling where the cost model prefers it (prefill_sk_plan): one workgroup
-    // per CU, each taking an equal share of all tasks' key-step pairs, a task split
-    // between shares merged by its last share; a ticket per task in the workspace header
-    // and two partial slots per workgroup after it.
+    // per CU, each taking an equal share of all tasks' key-step pairs; a task split
+    // between shares is merged by the fold launch that follows (the work list's task
+    // offsets in the workspace header, two partial slots per workgroup after it).
     pp.sk_groups = 0;
     const PfSkPlan sk = prefill_sk_plan(batch, q_len, num_heads, num_kv_heads, head_dim,
                                         max_context, workspace_bytes);
@@ -935,7 +941,7 @@ int attention_impl(const void* query, const void* k_cache, const void* v_cache,
       pp.ntasks = static_cast<int>(tasks);
       pp.sk_ml = reinterpret_cast<float*>(ws + sk.ml_offset);
       pp.sk_acc = reinterpret_cast<float*>(ws + sk.acc_offset);
-      pp.tickets = reinterpret_cast<int*>(ws) + kHdrTickets;
+      pp.sk_pre = reinterpret_cast<int*>(ws) + kHdrPrefix;
     }
     bool sup = false;
     const hipStream_t st = static_cast<hipStream_t>(stream);

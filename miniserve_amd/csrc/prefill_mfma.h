@@ -172,19 +172,16 @@ struct PrefillParams {
   // take equal contiguous shares of the work list (every task's key-step pairs, tasks in
   // order). A task split between workgroups has each share store an unnormalised partial
   // (m, l, acc) per row at slot 2 * share + (0: the share's first task, 1: its last);
-  // the last share to take the task's ticket folds them into the output.
+  // the fold launch that follows (prefill_sk_fold_kernel) merges them into the output.
   int sk_groups;
   int ntasks;         // rblocks * KVH * batch
   float* sk_ml;       // [2 * sk_groups][kPfRows][2]
   float* sk_acc;      // [2 * sk_groups][kPfRows][D]
-  int* tickets;       // one per task, zero before and after every launch
+  int* sk_pre;        // [ntasks + 1]: the work list's task offsets, written by workgroup 0
 };
 
 // Largest task count of a stream-K prefill launch (its work-list prefix sums sit in LDS).
 constexpr int kPfSkMaxTasks = 2048;
-// Cache-policy operand of a buffer load / store with SC1 set (gfx950: bit 4), the bit the
-// compiler sets on agent-scope atomic loads and stores.
-constexpr int kAuxSc1 = 16;
 
 // Geometry of one prefill task (sequence b, KV head, 128-row block; not the cascade's
 // PX tasks): its rows, context and the key range [lo_all, hi_all) its rows see, and the
@@ -260,7 +257,6 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   // tasks' counts, computed here from the context lengths, so the launch is capture-safe),
   // and this workgroup's share is [r_begin, r_end) of the list.
   __shared__ int s_skpre[PX ? 1 : kPfSkMaxTasks + 1];
-  __shared__ int s_last;
   const bool sk = !PX && p.sk_groups > 0;
   int r_begin = 0, r_end = 0, sk_task = 0, sk_share = 0;
   if constexpr (!PX) {
@@ -287,6 +283,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       }
       if (tid == kPfThreads - 1) s_skpre[p.ntasks] = excl;  // the list's length
       __syncthreads();
+      if (blockIdx.x == 0)  // for the fold launch
+        for (int t = tid; t <= p.ntasks; t += kPfThreads) p.sk_pre[t] = s_skpre[t];
       const unsigned i = blockIdx.x;
       // shares dealt to the XCDs in contiguous runs, as tasks are without stream-K
       sk_share = (MSATTN_PF_XCD && p.sk_groups % kXcds == 0)
@@ -297,7 +295,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       // all the task arithmetic that follows, in scalar registers)
       const int total = __builtin_amdgcn_readfirstlane(s_skpre[p.ntasks]);
       // Shares: no more than the list's length, so that every share holds work (a task's
-      // contributors are then consecutive shares, each taking its ticket); workgroups
+      // contributors are then consecutive shares, each storing a partial); workgroups
       // past them have none.
       pf_sk_range(sk_share, total, pf_sk_shares(p.sk_groups, total), &r_begin, &r_end);
       int lo = 0, hi = p.ntasks;  // the task holding r_begin: s_skpre[lo] <= r_begin < s_skpre[hi]
@@ -1121,22 +1119,17 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
         }
         continue;
       }
-      if (!full) {  // stream-K share of a split task: its unnormalised partial, device scope
+      if (!full) {  // stream-K share of a split task: its unnormalised partial
         if (row_ok[rb]) {
           const int rs = (2 * sk_share + (seg == 0 ? 0 : 1)) * kPfRows + (w * WROWS + rb * 16 + n);
-          if (g == 0) store2_device(p.sk_ml + static_cast<int64_t>(rs) * 2, M, l);
-          // 16-byte stores with cache policy SC1 (written through to the memory every XCD
-          // reads, as the agent-scope atomic stores are; half their transactions)
-          const __amdgpu_buffer_rsrc_t racc = tile_rsrc(p.sk_acc, 2 * p.sk_groups * kPfRows * D * 4);
+          if (g == 0) *reinterpret_cast<float2*>(p.sk_ml + static_cast<int64_t>(rs) * 2) = make_float2(M, l);
+          float* const pa = p.sk_acc + static_cast<int64_t>(rs) * D + 4 * g;
 #pragma unroll
           for (int t = 0; t < ND; ++t) {
             const float4 o1 = s_acc[(w * ND + t) * kWave + lane];
-            const mf_u32x4 v = {__float_as_uint(acc[rb][t][0] * a0 + o1.x * a1),
-                                __float_as_uint(acc[rb][t][1] * a0 + o1.y * a1),
-                                __float_as_uint(acc[rb][t][2] * a0 + o1.z * a1),
-                                __float_as_uint(acc[rb][t][3] * a0 + o1.w * a1)};
-            __builtin_amdgcn_raw_buffer_store_b128(v, racc, (rs * D + 16 * t + 4 * g) * 4, 0,
-                                                   kAuxSc1);
+            *reinterpret_cast<float4*>(pa + 16 * t) =
+                make_float4(acc[rb][t][0] * a0 + o1.x * a1, acc[rb][t][1] * a0 + o1.y * a1,
+                            acc[rb][t][2] * a0 + o1.z * a1, acc[rb][t][3] * a0 + o1.w * a1);
           }
         }
         continue;
@@ -1157,82 +1150,84 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       }
     }
   }
-  if constexpr (!PX) {
-    if (!full) {
-      // The share's partial is stored through to the memory every XCD reads (agent-scope
-      // stores, SC1) and acknowledged (s_waitcnt) in every thread before the barrier; then
-      // the task's ticket. The last of its shares to arrive reads every share's partial
-      // with agent-scope loads (after a barrier that follows the ticket's return), folds
-      // them (log-sum-exp, base 2) into the normalised output, and leaves the ticket at
-      // zero. The ordering argument is the partition decode's in-kernel merge's.
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      __syncthreads();
-      const int p0 = __builtin_amdgcn_readfirstlane(s_skpre[task]);
-      const int p1 = __builtin_amdgcn_readfirstlane(s_skpre[task + 1]);
-      const int total = __builtin_amdgcn_readfirstlane(s_skpre[p.ntasks]);
-      const int G = pf_sk_shares(p.sk_groups, total);
-      const int l_lo = pf_sk_owner(p0, total, G), l_hi = pf_sk_owner(p1 - 1, total, G);
-      if (tid == 0) {
-        int* t = p.tickets + task;
-        const int old = __hip_atomic_fetch_add(t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = old == l_hi - l_lo;
-        if (last) __hip_atomic_store(t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
-      }
-      __syncthreads();
-      if (s_last) {
-        constexpr int DPT = D / 4;  // dims per thread: 4 threads a row, 128 rows
-        static_assert(kPfThreads == 4 * kPfRows, "four threads per row of the task block");
-        const int r = tid >> 2;
-        const int d0 = (tid & 3) * DPT;
-        if (r < rows_here) {
-          float M = -INFINITY, L = 0.0f;
-          float a[DPT];
-#pragma unroll
-          for (int k = 0; k < DPT; ++k) a[k] = 0.0f;
-          // each contributor's (m, l) and acc slice requested together (one round trip per
-          // contributor), with agent-scope loads: SC1, which do not take a line from this
-          // XCD's L2 or this CU's L1
-          const __amdgpu_buffer_rsrc_t racc = tile_rsrc(p.sk_acc, 2 * p.sk_groups * kPfRows * D * 4);
-          for (int l = l_lo; l <= l_hi; ++l) {
-            const int rs = pf_sk_partial_slot(l, p0, total, G) * kPfRows + r;
-            const float2 ml = load2_device(p.sk_ml + static_cast<int64_t>(rs) * 2);
-            mf_u32x4 v[DPT / 4];
-#pragma unroll
-            for (int k = 0; k < DPT / 4; ++k)
-              v[k] = __builtin_amdgcn_raw_buffer_load_b128(racc, (rs * D + d0 + 4 * k) * 4, 0,
-                                                          kAuxSc1);
-            if (ml.x == -INFINITY) continue;  // no key of this row in that share
-            const float Mn = fmaxf(M, ml.x);
-            const float alpha = __builtin_amdgcn_exp2f(M - Mn);  // 0 while M = -inf
-            const float beta = __builtin_amdgcn_exp2f(ml.x - Mn);
-            L = L * alpha + ml.y * beta;
-#pragma unroll
-            for (int k = 0; k < DPT / 4; ++k) {
-              a[4 * k] = a[4 * k] * alpha + __uint_as_float(v[k].x) * beta;
-              a[4 * k + 1] = a[4 * k + 1] * alpha + __uint_as_float(v[k].y) * beta;
-              a[4 * k + 2] = a[4 * k + 2] * alpha + __uint_as_float(v[k].z) * beta;
-              a[4 * k + 3] = a[4 * k + 3] * alpha + __uint_as_float(v[k].w) * beta;
-            }
-            M = Mn;
-          }
-          const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-          const int row = row0 + r;
-          const int i = row / p.G;
-          const int64_t orow =
-              (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
-          T* op = static_cast<T*>(p.out) + orow * D + d0;
-#pragma unroll
-          for (int k = 0; k < DPT; k += 4)
-            *reinterpret_cast<uint2*>(op + k) = make_uint2(Pack2<T>::pack(a[k] * inv, a[k + 1] * inv),
-                                                           Pack2<T>::pack(a[k + 2] * inv, a[k + 3] * inv));
-        }
-      }
-    }
-  }
   __syncthreads();  // this task's LDS reads are done before the next task's copies
   }  // task loop
 }
+// The stream-K schedule's fold launch: for each task split between shares, the merge of
+// its shares' partials (m_j, l_j, acc_j) per row into the normalised output, with
+// M = max m_j and w_j = 2^(m_j - M): out = sum_j w_j acc_j / sum_j w_j l_j (partials with
+// m = -inf carry no weight; a row with no key at all gets zeros). A workgroup takes
+// kPfFoldRows(D) rows of one task, D / 4 threads a row, 4 dims a thread, so that the
+// partials of a task are read by many CUs at once. Tasks one share took whole were written
+// by the prefill kernel; their workgroups return at once.
+constexpr int kPfFoldThreads = 256;
+template <int D>
+constexpr int pf_fold_rows() { return kPfFoldThreads / (D / 4); }
+
+template <typename T, int D>
+__global__ __launch_bounds__(kPfFoldThreads) void prefill_sk_fold_kernel(const PrefillParams p) {
+  constexpr int TPR = D / 4;                    // threads per row
+  constexpr int FR = pf_fold_rows<D>();         // rows per workgroup
+  constexpr int PER_TASK = kPfRows / FR;        // workgroups per task
+  static_assert(kWave % TPR == 0 && kPfRows % FR == 0, "a row's threads in one wave");
+  const unsigned task = blockIdx.x / PER_TASK;
+  if (task >= static_cast<unsigned>(p.ntasks)) return;
+  const int p0 = p.sk_pre[task], p1 = p.sk_pre[task + 1], total = p.sk_pre[p.ntasks];
+  if (p1 <= p0 || total <= 0) return;
+  const int G = pf_sk_shares(p.sk_groups, total);
+  const int l_lo = pf_sk_owner(p0, total, G), l_hi = pf_sk_owner(p1 - 1, total, G);
+  if (l_lo == l_hi) return;  // one share's: written whole
+  const unsigned per_b = static_cast<unsigned>(p.rblocks) * static_cast<unsigned>(p.KVH);
+  const int b = static_cast<int>(task / per_b);
+  const unsigned bx = task - static_cast<unsigned>(b) * per_b;
+  const int rblock = p.rblocks - 1 - static_cast<int>(bx % static_cast<unsigned>(p.rblocks));
+  const int kvh = static_cast<int>(bx / static_cast<unsigned>(p.rblocks));
+  const int row0 = rblock * kPfRows;
+  const int rows_here = min(kPfRows, p.rows_per_kvh - row0);
+  const int j = static_cast<int>(threadIdx.x) % TPR;
+  const int r = static_cast<int>(blockIdx.x % PER_TASK) * FR + static_cast<int>(threadIdx.x) / TPR;
+  if (r >= rows_here) return;  // (the row's TPR threads leave together)
+  // The row's M and L: thread j takes shares l_lo + j, l_lo + j + TPR, ...; then the row's
+  // threads combine theirs.
+  float M = -INFINITY, L = 0.0f;
+  for (int l = l_lo + j; l <= l_hi; l += TPR) {
+    const int rs = pf_sk_partial_slot(l, p0, total, G) * kPfRows + r;
+    const float2 ml = *reinterpret_cast<const float2*>(p.sk_ml + static_cast<int64_t>(rs) * 2);
+    if (ml.x == -INFINITY) continue;  // no key of this row in that share
+    const float Mn = fmaxf(M, ml.x);
+    L = L * __builtin_amdgcn_exp2f(M - Mn) + ml.y * __builtin_amdgcn_exp2f(ml.x - Mn);
+    M = Mn;  // (2^(M - Mn) is 0 while M = -inf)
+  }
+#pragma unroll
+  for (int o = 1; o < TPR; o <<= 1) {
+    const float Mo = __shfl_xor(M, o, kWave);
+    const float Lo = __shfl_xor(L, o, kWave);
+    const float Mn = fmaxf(M, Mo);
+    if (Mn != -INFINITY) {
+      L = L * __builtin_amdgcn_exp2f(M - Mn) + Lo * __builtin_amdgcn_exp2f(Mo - Mn);
+      M = Mn;
+    }
+  }
+  float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+  for (int l = l_lo; l <= l_hi; ++l) {
+    const int64_t rs = static_cast<int64_t>(pf_sk_partial_slot(l, p0, total, G)) * kPfRows + r;
+    const float m = p.sk_ml[rs * 2];
+    const float4 v = *reinterpret_cast<const float4*>(p.sk_acc + rs * D + 4 * j);
+    const float w = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+    a.x = fmaf(v.x, w, a.x);
+    a.y = fmaf(v.y, w, a.y);
+    a.z = fmaf(v.z, w, a.z);
+    a.w = fmaf(v.w, w, a.w);
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  const int row = row0 + r;
+  const int i = row / p.G;
+  const int64_t orow = (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
+  *reinterpret_cast<uint2*>(static_cast<T*>(p.out) + orow * D + 4 * j) =
+      make_uint2(Pack2<T>::pack(a.x * inv, a.y * inv), Pack2<T>::pack(a.z * inv, a.w * inv));
+}
+
 template <typename T, typename KT>
 hipError_t launch_prefill_mfma_impl(const PrefillParams& p, int D, hipStream_t stream,
                                     bool* supported) {
@@ -1245,6 +1240,18 @@ hipError_t launch_prefill_mfma_impl(const PrefillParams& p, int D, hipStream_t s
   else
     hipLaunchKernelGGL((prefill_mfma_kernel<T, KT, 64, kPfRB, false>), grid, dim3(kPfThreads), 0,
                        stream, p);
+  if (p.sk_groups > 0) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (D == 128)
+      hipLaunchKernelGGL((prefill_sk_fold_kernel<T, 128>),
+                         dim3(static_cast<unsigned>(p.ntasks * (kPfRows / pf_fold_rows<128>()))),
+                         dim3(kPfFoldThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((prefill_sk_fold_kernel<T, 64>),
+                         dim3(static_cast<unsigned>(p.ntasks * (kPfRows / pf_fold_rows<64>()))),
+                         dim3(kPfFoldThreads), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

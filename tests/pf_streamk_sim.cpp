@@ -3,10 +3,11 @@
 // sizes and workgroup counts, every workgroup's segment loop is run as the kernel runs it,
 // and the result is checked:
 //   - every work-list position is taken by exactly one share;
-//   - a task covered by one share is written whole (no partial, no ticket);
-//   - a split task's partial slots are exactly the slots its merger reads, each slot is
-//     written once in the launch, and the number of its partials equals the ticket count
-//     at which the merger folds them (l_hi - l_lo + 1).
+//   - a task covered by one share is written whole (no partial), and the fold launch
+//     skips it (its first and last contributors are one share);
+//   - a split task's partial slots are exactly the slots the fold launch reads, each slot
+//     is written once in the launch, and the number of its partials is the contributor
+//     count the fold reads (l_hi - l_lo + 1, more than one).
 // Built with g++ and run by tests/test_pf_streamk.py:
 //   pf_streamk_sim <trials> <mode>   mode 1 plants a mistake: shares = groups unclamped.
 // Prints "violations trials_with_splits" and exits 0.
@@ -36,7 +37,7 @@ int main(int argc, char** argv) {
     const int total = P[ntasks];
     const int groups = static_cast<int>(pick(1, 320));
     const int shares = mode == 1 ? groups : msattn::pf_sk_shares(groups, total);
-    std::vector<int> taken(total, 0), full(ntasks, 0), tickets(ntasks, 0);
+    std::vector<int> taken(total, 0), full(ntasks, 0), parts(ntasks, 0);
     std::vector<std::vector<int>> written(ntasks);
     std::vector<int> slot_writes(2 * groups, 0);
     bool split = false;
@@ -69,7 +70,7 @@ int main(int argc, char** argv) {
           const int slot = 2 * l + (seg == 0 ? 0 : 1);
           written[t].push_back(slot);
           slot_writes[slot]++;
-          tickets[t]++;
+          parts[t]++;
           split = true;
         }
       }
@@ -80,6 +81,9 @@ int main(int argc, char** argv) {
     for (int t = 0; t < ntasks; ++t) {
       if (full[t]) {
         violations += full[t] != 1 || !written[t].empty();
+        // the fold launch's test: one contributor, nothing to fold
+        violations += msattn::pf_sk_owner(P[t], total, shares) !=
+                      msattn::pf_sk_owner(P[t + 1] - 1, total, shares);
         continue;
       }
       if (written[t].empty()) {  // nobody wrote this task's output
@@ -88,7 +92,7 @@ int main(int argc, char** argv) {
       }
       const int l_lo = msattn::pf_sk_owner(P[t], total, shares);
       const int l_hi = msattn::pf_sk_owner(P[t + 1] - 1, total, shares);
-      if (tickets[t] != l_hi - l_lo + 1) ++violations;  // the merger never runs, or early
+      if (parts[t] != l_hi - l_lo + 1 || l_lo == l_hi) ++violations;  // a part unread, or none folded
       std::set<int> reads;
       for (int l = l_lo; l <= l_hi; ++l) reads.insert(msattn::pf_sk_partial_slot(l, P[t], total, shares));
       const std::set<int> wrote(written[t].begin(), written[t].end());

@@ -256,7 +256,8 @@ def route(B, q_len, H, KVH, D, ctx, qd=nat.BF16, kvd=None, ws=None, slot_stride=
     # prefill tasks scheduled stream-K where one task per CU leaves CUs idle long enough
     ((1, 128, 32, 8, 128, 8192), nat.ROUTE_PREFILL_STREAMK),   # 32 tasks of 64 key-step pairs
     ((2, 384, 32, 8, 128, 4096), nat.ROUTE_PREFILL),           # 192 tasks: one round
-    ((4, 128, 32, 8, 128, 2048), nat.ROUTE_PREFILL),           # 128 tasks of 16 pairs
+    ((4, 128, 32, 8, 128, 2048), nat.ROUTE_PREFILL_STREAMK),   # 128 tasks of 16 pairs
+    ((2, 512, 28, 4, 128, 4608), nat.ROUTE_PREFILL),           # 224 tasks of 36 pairs
     # stream-K thresholds: 2^16 table tiles at head_dim 128, 2^17 at head_dim 64
     ((64, 1, 32, 8, 128, 8158), nat.ROUTE_STREAMK),            # C3 called with max(lens)
     ((16, 1, 32, 8, 128, 8192), nat.ROUTE_STREAMK),            # 65,536 tiles

@@ -71,6 +71,7 @@ def run_hip(device, q, kc, vc, table, lens, **kw):
 # partition kernels, 1 stream-K, 2 the partition kernel merging in-kernel); the prefill
 # kernel leaves it untouched (its stream-K schedule uses only the tickets and partials).
 _SENTINEL = 0x5EED
+_SK = "prefill stream-K"
 _KIND_OF_ROUTE = {"prefill": _SENTINEL, "prefill stream-K": _SENTINEL, "partition-fused": 2,
                   "partition": 0, "generic": 0, "stream-K": 1}
 
@@ -898,12 +899,12 @@ def test_streamk_graph_replays(device):
     (32, 8, 128, 64, [64, 700], torch.float16, True, None, "prefill"),
     (8, 8, 128, 80, [80, 150], torch.bfloat16, False, None, "prefill"),       # non-causal
     (28, 4, 128, 200, [1200, 300], torch.bfloat16, True, 128, "prefill"),     # sliding window
-    (16, 2, 128, 80, [50, 2000], torch.bfloat16, True, None, "prefill"),      # context shorter than the chunk
+    (16, 2, 128, 80, [50, 2000], torch.bfloat16, True, None, _SK),            # context shorter than the chunk
     # head_dim 64 (Qwen2.5-0.5B geometry): a staging pass spans two 16-token tiles
-    (14, 2, 64, 512, [2560, 600], torch.bfloat16, True, None, "prefill"),
-    (14, 2, 64, 37, [37, 1500, 90], torch.float16, True, 100, "prefill"),
+    (14, 2, 64, 512, [2560, 600], torch.bfloat16, True, None, _SK),
+    (14, 2, 64, 37, [37, 1500, 90], torch.float16, True, 100, _SK),
     (8, 8, 64, 72, [72, 333], torch.bfloat16, False, None, "prefill"),        # non-causal
-    (14, 2, 64, 37, [37, 1500, 90], torch.bfloat16, True, None, "prefill"),
+    (14, 2, 64, 37, [37, 1500, 90], torch.bfloat16, True, None, _SK),
     # few pairs, at most 64 rows per KV head: the partition kernel's 16-row tiles
     (8, 8, 128, 33, [33, 90], torch.bfloat16, False, None, "partition-fused"),
     (8, 8, 64, 40, [40, 333], torch.bfloat16, False, None, "partition-fused"),
@@ -928,8 +929,6 @@ def test_prefill_mfma(device, H, KVH, D, q_len, lens, dtype, causal, window, rou
             assert not out[b, : q_len - L].any()
 
 
-_SK = "prefill stream-K"
-
 
 @pytest.mark.parametrize("B,H,KVH,D,q_len,lo,hi,dtype,kv_dtype,want", [
     # 16 tasks of ~94 key-step pairs over 256 workgroups: every task split over ~16 shares
@@ -948,11 +947,11 @@ _SK = "prefill stream-K"
 def test_prefill_stream_k_schedule(device, B, H, KVH, D, q_len, lo, hi, dtype, kv_dtype,
                                    want):
     """The prefill kernel's stream-K schedule (one workgroup per CU, each an equal share of
-    all tasks' key-step pairs; a task split between shares merged in-kernel by the last to
-    take its ticket), which the cost model picks for launches that would leave CUs idle,
-    against the float64 oracle: tasks over many shares, shares over two tasks, the staged
-    (fp8) path, and a launch of one task per CU (no stream-K); three calls in a row on one
-    workspace (the tickets must come back to zero)."""
+    all tasks' key-step pairs; a task split between shares merged by the fold launch that
+    follows), which the cost model picks for launches that would leave CUs idle, against
+    the float64 oracle: tasks over many shares, shares over two tasks, the staged (fp8)
+    path, and a launch of one task per CU (no stream-K); three calls in a row on one
+    workspace (whose ticket area, which the decode kernels use, stays at zero)."""
     g = torch.Generator().manual_seed(B * q_len + H)
     lens = [int(x) for x in torch.randint(lo, hi + 1, (B,), generator=g)]
     lens = [max(L, q_len) for L in lens]
@@ -972,7 +971,7 @@ def test_prefill_stream_k_schedule(device, B, H, KVH, D, q_len, lo, hi, dtype, k
         out = paged_attention(qd, kc.to(device), vc.to(device), table, lens,
                               max_context=width * 16, workspace=ws)
         torch.cuda.synchronize()
-        assert not ws[:(64 + 4096) * 4].view(torch.int32)[64:].any(), "tickets not back at zero"
+        assert not ws[:(64 + 4096) * 4].view(torch.int32)[64:].any(), "tickets not at zero"
         ref = dense.paged_attention_f64(q, kc, vc, table, lens, kv_cast=True)
         err = rel_err(out, ref)
         note(f"stream-K prefill max-rel {err:.3e}")
