@@ -238,12 +238,12 @@ Layout workspace_layout(int batch, int q_len, int num_heads, int num_kv_heads, i
                                               max_context, kPfSkMaxGroups);
   if (2 * pf_groups * kPfRows > L.slots) L.slots = 2 * pf_groups * kPfRows;
   // The header's prefix area: a stream-K decode's tiles per sequence (batch + 1 words), or a
-  // stream-K prefill's task offsets for its fold launch (tasks + 1).
+  // stream-K prefill's task offsets and head size for its fold launch (tasks + 2).
   size_t prefix_words = static_cast<size_t>(batch) + 1;
   if (pf_groups > 0) {
     const int64_t rows = static_cast<int64_t>(q_len) * (num_heads / num_kv_heads);
     const size_t tasks = static_cast<size_t>((rows + kPfRows - 1) / kPfRows * num_kv_heads * batch);
-    if (tasks + 1 > prefix_words) prefix_words = tasks + 1;
+    if (tasks + 2 > prefix_words) prefix_words = tasks + 2;
   }
   L.hdr_bytes = round256(sizeof(int) * (kHdrPrefix + prefix_words));
   L.ml_bytes = round256(static_cast<size_t>(L.slots) * 2 * sizeof(float));

@@ -40,8 +40,8 @@ MSATTN_SK_HD inline int pf_sk_owner(int x, int total, int shares) {
   return static_cast<int>((static_cast<int64_t>(x + 1) * shares - 1) / total);
 }
 
-// The slot of share l's partial of the task that starts at position p0: its first task's
-// slot unless the share began in an earlier task.
+// The slot of share l's partial of the task whose entry in the list (its head included)
+// starts at position p0: its first task's slot unless the share began in an earlier task.
 MSATTN_SK_HD inline int pf_sk_partial_slot(int l, int p0, int total, int shares) {
   const bool began_before = static_cast<int64_t>(l) * total / shares < p0;
   return 2 * l + (began_before ? 1 : 0);

@@ -177,11 +177,22 @@ struct PrefillParams {
   int ntasks;         // rblocks * KVH * batch
   float* sk_ml;       // [2 * sk_groups][kPfRows][2]
   float* sk_acc;      // [2 * sk_groups][kPfRows][D]
-  int* sk_pre;        // [ntasks + 1]: the work list's task offsets, written by workgroup 0
+  int* sk_pre;        // [ntasks + 2]: the work list's task offsets and its head size,
+                      // written by workgroup 0
 };
 
 // Largest task count of a stream-K prefill launch (its work-list prefix sums sit in LDS).
 constexpr int kPfSkMaxTasks = 2048;
+// Positions of the stream-K work list ahead of each task's key-step pairs that hold no work
+// (a head): a share whose range takes a task's start past its own pays a second task start
+// and end (context length, table window, first copies; the key groups' merge and stores),
+// and the head gives it that much less of the pairs, so that the shares end together.
+// Where every task boundary already falls on a share boundary (equal shares of whole tasks,
+// or tasks of whole shares), no share holds a second start and the list has no heads.
+#ifndef MSATTN_PF_SK_HEAD
+#define MSATTN_PF_SK_HEAD 3
+#endif
+constexpr int kPfSkHead = MSATTN_PF_SK_HEAD;
 
 // Geometry of one prefill task (sequence b, KV head, 128-row block; not the cascade's
 // PX tasks): its rows, context and the key range [lo_all, hi_all) its rows see, and the
@@ -258,7 +269,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   // and this workgroup's share is [r_begin, r_end) of the list.
   __shared__ int s_skpre[PX ? 1 : kPfSkMaxTasks + 1];
   const bool sk = !PX && p.sk_groups > 0;
-  int r_begin = 0, r_end = 0, sk_task = 0, sk_share = 0;
+  int r_begin = 0, r_end = 0, sk_task = 0, sk_share = 0, sk_head = 0;
   if constexpr (!PX) {
     if (sk) {
       constexpr int kPer = (kPfSkMaxTasks + kPfThreads - 1) / kPfThreads;
@@ -282,9 +293,36 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
         excl += cnt[k];
       }
       if (tid == kPfThreads - 1) s_skpre[p.ntasks] = excl;  // the list's length
+      if (tid == 0) s_pg[kPfThreads / kWave] = 1;  // every boundary on a share boundary, so far
       __syncthreads();
-      if (blockIdx.x == 0)  // for the fold launch
+      {
+        // Heads unless every task boundary sits on a share boundary of the list without them.
+        const int total0 = s_skpre[p.ntasks];
+        const int shares0 = pf_sk_shares(p.sk_groups, total0);
+        const int q = shares0 > 0 && total0 % shares0 == 0 ? total0 / shares0 : 0;
+        bool off = q == 0;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int t = tid * kPer + k;
+          if (t < p.ntasks && q > 0) off = off || s_skpre[t] % q != 0;
+        }
+        if (off) s_pg[kPfThreads / kWave] = 0;  // (any writer stores the same value)
+        __syncthreads();
+        sk_head = s_pg[kPfThreads / kWave] ? 0 : kPfSkHead;
+        if (sk_head > 0) {
+#pragma unroll
+          for (int k = 0; k < kPer; ++k) {
+            const int t = tid * kPer + k;
+            if (t < p.ntasks) s_skpre[t] += sk_head * t;
+          }
+          if (tid == kPfThreads - 1) s_skpre[p.ntasks] += sk_head * p.ntasks;
+        }
+        __syncthreads();
+      }
+      if (blockIdx.x == 0) {  // for the fold launch: the list, then the head size
         for (int t = tid; t <= p.ntasks; t += kPfThreads) p.sk_pre[t] = s_skpre[t];
+        if (tid == 0) p.sk_pre[p.ntasks + 1] = sk_head;
+      }
       const unsigned i = blockIdx.x;
       // shares dealt to the XCDs in contiguous runs, as tasks are without stream-K
       sk_share = (MSATTN_PF_XCD && p.sk_groups % kXcds == 0)
@@ -334,9 +372,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     const unsigned per_b = static_cast<unsigned>(p.rblocks) * static_cast<unsigned>(p.KVH);
     if (sk) {
       if (sk_task >= p.ntasks || r_begin >= r_end) break;
-      const int p0 = __builtin_amdgcn_readfirstlane(s_skpre[sk_task]);
+      // the task's pairs: positions p0 .. p1 - 1, after its head
+      const int p0 = __builtin_amdgcn_readfirstlane(s_skpre[sk_task]) + sk_head;
       const int p1 = __builtin_amdgcn_readfirstlane(s_skpre[sk_task + 1]);
-      if (p0 >= r_end) break;
+      if (p0 >= r_end) break;  // the share ends before (or in the head of) this task
       it_lo = r_begin > p0 ? r_begin - p0 : 0;
       it_hi = (r_end < p1 ? r_end : p1) - p0;
       full = it_lo == 0 && it_hi == p1 - p0;
@@ -1172,7 +1211,9 @@ __global__ __launch_bounds__(kPfFoldThreads) void prefill_sk_fold_kernel(const P
   static_assert(kWave % TPR == 0 && kPfRows % FR == 0, "a row's threads in one wave");
   const unsigned task = blockIdx.x / PER_TASK;
   if (task >= static_cast<unsigned>(p.ntasks)) return;
-  const int p0 = p.sk_pre[task], p1 = p.sk_pre[task + 1], total = p.sk_pre[p.ntasks];
+  // the task's head starts at pv, its pairs at p0 (the shares' partial slots count from pv)
+  const int pv = p.sk_pre[task], p1 = p.sk_pre[task + 1], total = p.sk_pre[p.ntasks];
+  const int p0 = pv + p.sk_pre[p.ntasks + 1];
   if (p1 <= p0 || total <= 0) return;
   const int G = pf_sk_shares(p.sk_groups, total);
   const int l_lo = pf_sk_owner(p0, total, G), l_hi = pf_sk_owner(p1 - 1, total, G);
@@ -1191,7 +1232,7 @@ __global__ __launch_bounds__(kPfFoldThreads) void prefill_sk_fold_kernel(const P
   // threads combine theirs.
   float M = -INFINITY, L = 0.0f;
   for (int l = l_lo + j; l <= l_hi; l += TPR) {
-    const int rs = pf_sk_partial_slot(l, p0, total, G) * kPfRows + r;
+    const int rs = pf_sk_partial_slot(l, pv, total, G) * kPfRows + r;
     const float2 ml = *reinterpret_cast<const float2*>(p.sk_ml + static_cast<int64_t>(rs) * 2);
     if (ml.x == -INFINITY) continue;  // no key of this row in that share
     const float Mn = fmaxf(M, ml.x);
@@ -1211,7 +1252,7 @@ __global__ __launch_bounds__(kPfFoldThreads) void prefill_sk_fold_kernel(const P
   float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 4
   for (int l = l_lo; l <= l_hi; ++l) {
-    const int64_t rs = static_cast<int64_t>(pf_sk_partial_slot(l, p0, total, G)) * kPfRows + r;
+    const int64_t rs = static_cast<int64_t>(pf_sk_partial_slot(l, pv, total, G)) * kPfRows + r;
     const float m = p.sk_ml[rs * 2];
     const float4 v = *reinterpret_cast<const float4*>(p.sk_acc + rs * D + 4 * j);
     const float w = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);

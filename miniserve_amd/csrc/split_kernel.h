@@ -54,7 +54,8 @@ constexpr int kPartMax = MSATTN_PART_MAX;
 //   kind 1 also: hdr[1] sumT, [2] chunk c, [3] sub-ranges, [4] UG, [5] NUG, [6] B,
 //   [7] RT, and hdr[kHdrPrefix + b] = tiles of sequences before b (b = 0..B).
 //   A chunked prefill on the prefill kernel's stream-K schedule writes hdr[kHdrPrefix + t]
-//   = key-step pairs of its tasks before t (t = 0..tasks) for its fold launch.
+//   = work-list offset of task t (t = 0..tasks) and hdr[kHdrPrefix + tasks + 1] = the
+//   list's head size, for its fold launch.
 //   kinds 0 and 2 (partition kernels) also: hdr[8] partition tokens, [9] waves per
 //   workgroup, [14] workgroups a CU may hold (the launch's shape, for tests and
 //   measurements; the merge does not read them).

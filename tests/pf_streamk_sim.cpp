@@ -1,8 +1,9 @@
 // CPU simulation of the chunked-prefill kernel's stream-K schedule
 // (miniserve_amd/csrc/pf_streamk.h and the task loop of prefill_mfma.h): for random task
 // sizes and workgroup counts, every workgroup's segment loop is run as the kernel runs it,
-// and the result is checked:
-//   - every work-list position is taken by exactly one share;
+// and the result is checked (each task's entry in the list is a head of `head` positions
+// that hold no work, then its pairs):
+//   - every pair position is taken by exactly one share, no head position by any;
 //   - a task covered by one share is written whole (no partial), and the fold launch
 //     skips it (its first and last contributors are one share);
 //   - a split task's partial slots are exactly the slots the fold launch reads, each slot
@@ -30,9 +31,10 @@ int main(int argc, char** argv) {
     const int ntasks = static_cast<int>(pick(1, 300));
     std::vector<int> P(ntasks + 1, 0);
     const int kind = static_cast<int>(pick(0, 2));
+    const int head = static_cast<int>(pick(0, 4));
     for (int t = 0; t < ntasks; ++t) {
       const int c = kind == 0 ? 1 : static_cast<int>(kind == 1 ? pick(1, 4) : pick(1, 200));
-      P[t + 1] = P[t] + c;
+      P[t + 1] = P[t] + head + c;
     }
     const int total = P[ntasks];
     const int groups = static_cast<int>(pick(1, 320));
@@ -59,7 +61,7 @@ int main(int argc, char** argv) {
       }
       for (int t = lo, seg = 0;; ++t, ++seg) {
         if (t >= ntasks || rb >= re) break;
-        const int p0 = P[t], p1 = P[t + 1];
+        const int p0 = P[t] + head, p1 = P[t + 1];
         if (p0 >= re) break;
         const int it_lo = rb > p0 ? rb - p0 : 0;
         const int it_hi = std::min(re, p1) - p0;
@@ -76,13 +78,14 @@ int main(int argc, char** argv) {
       }
     }
     with_splits += split;
-    for (int x = 0; x < total; ++x) violations += taken[x] != 1;
+    for (int t = 0; t < ntasks; ++t)
+      for (int x = P[t]; x < P[t + 1]; ++x) violations += taken[x] != (x >= P[t] + head ? 1 : 0);
     for (int s : slot_writes) violations += s > 1;
     for (int t = 0; t < ntasks; ++t) {
       if (full[t]) {
         violations += full[t] != 1 || !written[t].empty();
         // the fold launch's test: one contributor, nothing to fold
-        violations += msattn::pf_sk_owner(P[t], total, shares) !=
+        violations += msattn::pf_sk_owner(P[t] + head, total, shares) !=
                       msattn::pf_sk_owner(P[t + 1] - 1, total, shares);
         continue;
       }
@@ -90,7 +93,7 @@ int main(int argc, char** argv) {
         ++violations;
         continue;
       }
-      const int l_lo = msattn::pf_sk_owner(P[t], total, shares);
+      const int l_lo = msattn::pf_sk_owner(P[t] + head, total, shares);
       const int l_hi = msattn::pf_sk_owner(P[t + 1] - 1, total, shares);
       if (parts[t] != l_hi - l_lo + 1 || l_lo == l_hi) ++violations;  // a part unread, or none folded
       std::set<int> reads;
