@@ -1,32 +1,34 @@
 // Chunked-prefill paged attention on MFMA (gfx950): q_len > 1, bf16/fp16 query (over a
 // cache of its type or of fp8 e4m3), head_dim 64 or 128.
 //
-// One workgroup owns 16 * RB * 4 query rows of one (sequence b, KV head): rows are the
-// (query token i, GQA head g) pairs r = i * group + g. It has two groups of 4 waves, one
-// wave of each group per SIMD: both groups hold the same rows (each wave RB blocks of 16
-// rows, so every K/V operand it reads from LDS feeds RB MFMAs) and split the keys, group 0
-// taking the even 64-token steps and group 1 the odd ones; the two running (m, l, O) are
-// merged through LDS at the end. With two waves per SIMD, one wave's softmax and LDS
-// traffic overlap the other's MFMAs. Per group and step:
-//   * K and V of the step are staged through the group's LDS buffers, double-buffered:
-//     while a step is computed from one buffer, the group's next step (loaded into
-//     registers one pair of steps ahead) goes into the other; one barrier per step pair;
-//   * S^T = K Q^T on v_mfma_f32_16x16x32: A = K rows read from LDS, B = the wave's query
-//     rows kept in registers, so lane (g = l/16, n = l%16) holds the scores of query row n
-//     for tokens 4g .. 4g+3 of each 16-token slice;
+// One workgroup owns 128 query rows of one (sequence b, KV head): rows are the (query
+// token i, GQA head g) pairs r = i * group + g. It has two groups of 4 waves, one wave of
+// each group per SIMD: both groups hold the same rows (32 per wave, one 32-row MFMA
+// block, so every K/V operand it reads from LDS feeds a 32-row product) and split the
+// keys, group 0 taking the even 64-token steps and group 1 the odd ones; the two running
+// (m, l, O) are merged through LDS at the end. With two waves per SIMD, one wave's softmax
+// and LDS traffic overlap the other's MFMAs. Per group and step:
+//   * K and V of the step are staged through the group's LDS buffers, double-buffered
+//     (copied there by the load unit for a cache of the query's type, through registers
+//     for the converted caches); one barrier per step pair;
+//   * S^T = K Q^T on v_mfma_f32_32x32x16, one 32-key tile at a time: A = K rows read from
+//     LDS, B = the wave's query rows kept in registers, so lane (cc = l % 32, hh = l / 32)
+//     holds the scores of query row cc for keys (v & 3) + 8 (v >> 2) + 4 hh of the tile
+//     in register v. The longer MFMA (32 cycles, half as many per step as 16x16x32) leaves
+//     more issue slots between MFMAs for the softmax's VALU work (a standalone probe with
+//     two waves per SIMD: 810 -> 688 cycles for the same MFMA and VALU work);
 //   * online softmax per row (fp32, base 2), causal / window masks only on the steps that
-//     cross a row's key range;
-//   * O^T += V^T P^T on the same MFMA: B = P^T comes straight from the score registers,
-//     A = V^T is read transposed from the row-major V rows with ds_read_b64_tr_b16 (each
-//     lane names 4 dims of one token; lane i of a 16-lane group receives dim i of four
-//     tokens). Lane (g, n) accumulates O[row n][dims 16t + 4g + r], so the softmax
-//     rescale stays in the lane.
-// LDS row strides are chosen per access: K rows are D + 8 elements apart (68 dwords for
-// head_dim 128, 4 mod 64 banks; 36 for 64: 36 n mod 64 takes 16 distinct multiples of 4),
-// so the 16 rows of a 16-byte-per-lane read fall on disjoint banks; V rows D + 16 (72
-// dwords, 8 mod 64; or 40), so the 8-byte transposed reads of 8 consecutive rows tile the
-// 64 banks.
-// The rows' outputs are normalised and written directly (no split-K partials).
+//     cross a row's key range; a row's keys are split over the two lane halves;
+//   * O^T += V^T P^T on the same MFMA, in 16-key chunks: B = P^T comes straight from the
+//     score registers (registers 8 c .. 8 c + 7 are chunk c's keys 4 hh .. + 3 and
+//     8 + 4 hh .. + 3), A = V^T is read transposed from the row-major V rows with
+//     ds_read_b64_tr_b16 (each lane names 4 dims of one token; lane i of a 16-lane group
+//     receives dim i of four tokens), so lane (cc, hh) accumulates O[row cc][dims
+//     32 t + (v & 3) + 8 (v >> 2) + 4 hh] and the softmax rescale stays in the lane.
+// LDS rows of copied K/V are unpadded with a 16-byte chunk swizzle; the register-staged
+// rows are padded (K rows D + 8 elements apart, V rows D + 16).
+// A task's rows are normalised and written directly, or, on the stream-K schedule, left as
+// partials for the fold launch when the task is split between workgroups.
 //
 // Semantics: PagedAttention.forward with q_len > 1 (miniserve/attention.py:205-250,
 // mask :135-153; the trailing query positions q_pos = len - q_len + i, :146).
@@ -49,7 +51,7 @@
 #define MSATTN_PF_SCHED 1
 #endif
 #ifndef MSATTN_PF_NV
-#define MSATTN_PF_NV 5
+#define MSATTN_PF_NV 3
 #endif
 // Wave priority of key group 1 over its loop (copy path).
 #ifndef MSATTN_PF_G1PRIO
@@ -64,11 +66,53 @@
 
 namespace msattn {
 
+typedef float mf_f32x16 __attribute__((ext_vector_type(16)));
+// One 32x32x16 MFMA: C[32 x 32] += A[32 x 16] B[16 x 32]. Lane l holds A's row l % 32 and
+// B's column l % 32, elements k = 8 (l / 32) .. + 7 of each; and C's column l % 32, rows
+// (v & 3) + 8 (v >> 2) + 4 (l / 32) in its registers v = 0 .. 15.
+template <typename T> struct Mfma32;
+template <> struct Mfma32<bf16_t> {
+  __device__ static mf_f32x16 mac(const uint4& a, const uint4& b, mf_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mf_bf16x8, a),
+                                                   __builtin_bit_cast(mf_bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma32<_Float16> {
+  __device__ static mf_f32x16 mac(const uint4& a, const uint4& b, mf_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mf_f16x8, a),
+                                                  __builtin_bit_cast(mf_f16x8, b), c, 0, 0, 0);
+  }
+};
+__device__ __forceinline__ mf_f32x16 zero16() {
+  mf_f32x16 z;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) z[e] = 0.0f;
+  return z;
+}
+// Max / sum over the two 32-lane halves of the wave (lanes i and i + 32), every lane
+// receiving it (v_permlane32_swap; with MSATTN_ROW_SWAPS=0 a lane shuffle).
+__device__ __forceinline__ float halves_max(float v) {
+#if MSATTN_ROW_SWAPS
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+#else
+  return fmaxf(v, __shfl_xor(v, 32, kWave));
+#endif
+}
+__device__ __forceinline__ float halves_sum(float v) {
+#if MSATTN_ROW_SWAPS
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+#else
+  return v + __shfl_xor(v, 32, kWave);
+#endif
+}
+
 constexpr int kPfWaves = 4;                     // waves per key group (one per SIMD)
 constexpr int kPfGroups = 2;                    // key groups: even / odd steps
 constexpr int kPfGroupThreads = kPfWaves * kWave;
 constexpr int kPfThreads = kPfGroups * kPfGroupThreads;
-constexpr int kPfRB = MSATTN_PF_RB;             // 16-row blocks per wave
+constexpr int kPfRB = MSATTN_PF_RB;             // query rows per wave / 16 (2: one 32-row block)
 constexpr int kPfRows = 16 * kPfRB * kPfWaves;  // query rows per workgroup
 constexpr int kPfStep = 64;                     // key tokens per step
 constexpr int kPfPageChunk = 512;               // page ids cached in LDS at a time
@@ -234,12 +278,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   typedef typename KV::raw_t raw_t;
   constexpr int EB = static_cast<int>(sizeof(KT));
   static_assert(D == 64 || D == 128, "prefill MFMA kernel handles head_dim 64 and 128");
-  static_assert(RB == 1 || RB == 2, "one or two 16-row blocks per wave");
   // A cache of the query's type is copied into LDS by the load unit; other caches pass
   // through registers, where they are converted.
   constexpr bool DMA = MSATTN_PF_DMA && std::is_same<T, KT>::value;
-  constexpr int JD = D / 32;              // k-steps of S^T
-  constexpr int ND = D / 16;              // 16-dim tiles of O^T
+  constexpr int JD = D / 16;              // k-steps of S^T (16 dims each)
+  constexpr int ND = D / 32;              // 32-dim tiles of O^T
+  static_assert(16 * RB == 32, "one 32-row MFMA block per wave");
   // LDS row strides (elements): unpadded, swizzled rows for the copies; padded rows for
   // register staging (K: 68 / 36 dwords, V: 72 / 40 dwords).
   constexpr int RSK = DMA ? D : D + 8;
@@ -359,8 +403,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   const int wg = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int grp = wg / kPfWaves;
   const int w = wg - grp * kPfWaves;
-  const int g = lane >> 4;
-  const int n = lane & 15;
+  const int hh = lane >> 5;  // lane half: keys / dims 4 hh .. of each group of 8
+  const int cc = lane & 31;  // the lane's query row in the wave's 32-row block
   int it_lo = 0, it_hi = 1 << 28;
   bool full = true;  // the whole task: normalised output; else a partial
   unsigned task = 0;
@@ -434,34 +478,28 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     hi_all = p.causal ? min(ctx, ctx - p.q_len + i_last + 1) : ctx;
   }
 
-  // This lane's query rows (MFMA column n of each of the wave's row blocks).
-  bool row_ok[RB];
-  int lo_n[RB], hi_n[RB];
-  // Index of row block rb's query row in the [tokens, heads] query / output arrays
+  // This lane's query row: MFMA column cc of the wave's 32-row block (both lane halves hold
+  // it, each for half of every 8 keys or dims).
+  const bool row_ok = row0 + w * WROWS + cc < p.rows_per_kvh;
+  int lo_n = 0, hi_n = 0;
+  // Index of the lane's query row in the [tokens, heads] query / output arrays
   // (recomputed where needed rather than held through the key loop).
-  auto out_row = [&](int rb) {
-    const int row = row0 + w * WROWS + rb * 16 + n;
+  auto out_row = [&]() {
+    const int row = row0 + w * WROWS + cc;
     const int i = row / p.G;
     return (static_cast<int64_t>(b) * p.q_len + i) * p.H + kvh * p.G + (row - i * p.G);
   };
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int row = row0 + w * WROWS + rb * 16 + n;
-    row_ok[rb] = row < p.rows_per_kvh;
-    lo_n[rb] = 0;
-    hi_n[rb] = 0;
-    if (row_ok[rb]) {
-      const int i = row / p.G;
-      const int qpos = ctx - p.q_len + i;
-      if constexpr (PX) {
-        lo_n[rb] = lo_all;
-        hi_n[rb] = min(hi_all, max(0, p.row_lens[i]));
-      } else {
-        hi_n[rb] = p.causal ? min(ctx, qpos + 1) : ctx;
-        lo_n[rb] = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
-      }
-      if (hi_n[rb] < lo_n[rb]) hi_n[rb] = lo_n[rb];
+  if (row_ok) {
+    const int i = (row0 + w * WROWS + cc) / p.G;
+    const int qpos = ctx - p.q_len + i;
+    if constexpr (PX) {
+      lo_n = lo_all;
+      hi_n = min(hi_all, max(0, p.row_lens[i]));
+    } else {
+      hi_n = p.causal ? min(ctx, qpos + 1) : ctx;
+      lo_n = p.window > 0 ? max(0, qpos - p.window + 1) : 0;
     }
+    if (hi_n < lo_n) hi_n = lo_n;
   }
   // Keys every row of this wave sees: [wave_lo, wave_hi) (rows grow with the query).
   int wave_lo = 0, wave_hi = 0;
@@ -475,36 +513,29 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
       wave_lo = p.window > 0 ? max(0, qb_ - p.window + 1) : 0;
     }
     if constexpr (PX) {  // the smallest per-row limit of the wave's valid rows
-      int h = INT_MAX;
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) h = row_ok[rb] ? min(h, hi_n[rb]) : h;
+      int h = row_ok ? hi_n : INT_MAX;
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) h = min(h, __shfl_xor(h, o, kWave));
       wave_lo = lo_all;
       wave_hi = h == INT_MAX ? 0 : h;
     }
   }
-  uint4 qb[RB][JD];
+  // The B operand Q^T of k-step j: the row's dims 16 j + 8 hh .. + 7.
+  uint4 qb[JD];
   {
     const T* qp = static_cast<const T*>(p.q);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int j = 0; j < JD; ++j) {
-        qb[rb][j] = make_uint4(0u, 0u, 0u, 0u);
-        if (row_ok[rb]) qb[rb][j] = *reinterpret_cast<const uint4*>(qp + out_row(rb) * D + 32 * j + 8 * g);
-      }
+    for (int j = 0; j < JD; ++j) {
+      qb[j] = make_uint4(0u, 0u, 0u, 0u);
+      if (row_ok) qb[j] = *reinterpret_cast<const uint4*>(qp + out_row() * D + 16 * j + 8 * hh);
+    }
   }
 
-  mf_f32x4 acc[RB][ND];
-  float m_run[RB], l_run[RB];
+  // O^T in 32-dim tiles: acc[t] register v = dim 32 t + (v & 3) + 8 (v >> 2) + 4 hh.
+  mf_f32x16 acc[ND];
+  float m_run = -INFINITY, l_run = 0.0f;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-    for (int t = 0; t < ND; ++t) acc[rb][t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-    m_run[rb] = -INFINITY;
-    l_run[rb] = 0.0f;
-  }
+  for (int t = 0; t < ND; ++t) acc[t] = zero16();
 
   const KT* kbase = static_cast<const KT*>(p.k);
   const KT* vbase = static_cast<const KT*>(p.v);
@@ -546,44 +577,28 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     const int t_base = step * kPfStep;
     return t_base >= wave_lo && t_base + kPfStep <= wave_hi;
   };
-  // S^T of a step for the wave's row blocks, slices sl0 .. sl0 + NS - 1 of 16 tokens;
-  // ka_of(sl, j) reads the K operand of slice sl, k-step j (key row 16 sl + n, dims
-  // 32 j + 8 g ..).
-  auto scores = [&](auto&& ka_of, mf_f32x4 (&sv)[RB][4], auto sl0_c, auto ns_c) {
-    constexpr int SL0 = decltype(sl0_c)::value;
-    constexpr int NS = decltype(ns_c)::value;
+  // S^T of a step's 32-key tile TL for the wave's 32 rows; ka_of(TL, j) reads the K
+  // operand of k-step j (key row 32 TL + cc, dims 16 j + 8 hh ..). Lane (cc, hh) then holds
+  // row cc's scores of keys 32 TL + (v & 3) + 8 (v >> 2) + 4 hh in register v.
+  auto scores = [&](auto&& ka_of, mf_f32x16 (&sv)[2], auto tile_c) {
+    constexpr int TL = decltype(tile_c)::value;
+    mf_f32x16 st = zero16();
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+    for (int j = 0; j < JD; ++j) st = Mfma32<T>::mac(ka_of(TL, j), qb[j], st);
+    sv[TL] = st;
+  };
+  // Keys outside the row's range score -inf (steps that cross some row's range).
+  auto mask_scores = [&](int step, mf_f32x16 (&sv)[2], auto tile_c) {
+    constexpr int TL = decltype(tile_c)::value;
+    const int t_base = step * kPfStep + 32 * TL + 4 * hh;
 #pragma unroll
-      for (int sl = SL0; sl < SL0 + NS; ++sl) sv[rb][sl] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < JD; ++j) {
-      uint4 ka[NS];
-#pragma unroll
-      for (int u = 0; u < NS; ++u) ka[u] = ka_of(SL0 + u, j);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int u = 0; u < NS; ++u)
-          sv[rb][SL0 + u] = Mfma16<T>::mac(ka[u], qb[rb][j], sv[rb][SL0 + u]);
+    for (int v = 0; v < 16; ++v) {
+      const int tok = t_base + (v & 3) + 8 * (v >> 2);
+      sv[TL][v] = (tok >= lo_n && tok < hi_n) ? sv[TL][v] : -INFINITY;
     }
   };
-  // Keys outside a row's range score -inf (steps that cross some row's range); slices
-  // sl0 .. sl0 + ns - 1.
-  auto mask_scores = [&](int step, mf_f32x4 (&sv)[RB][4], int sl0, int ns) {
-    const int t_base = step * kPfStep;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int sl = 0; sl < 4; ++sl)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (sl < sl0 || sl >= sl0 + ns) continue;
-          const int tok = t_base + 16 * sl + 4 * g + r;
-          sv[rb][sl][r] = (tok >= lo_n[rb] && tok < hi_n[rb]) ? sv[rb][sl][r] : -INFINITY;
-        }
-  };
-  // Online softmax of one row block over one half-step (32 keys, slices 2 ks, 2 ks + 1).
+  // Online softmax of the lane's row over one half-step (the 32-key tile ks: 16 keys per
+  // lane half).
   // The weights are exp2(s * scale_log2 - m) for the row's running max m (base 2; the row
   // max is taken on raw scores, scale_log2 > 0 keeps the order). m moves only when some
   // weight would exceed 2^kPfRescaleSlack: the weights stay within what fp32 sums and the
@@ -595,100 +610,103 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   // sum, so a lane whose sum is within 2^kPfRescaleSlack holds no weight over it: the
   // sum is the test, and the scores' max is taken only on the slow path. A row whose m
   // is still -inf (no key seen yet) takes the slow path too. softmax_redo moves m to the
-  // row max (over the 4 lane groups) when it is above m, rescales l and acc, and takes
+  // row max (over both lane halves) when it is above m, rescales l and acc, and takes
   // the weights again. (MSATTN_PF_SUM_CHECK=0: each lane tests its scores' max against
   // m + kPfRescaleSlack instead, l's increment summed in fp32 before rounding.)
-  uint4 pb[RB][2];
-  float psum[RB];
-  float lmax[RB];
-  auto softmax_exp = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) __attribute__((always_inline)) {
-    const float m_use = m_run[rb] != -INFINITY ? m_run[rb] : 0.0f;
-    float pr[8];
+  // The B operand P^T of the 16-key chunk c2 of tile ks: registers v = 8 c2 .. 8 c2 + 7,
+  // i.e. keys 16 c2 + 4 hh .. + 3 and 16 c2 + 8 + 4 hh .. + 3, the two 4-token reads of V.
+  uint4 pb[2][2];
+  float psum;
+  float lmax;
+  auto softmax_exp = [&](const mf_f32x16 (&sv)[2], auto ks_c) __attribute__((always_inline)) {
+    constexpr int KS = decltype(ks_c)::value;
+    const float m_use = m_run != -INFINITY ? m_run : 0.0f;
+    float pr[16];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int v = 0; v < 16; ++v)
+      pr[v] = __builtin_amdgcn_exp2f(fmaf(sv[KS][v], p.scale_log2, -m_use));
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        pr[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(sv[rb][2 * ks + h][r], p.scale_log2, -m_use));
-    pb[rb][ks] = make_uint4(Pack2<T>::pack(pr[0], pr[1]), Pack2<T>::pack(pr[2], pr[3]),
-                            Pack2<T>::pack(pr[4], pr[5]), Pack2<T>::pack(pr[6], pr[7]));
+    for (int c2 = 0; c2 < 2; ++c2)
+      pb[KS][c2] = make_uint4(Pack2<T>::pack(pr[8 * c2], pr[8 * c2 + 1]),
+                              Pack2<T>::pack(pr[8 * c2 + 2], pr[8 * c2 + 3]),
+                              Pack2<T>::pack(pr[8 * c2 + 4], pr[8 * c2 + 5]),
+                              Pack2<T>::pack(pr[8 * c2 + 6], pr[8 * c2 + 7]));
     if constexpr (kPfSumCheck) {
       const uint32_t one2 = Pack2<T>::pack(1.0f, 1.0f);
-      const uint4 w = pb[rb][ks];
-      psum[rb] = Dot2<T>::dot(w.w, one2, Dot2<T>::dot(w.z, one2, Dot2<T>::dot(w.y, one2,
-                 Dot2<T>::dot(w.x, one2, 0.0f))));
-    } else {
-      float s = 0.0f;
+      float s2[2];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) s += pr[i];
-      psum[rb] = s;
+      for (int c2 = 0; c2 < 2; ++c2) {
+        const uint4 wv = pb[KS][c2];
+        s2[c2] = Dot2<T>::dot(wv.w, one2, Dot2<T>::dot(wv.z, one2, Dot2<T>::dot(wv.y, one2,
+                 Dot2<T>::dot(wv.x, one2, 0.0f))));
+      }
+      psum = s2[0] + s2[1];
+    } else {
+      float sum = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sum += pr[v];
+      psum = sum;
     }
   };
   // The lane's scores' max over the half-step.
-  auto lane_max = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) __attribute__((always_inline)) {
+  auto lane_max = [&](const mf_f32x16 (&sv)[2], auto ks_c) __attribute__((always_inline)) {
+    constexpr int KS = decltype(ks_c)::value;
     float lm = -INFINITY;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) lm = fmaxf(lm, sv[rb][2 * ks + h][r]);
+    for (int v = 0; v < 16; ++v) lm = fmaxf(lm, sv[KS][v]);
     return lm;
   };
   // The weights with the current m (and, without the sum test, the lane's max).
-  auto softmax_fast = [&](const mf_f32x4 (&sv)[RB][4], int rb, int ks) __attribute__((always_inline)) {
-    if constexpr (!kPfSumCheck) lmax[rb] = lane_max(sv, rb, ks);
-    softmax_exp(sv, rb, ks);
+  auto softmax_fast = [&](const mf_f32x16 (&sv)[2], auto ks_c) __attribute__((always_inline)) {
+    if constexpr (!kPfSumCheck) lmax = lane_max(sv, ks_c);
+    softmax_exp(sv, ks_c);
   };
   auto over_bound = [&]() __attribute__((always_inline)) {
-    bool over = false;
-    static_for<RB>([&](auto rc) {
-      constexpr int rb = decltype(rc)::value;
-      if constexpr (kPfSumCheck)
-        over |= psum[rb] > kPfSumBound || m_run[rb] == -INFINITY;
-      else
-        over |= lmax[rb] * p.scale_log2 > m_run[rb] + kPfRescaleSlack;
-    });
+    bool over;
+    if constexpr (kPfSumCheck)
+      over = psum > kPfSumBound || m_run == -INFINITY;
+    else
+      over = lmax * p.scale_log2 > m_run + kPfRescaleSlack;
     return __any(over);
   };
   // Slow path for the wave: move m, rescale l and acc, take the weights again.
-  auto softmax_redo = [&](const mf_f32x4 (&sv)[RB][4], int ks) __attribute__((always_inline)) {
-    // (static_for: every array index stays a constant, the arrays stay in registers)
-    static_for<RB>([&](auto rc) {
-      constexpr int rb = decltype(rc)::value;
-      if constexpr (kPfSumCheck) lmax[rb] = lane_max(sv, rb, ks);
-      const float mt = rows4_max(lmax[rb]) * p.scale_log2;  // the row max, base-2 units
-      const float m_new = mt > m_run[rb] + (kPfSumCheck ? 0.0f : kPfRescaleSlack) ? mt : m_run[rb];
-      const float alpha = m_new != -INFINITY ? __builtin_amdgcn_exp2f(m_run[rb] - m_new) : 1.0f;
-      l_run[rb] *= alpha;
-      m_run[rb] = m_new;
-      if (__any(alpha != 1.0f)) {
+  auto softmax_redo = [&](const mf_f32x16 (&sv)[2], auto ks_c) __attribute__((always_inline)) {
+    if constexpr (kPfSumCheck) lmax = lane_max(sv, ks_c);
+    const float mt = halves_max(lmax) * p.scale_log2;  // the row max, base-2 units
+    const float m_new = mt > m_run + (kPfSumCheck ? 0.0f : kPfRescaleSlack) ? mt : m_run;
+    const float alpha = m_new != -INFINITY ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+    l_run *= alpha;
+    m_run = m_new;
+    if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int t = 0; t < ND; ++t) acc[rb][t] *= alpha;
-      }
-      softmax_exp(sv, rb, ks);
-    });
+      for (int t = 0; t < ND; ++t) acc[t] *= alpha;
+    }
+    softmax_exp(sv, ks_c);
   };
   // After a half-step's weights (fast, and the redo when needed): l += their sum.
-  auto softmax_end = [&](const mf_f32x4 (&sv)[RB][4], int ks) __attribute__((always_inline)) {
-    if (__builtin_expect(over_bound(), 0)) softmax_redo(sv, ks);
-    static_for<RB>([&](auto rc) {
-      constexpr int rb = decltype(rc)::value;
-      l_run[rb] += psum[rb];
-    });
+  auto softmax_end = [&](const mf_f32x16 (&sv)[2], auto ks_c) __attribute__((always_inline)) {
+    if (__builtin_expect(over_bound(), 0)) softmax_redo(sv, ks_c);
+    l_run += psum;
   };
-  // O^T += V^T P^T over half-step ks; va_of(ks, t) reads the A operand V^T (dims 16 t ..,
-  // tokens 32 ks ..).
-  auto pv = [&](auto&& va_of, int ks) {
-    uint4 va[ND];
+  // O^T += V^T P^T over half-step ks (the 32-key tile ks, in 16-key chunks c2); va_of(ks,
+  // c2, t) reads the A operand V^T (dims 32 t + cc, the chunk's keys as pb's).
+  auto pv = [&](auto&& va_of, auto ks_c) {
+    constexpr int KS = decltype(ks_c)::value;
 #pragma unroll
-    for (int t = 0; t < ND; ++t) va[t] = va_of(ks, t);
+    for (int c2 = 0; c2 < 2; ++c2) {
+      uint4 va[ND];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+      for (int t = 0; t < ND; ++t) va[t] = va_of(KS, c2, t);
 #pragma unroll
-      for (int t = 0; t < ND; ++t) acc[rb][t] = Mfma16<T>::mac(va[t], pb[rb][ks], acc[rb][t]);
+      for (int t = 0; t < ND; ++t) acc[t] = Mfma32<T>::mac(va[t], pb[KS][c2], acc[t]);
+    }
   };
   // Transposed reads: lane s of a 16-lane group names 4 dims of one token (tokens
   // base + (s >> 2), dims 4 * (s & 3) ..); lane i then receives dim i of those four
-  // tokens. lo covers tokens 4 g .. 4 g + 3 of the 32-token half, hi the same 16 later.
-  const int tr_tok = lane >> 2 & 3;
+  // tokens. Group q = lane / 16 reads dims 16 (q & 1) .. of its tile for tokens 4 hh ..
+  // (lo) and 8 + 4 hh .. (hi) of the 16-key chunk: lane (cc, hh) receives dim cc.
+  const int tr_tok = lane >> 2 & 3;        // the token a lane names, within its 4
+  const int tr_dim = 16 * (lane >> 4 & 1) + 4 * (lane & 3);  // the dims it names
   auto tr_pair = [&](uint16_t* lo, uint16_t* hi) {
     const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)lo));
     const uint2 c = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)hi));
@@ -708,15 +726,14 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     constexpr int RPI = kWave / CPRD;  // rows per copy instruction (4 or 8)
     constexpr int NI = 16 / RPI;       // copy instructions per 16-row tile
     // Lane byte offsets of the reads, as one base XORed with a constant per k-step / dim
-    // tile: K chunk (4 j + g) ^ s = 4 (j ^ (s >> 2)) + (g ^ (s & 3)) puts j in bits 6-7 of
-    // the offset, V chunk pair (2 t + h) ^ s in bits 5-7, bits the row and lane terms leave
-    // zero (slots are 256-byte aligned), so no register per j or t is held.
-    const int swz_n = pf_swz<D>(n);
-    const uint32_t kx = static_cast<uint32_t>(n * 2 * D + 16 * (g ^ (swz_n & 3)) + 64 * (swz_n >> 2));
-    const int vrow = 4 * g + tr_tok;
-    const int swz_v = pf_swz<D>(vrow);
-    const uint32_t vx = static_cast<uint32_t>(vrow * 2 * D + 16 * ((lane >> 1 & 1) ^ (swz_v & 1)) +
-                                              32 * (swz_v >> 1) + 8 * (lane & 1));
+    // tile, so no register per j or t is held (slots are 256-byte aligned, rows 2 D
+    // bytes): the K chunk (2 j + hh) of key row cc sits at (2 j + hh) ^ s, s = pf_swz(cc),
+    // byte 16 (hh ^ s) ^ 32 j; the V chunk (4 t + c) (c < 4) of token row r at
+    // 16 ((c ^ s) ^ 4 t), and token row r + 8 (r < 8) has s ^ 1, one chunk over.
+    const uint32_t kx = static_cast<uint32_t>(cc * 2 * D + 16 * (hh ^ pf_swz<D>(cc)));
+    const int vrow = 4 * hh + tr_tok;
+    const uint32_t vx = static_cast<uint32_t>(vrow * 2 * D + 16 * ((tr_dim >> 3) ^ pf_swz<D>(vrow)) +
+                                              8 * (lane & 1));
     uint32_t dvo[NI];
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
@@ -789,16 +806,18 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     // slot from a copy into another); each slot is 256-byte aligned.
     static_assert(sizeof(s_k0[0]) % 256 == 0 && sizeof(s_v0[0]) % 256 == 0, "slot alignment");
     auto k_from = [&](uint16_t* buf) {
-      return [&, buf](int sl, int j) {
-        const uint32_t a = (kx ^ static_cast<uint32_t>(64 * j)) + static_cast<uint32_t>(32 * sl * D);
+      return [&, buf](int tl, int j) {
+        const uint32_t a = (kx ^ static_cast<uint32_t>(32 * j)) + static_cast<uint32_t>(64 * tl * D);
         return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(buf) + a);
       };
     };
     auto v_from = [&](uint16_t* buf) {
-      return [&, buf](int ks, int t) {
-        const uint32_t a = (vx ^ static_cast<uint32_t>(32 * t)) + static_cast<uint32_t>(64 * ks * D);
-        char* lo = reinterpret_cast<char*>(buf) + a;
-        return tr_pair(reinterpret_cast<uint16_t*>(lo), reinterpret_cast<uint16_t*>(lo + 32 * D));
+      return [&, buf](int ks, int c2, int t) {
+        const uint32_t x = vx ^ static_cast<uint32_t>(64 * t);
+        const uint32_t row = static_cast<uint32_t>((32 * ks + 16 * c2) * 2 * D);
+        char* const base = reinterpret_cast<char*>(buf);
+        return tr_pair(reinterpret_cast<uint16_t*>(base + x + row),
+                       reinterpret_cast<uint16_t*>(base + (x ^ 16u) + row + 16 * D));
       };
     };
 
@@ -818,7 +837,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     //   r3: P.V of keys 32-63.
     // The scores sv and weights pb of a step live across blocks (and, for group 1, across
     // an iteration's barrier). `copies` issues copy instructions among the block's MFMAs.
-    mf_f32x4 sv[RB][4];
+    mf_f32x16 sv[2];
     // The MFMA-only blocks run at MSATTN_PF_MPRIO and return to the group's priority.
     auto prio_up = [] {
       if constexpr (MSATTN_PF_MPRIO > 0) __builtin_amdgcn_s_setprio(MSATTN_PF_MPRIO);
@@ -831,37 +850,35 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
     };
     auto r0 = [&](uint16_t* kc, int step, bool full, auto&& side) {
       prio_up();
-      scores(k_from(kc), sv, I0{}, I2{});
+      scores(k_from(kc), sv, I0{});
       side();
       prio_down();
-      if (!full) mask_scores(step, sv, 0, 2);
+      if (!full) mask_scores(step, sv, I0{});
     };
     auto r1 = [&](uint16_t* kc, int step, bool full, auto&& copies) {
-      scores(k_from(kc), sv, I2{}, I2{});
+      scores(k_from(kc), sv, I1{});
       copies();
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) softmax_fast(sv, rb, 0);
-      if constexpr (MSATTN_PF_SCHED) pf_sched_half<JD * RB * 2, MSATTN_PF_NV, NI>();
+      softmax_fast(sv, I0{});
+      if constexpr (MSATTN_PF_SCHED) pf_sched_half<JD, MSATTN_PF_NV, NI>();
       // The weights stay in this block (the compiler would otherwise move them past the
       // branches below, next to their use and away from the MFMAs they overlap).
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][0]);
-      softmax_end(sv, 0);
-      if (!full) mask_scores(step, sv, 2, 2);
+      keep_here(pb[0][0]);
+      keep_here(pb[0][1]);
+      softmax_end(sv, I0{});
+      if (!full) mask_scores(step, sv, I1{});
     };
     auto r2 = [&](uint16_t* vc, auto&& copies) {
-      pv(v_from(vc), 0);
+      pv(v_from(vc), I0{});
       copies();
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) softmax_fast(sv, rb, 1);
-      if constexpr (MSATTN_PF_SCHED) pf_sched_half<RB * ND, MSATTN_PF_NV, NI>();
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) keep_here(pb[rb][1]);
-      softmax_end(sv, 1);
+      softmax_fast(sv, I1{});
+      if constexpr (MSATTN_PF_SCHED) pf_sched_half<2 * ND, MSATTN_PF_NV, NI>();
+      keep_here(pb[1][0]);
+      keep_here(pb[1][1]);
+      softmax_end(sv, I1{});
     };
     auto r3 = [&](uint16_t* vc) {
       prio_up();
-      pv(v_from(vc), 1);
+      pv(v_from(vc), I1{});
       prio_down();
     };
     auto no_copies = [] {};
@@ -1046,32 +1063,36 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
         *reinterpret_cast<uint4*>(vb + r * RSV + st_c * 8) = KV::operand(vst[j]);
       }
     };
-    const int tr_dim = 4 * (lane & 3);
     auto compute = [&](int step, int buf) {
       uint16_t* const kb = buf ? &s_k1[grp][0] : &s_k0[grp][0];
       uint16_t* const vb = buf ? &s_v1[grp][0] : &s_v0[grp][0];
-      mf_f32x4 sv[RB][4];
+      using J0 = std::integral_constant<int, 0>;
+      using J1 = std::integral_constant<int, 1>;
+      mf_f32x16 sv[2];
+      auto ka_of = [&](int tl, int j) {
+        return *reinterpret_cast<const uint4*>(kb + (32 * tl + cc) * RSK + 16 * j + 8 * hh);
+      };
       if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(1);
-      scores([&](int sl, int j) {
-        return *reinterpret_cast<const uint4*>(kb + (16 * sl + n) * RSK + 32 * j + 8 * g);
-      }, sv, std::integral_constant<int, 0>{}, std::integral_constant<int, 4>{});
+      scores(ka_of, sv, J0{});
+      scores(ka_of, sv, J1{});
       if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(0);
-      if (!step_full(step)) mask_scores(step, sv, 0, 4);
+      if (!step_full(step)) {
+        mask_scores(step, sv, J0{});
+        mask_scores(step, sv, J1{});
+      }
       // Half-step by half-step: the same order of operations as the copy path
       // (bit-identical results).
-      auto va_of = [&](int ks, int t) {
-        uint16_t* lo = vb + (32 * ks + 4 * g + tr_tok) * RSV + 16 * t + tr_dim;
-        return tr_pair(lo, lo + 16 * RSV);
+      auto va_of = [&](int ks, int c2, int t) {
+        uint16_t* lo = vb + (32 * ks + 16 * c2 + 4 * hh + tr_tok) * RSV + 32 * t + tr_dim;
+        return tr_pair(lo, lo + 8 * RSV);
       };
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) softmax_fast(sv, rb, ks);
-        softmax_end(sv, ks);
+      static_for<2>([&](auto kc) {
+        softmax_fast(sv, kc);
+        softmax_end(sv, kc);
         if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(1);
-        pv(va_of, ks);
+        pv(va_of, kc);
         if constexpr (MSATTN_PF_PRIO) __builtin_amdgcn_s_setprio(0);
-      }
+      });
     };
 
     // Group grp takes steps step_first + grp + 2i (i = 0, 1, ...) from its own pair of
@@ -1113,80 +1134,72 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(const PrefillP
   }
 
   // ---- combine the two key groups (same rows, same lane layout), normalise, store ----
-  // Group 1 hands its (acc, m, l) through LDS (the K slots hold row block 0 / 1's
-  // accumulators, the first V slot m and l; all free after the loop): lane (g, n) of group
-  // 0's wave w reads exactly what lane (g, n) of group 1's wave w wrote: O[row n][dims
-  // 16t + 4g + r] and the row's running m and partial l.
-  static_assert(sizeof(s_k0) >= kPfWaves * ND * kWave * 16, "combine space");
-  static_assert(sizeof(s_v0) >= kPfWaves * RB * kWave * 8, "combine space");
+  // Group 1 hands its (acc, m, l) through LDS (the K slots hold the accumulators' dim
+  // tiles, NDH of them each, the first V slot m and l; all free after the loop): lane l of
+  // group 0's wave w reads exactly what lane l of group 1's wave w wrote. float4 i of dim
+  // tile t holds the row's dims 32 t + 8 i + 4 hh .. + 3.
+  constexpr int NDH = ND / 2;
+  static_assert(NDH >= 1 && sizeof(s_k0) >= kPfWaves * NDH * 4 * kWave * 16, "combine space");
+  static_assert(sizeof(s_v0) >= kPfWaves * kWave * 8, "combine space");
   float4* const s_acc0 = reinterpret_cast<float4*>(&s_k0[0][0]);
   float4* const s_acc1 = reinterpret_cast<float4*>(&s_k1[0][0]);
   float2* const s_ml = reinterpret_cast<float2*>(&s_v0[0][0]);
+  auto s_slot = [&](int t, int i) {
+    return (t < NDH ? s_acc0 : s_acc1) + ((w * NDH + t % NDH) * 4 + i) * kWave + lane;
+  };
   if (grp == 1) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      float4* const s_acc = rb == 0 ? s_acc0 : s_acc1;
+    for (int t = 0; t < ND; ++t)
 #pragma unroll
-      for (int t = 0; t < ND; ++t)
-        s_acc[(w * ND + t) * kWave + lane] =
-            make_float4(acc[rb][t][0], acc[rb][t][1], acc[rb][t][2], acc[rb][t][3]);
-      s_ml[(w * RB + rb) * kWave + lane] = make_float2(m_run[rb], l_run[rb]);
-    }
+      for (int i = 0; i < 4; ++i)
+        *s_slot(t, i) = make_float4(acc[t][4 * i], acc[t][4 * i + 1], acc[t][4 * i + 2], acc[t][4 * i + 3]);
+    s_ml[w * kWave + lane] = make_float2(m_run, l_run);
   }
   __syncthreads();
   if (grp == 0) {
+    const float2 ml1 = s_ml[w * kWave + lane];
+    const float M = fmaxf(m_run, ml1.x);
+    const float a0 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
+    const float a1 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml1.x - M);
+    float l = l_run * a0 + ml1.y * a1;
+    l = halves_sum(l);
+    // the two groups' unnormalised sums of float4 i of dim tile t
+    auto merged = [&](int t, int i) {
+      const float4 o1 = *s_slot(t, i);
+      return make_float4(acc[t][4 * i] * a0 + o1.x * a1, acc[t][4 * i + 1] * a0 + o1.y * a1,
+                         acc[t][4 * i + 2] * a0 + o1.z * a1, acc[t][4 * i + 3] * a0 + o1.w * a1);
+    };
+    if constexpr (PX) {  // unnormalised partial of this (row, key partition)
+      if (row_ok) {
+        const int64_t slot = out_row() * p.npart + blockIdx.y;
+        if (hh == 0) *reinterpret_cast<float2*>(p.pml + slot * 2) = make_float2(M, l);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const float4* const s_acc = rb == 0 ? s_acc0 : s_acc1;
-      const float2 ml1 = s_ml[(w * RB + rb) * kWave + lane];
-      const float M = fmaxf(m_run[rb], ml1.x);
-      const float a0 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[rb] - M);
-      const float a1 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml1.x - M);
-      float l = l_run[rb] * a0 + ml1.y * a1;
-      l = rows4_sum(l);
-      if constexpr (PX) {  // unnormalised partial of this (row, key partition)
-        if (row_ok[rb]) {
-          const int64_t slot = out_row(rb) * p.npart + blockIdx.y;
-          if (g == 0) *reinterpret_cast<float2*>(p.pml + slot * 2) = make_float2(M, l);
+        for (int t = 0; t < ND; ++t)
 #pragma unroll
-          for (int t = 0; t < ND; ++t) {
-            const float4 o1 = s_acc[(w * ND + t) * kWave + lane];
-            *reinterpret_cast<float4*>(p.pacc + slot * D + 16 * t + 4 * g) =
-                make_float4(acc[rb][t][0] * a0 + o1.x * a1, acc[rb][t][1] * a0 + o1.y * a1,
-                            acc[rb][t][2] * a0 + o1.z * a1, acc[rb][t][3] * a0 + o1.w * a1);
-          }
-        }
-        continue;
+          for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<float4*>(p.pacc + slot * D + 32 * t + 8 * i + 4 * hh) = merged(t, i);
       }
-      if (!full) {  // stream-K share of a split task: its unnormalised partial
-        if (row_ok[rb]) {
-          const int rs = (2 * sk_share + (seg == 0 ? 0 : 1)) * kPfRows + (w * WROWS + rb * 16 + n);
-          if (g == 0) *reinterpret_cast<float2*>(p.sk_ml + static_cast<int64_t>(rs) * 2) = make_float2(M, l);
-          float* const pa = p.sk_acc + static_cast<int64_t>(rs) * D + 4 * g;
+    } else if (!full) {  // stream-K share of a split task: its unnormalised partial
+      if (row_ok) {
+        const int rs = (2 * sk_share + (seg == 0 ? 0 : 1)) * kPfRows + (w * WROWS + cc);
+        if (hh == 0) *reinterpret_cast<float2*>(p.sk_ml + static_cast<int64_t>(rs) * 2) = make_float2(M, l);
+        float* const pa = p.sk_acc + static_cast<int64_t>(rs) * D + 4 * hh;
 #pragma unroll
-          for (int t = 0; t < ND; ++t) {
-            const float4 o1 = s_acc[(w * ND + t) * kWave + lane];
-            *reinterpret_cast<float4*>(pa + 16 * t) =
-                make_float4(acc[rb][t][0] * a0 + o1.x * a1, acc[rb][t][1] * a0 + o1.y * a1,
-                            acc[rb][t][2] * a0 + o1.z * a1, acc[rb][t][3] * a0 + o1.w * a1);
-          }
-        }
-        continue;
-      }
-      if (row_ok[rb]) {
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        T* op = static_cast<T*>(p.out) + out_row(rb) * D;
+        for (int t = 0; t < ND; ++t)
 #pragma unroll
-        for (int t = 0; t < ND; ++t) {
-          const float4 o1 = s_acc[(w * ND + t) * kWave + lane];
-          const float o0 = (acc[rb][t][0] * a0 + o1.x * a1) * inv;
-          const float o1_ = (acc[rb][t][1] * a0 + o1.y * a1) * inv;
-          const float o2 = (acc[rb][t][2] * a0 + o1.z * a1) * inv;
-          const float o3 = (acc[rb][t][3] * a0 + o1.w * a1) * inv;
-          const uint2 pk = make_uint2(Pack2<T>::pack(o0, o1_), Pack2<T>::pack(o2, o3));
-          *reinterpret_cast<uint2*>(op + 16 * t + 4 * g) = pk;
-        }
+          for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(pa + 32 * t + 8 * i) = merged(t, i);
       }
+    } else if (row_ok) {
+      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+      T* op = static_cast<T*>(p.out) + out_row() * D + 4 * hh;
+#pragma unroll
+      for (int t = 0; t < ND; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 o = merged(t, i);
+          *reinterpret_cast<uint2*>(op + 32 * t + 8 * i) =
+              make_uint2(Pack2<T>::pack(o.x * inv, o.y * inv), Pack2<T>::pack(o.z * inv, o.w * inv));
+        }
     }
   }
   __syncthreads();  // this task's LDS reads are done before the next task's copies
