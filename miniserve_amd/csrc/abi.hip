@@ -621,6 +621,7 @@ int partials_impl(const void* query, const void* k_cache, const void* v_cache,
   p.tickets = nullptr;
   p.k_new = nullptr;
   p.v_new = nullptr;
+  p.part_major = 0;  // the partition kernel's launcher chooses its grid order
   p.head_dim = head_dim;
   p.rows16 = rows16 ? 1 : 0;
   const int64_t gx = static_cast<int64_t>(p.max_parts) * num_kv_heads * p.rtiles;

@@ -42,6 +42,10 @@
 #define MSATTN_MFMA_WAVES 4
 #endif
 // Tiles in flight per wave (ring depth), head_dim 128 / head_dim 64.
+// 1: the partition kernel's grid runs partition-major (SplitParams::part_major).
+#ifndef MSATTN_PART_MAJOR
+#define MSATTN_PART_MAJOR 1
+#endif
 #ifndef MSATTN_MFMA_DEPTH
 #define MSATTN_MFMA_DEPTH 2
 #endif
@@ -686,13 +690,22 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
     p.hdr[kHdrWaves] = W;
     p.hdr[kHdrResidency] = WPC;
   }
-  // blockIdx.x = kvh + KVH * (part + max_parts * rtile); blockIdx.z = b.
+  // The grid order (SplitParams::part_major): partition-major over one x index, or
+  // blockIdx.x = kvh + KVH * (part + max_parts * rtile) with blockIdx.z = b.
   const unsigned bx = blockIdx.x;
   const int kvh = static_cast<int>(bx % static_cast<unsigned>(p.KVH));
   const unsigned rest = bx / static_cast<unsigned>(p.KVH);
-  const int part = static_cast<int>(rest % static_cast<unsigned>(p.max_parts));
-  const int rtile = static_cast<int>(rest / static_cast<unsigned>(p.max_parts));
-  const int b = blockIdx.z;
+  int part, rtile, b;
+  if (p.part_major) {
+    rtile = static_cast<int>(rest % static_cast<unsigned>(p.rtiles));
+    const unsigned rb = rest / static_cast<unsigned>(p.rtiles);
+    b = static_cast<int>(rb % static_cast<unsigned>(p.batch));
+    part = static_cast<int>(rb / static_cast<unsigned>(p.batch));
+  } else {
+    part = static_cast<int>(rest % static_cast<unsigned>(p.max_parts));
+    rtile = static_cast<int>(rest / static_cast<unsigned>(p.max_parts));
+    b = blockIdx.z;
+  }
 
   // Wave w owns a fixed run of the partition's tiles, so their page ids can be
   // requested together with the context length instead of after it.
@@ -1214,10 +1227,18 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
 }
 
 template <typename T, typename KT, int D, int RT, int W = kMfmaWaves, int WPC = kMfmaWgPerCu>
-hipError_t launch_decode_mfma_one(const SplitParams& p, hipStream_t stream) {
-  const unsigned gx = static_cast<unsigned>(p.max_parts) * static_cast<unsigned>(p.KVH) *
-                      static_cast<unsigned>(p.rtiles);
-  const dim3 grid(gx, 1, static_cast<unsigned>(p.batch));
+hipError_t launch_decode_mfma_one(const SplitParams& p_in, hipStream_t stream) {
+  // Partition-major order wherever the flat index fits: a launch's empty partitions (past
+  // their sequence's length, which the grid cannot know) are then dispatched after every
+  // workgroup with keys instead of among them.
+  SplitParams p = p_in;
+  const uint64_t flat = static_cast<uint64_t>(p.max_parts) * static_cast<uint64_t>(p.KVH) *
+                        static_cast<uint64_t>(p.rtiles) * static_cast<uint64_t>(p.batch);
+  p.part_major = MSATTN_PART_MAJOR && flat < (uint64_t(1) << 31) ? 1 : 0;
+  const unsigned gx = p.part_major ? static_cast<unsigned>(flat)
+                                   : static_cast<unsigned>(p.max_parts) * static_cast<unsigned>(p.KVH) *
+                                         static_cast<unsigned>(p.rtiles);
+  const dim3 grid(gx, 1, p.part_major ? 1u : static_cast<unsigned>(p.batch));
   // the fused append's instantiation (the host sets k_new only where it is built)
   if constexpr (sizeof(T) == 2 && RT <= 8) {
     if (p.k_new != nullptr) {

@@ -86,6 +86,11 @@ struct SplitParams {
   float scale_log2;
   int rows_per_kvh;  // q_len * G
   int rtiles;        // ceil(rows_per_kvh / RT)
+  // The MFMA partition kernel's grid order (set by its launcher): 1 = one flat x index
+  // kvh + KVH (rtile + rtiles (b + batch part)), partition-major, so that every sequence's
+  // first partitions are dispatched before any sequence's later (often empty) ones;
+  // 0 = x = kvh + KVH (part + max_parts rtile), z = b.
+  int part_major;
   int sk_group;        // stream-K: KV-head units per unit group
   int sk_unit_groups;  // stream-K: number of unit groups
   int sk_min_chunk;    // stream-K: smallest chunk (tiles)
