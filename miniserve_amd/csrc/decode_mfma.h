@@ -42,6 +42,13 @@
 #define MSATTN_MFMA_WAVES 4
 #endif
 // Tiles in flight per wave (ring depth), head_dim 128 / head_dim 64.
+// 8-wave workgroups (two waves per SIMD): each wave posts the tiles it has consumed in LDS
+// and runs at raised priority while it is not ahead of its SIMD partner (wave w ^ 4), as
+// the stream-K kernel does, so that the younger wave is not starved of load issue and
+// the two reach the workgroup's reduction together.
+#ifndef MSATTN_PART_BALANCE
+#define MSATTN_PART_BALANCE 1
+#endif
 // 1: the partition kernel's grid runs partition-major (SplitParams::part_major).
 #ifndef MSATTN_PART_MAJOR
 #define MSATTN_PART_MAJOR 1
@@ -662,6 +669,8 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
 
   __shared__ float s_red[kWaves][RT][D];
   __shared__ float s_ml[kWaves][RT][2];
+  constexpr bool kBalance = MSATTN_PART_BALANCE && kWaves > 4;
+  __shared__ int s_prog[kWaves];  // tiles consumed per wave (kBalance)
   __shared__ int s_last;  // in-kernel merge: this workgroup arrived last
   // LDS reserved beyond s_red / s_ml so that at most WPC workgroups share a
   // CU (the store below never runs; it keeps the array allocated).
@@ -1116,6 +1125,10 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
     br[d] = tile_base(d);
     issue(br[d], kr[d], vr[d]);
   });
+  if constexpr (kBalance) {  // the progress words start at zero (every wave reaches here)
+    if (tid < kWaves) s_prog[tid] = 0;
+    __syncthreads();
+  }
   static_for<kMaxT>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
     if (k >= nt) return;
@@ -1128,7 +1141,19 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
       if (app_here && k == k_app) append_patch(kr[k % DEPTH], vr[k % DEPTH], br[k % DEPTH]);
     }
     consume(k, kr[k % DEPTH], vr[k % DEPTH], br[k % DEPTH]);
+    if constexpr (kBalance) {
+      // Post this wave's progress; take priority while not ahead of the partner.
+      if (lane == 0)
+        __hip_atomic_store(&s_prog[w], k + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      const int other = __hip_atomic_load(&s_prog[w ^ (kWaves / 2)], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (k + 1 <= __builtin_amdgcn_readfirstlane(other))
+        __builtin_amdgcn_s_setprio(1);
+      else
+        __builtin_amdgcn_s_setprio(0);
+    }
   });
+  if constexpr (kBalance) __builtin_amdgcn_s_setprio(0);
 
   // Wave totals: l over the 4 lane groups, acc over the V token groups (lanes of equal
   // lane % LPR), reduce-scattered so a lane keeps two dims of each row: dims
