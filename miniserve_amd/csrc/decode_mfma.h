@@ -743,6 +743,100 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
   const int a0 = max(tok0, lo_all);
   const int a1 = min(min(tok0 + p.part, ctx), hi_all);
 
+  // Tiles [t_begin, t_end) of 16 absolute positions hold the keys; the wave's run is
+  // tiles tw0 .. tw0 + nt - 1 of it (earlier ones, below a window, read nothing).
+  const int t_begin = a0 / 16;
+  const int t_end = ceil_div(a1, 16);
+  const int nt = max(0, min(per_wave, t_end - tw0));
+
+  // Lane k holds tile tw0 + k's element offset, or -1 for a hole (a table entry outside
+  // [0, num_blocks), a page past the table, a tile outside the key range).
+  int64_t my_base = -1;
+  if (lane < nt && tw0 + lane >= t_begin && phys_pre >= 0 && phys_pre < p.num_blocks) {
+    const int t = tw0 + lane;
+    const int pg = (t * 16) / p.bs;
+    const int slot0 = t * 16 - pg * p.bs;
+    my_base = static_cast<int64_t>(phys_pre) * p.blk_stride +
+              static_cast<int64_t>(slot0) * p.slot_stride +
+              static_cast<int64_t>(kvh) * p.head_stride;
+  }
+
+  // Per-lane byte offsets inside a tile (32-bit: a tile spans 16 slots).
+  constexpr int EB = static_cast<int>(sizeof(KT));
+  const uint32_t k_row_off = static_cast<uint32_t>(tile_token<D>(n) * p.slot_stride * EB);
+  uint32_t v_lane_off[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    v_lane_off[j] = static_cast<uint32_t>(((TPI * j + va) * p.slot_stride + vc * 8) * EB);
+  const int tile_bytes = static_cast<int>((15 * p.slot_stride + D) * EB);
+
+  const KT* kbase = static_cast<const KT*>(p.k);
+  const KT* vbase = static_cast<const KT*>(p.v);
+
+  // P.V on the matrix core (fp32 query and cache, a full 16-row tile): O = P V as
+  // v_mfma_f32_16x16x4_f32 steps. Step r takes, in lane (g, n), A = P[row n][token
+  // tile_token(4g + r)] (the lane's own weight pr[r], where the scores landed) and
+  // B = V[that token][dim]; lane (g, n) loads 16 bytes of that token's row, dims
+  // 64 h + 4 n .. + 3, and element e of them feeds output block (h, e), whose column n
+  // is dim 64 h + 4 n + e. Output lane (g', n') then holds rows 4 g' .. 4 g' + 3 of dims
+  // 64 h + 4 n' + e: a float4 of consecutive dims per (row, h).
+  constexpr bool kPvMfma = MSATTN_PV_MFMA32 && std::is_same<T, float>::value &&
+                           std::is_same<KT, float>::value && RT == 16;
+  constexpr int NH = D / 64;         // 16-byte V loads per token step
+  constexpr int NVQ = 4 * NH;        // V loads per tile (MFMA P.V)
+  constexpr int NOB = 4 * NH;        // 16x16 output blocks (MFMA P.V)
+  uint32_t v_mfma_off[kPvMfma ? NVQ : 1];
+  if constexpr (kPvMfma) {
+    static_assert(NVQ == 2 * NJ, "the V ring holds the MFMA P.V loads");
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+        v_mfma_off[r * NH + h] = static_cast<uint32_t>(
+            (tile_token<D>(4 * g + r) * p.slot_stride + 64 * h + 4 * n) * EB);
+  }
+  // Element offset of the wave's tile k, or -1 (hole, or k >= nt).
+  auto tile_base = [&](int k) -> int64_t __attribute__((always_inline)) {
+    const uint32_t lo = static_cast<uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(my_base)), k));
+    const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
+    return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
+  };
+  auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) __attribute__((always_inline)) {
+    const bool ok = base >= 0;
+    const int64_t b0 = ok ? base : 0;
+    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
+    const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
+    KV::template load_k<0, JD>(rk, k_row_off, g, kb);
+    if constexpr (kPvMfma) {
+#pragma unroll
+      for (int q = 0; q < NVQ; ++q) {
+        const uint4 x = buffer_load16<0>(rv, v_mfma_off[q]);
+        if (q % 2 == 0) vb[q / 2].lo = x;
+        else vb[q / 2].hi = x;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) vb[j] = KV::template load<0>(rv, v_lane_off[j]);
+    }
+  };
+
+  // A ring of DEPTH tiles: the loads of DEPTH - 1 tiles are in flight while one is
+  // consumed. The sequence is fully unrolled (a wave owns at most kMaxT tiles) so
+  // every wait for a tile's loads is exact; loads for tiles at or past nt read
+  // nothing (their descriptors have no records).
+  constexpr int DEPTH = D == 64 ? MSATTN_MFMA_DEPTH_D64 : MSATTN_MFMA_DEPTH;
+  raw_t kr[DEPTH][JD], vr[DEPTH][NJ];
+  int64_t br[DEPTH];
+  // The first tiles' loads go out as soon as the context length is known, ahead of the
+  // lanes' row set-up and the query load, which then run under their round trip.
+  if (a1 > a0) {
+    static_for<DEPTH - 1>([&](auto dc) {
+      constexpr int d = decltype(dc)::value;
+      br[d] = tile_base(d);
+      issue(br[d], kr[d], vr[d]);
+    });
+  }
   // This lane's query row n: key range [lo_n, hi_n) and output row.
   int lo_n = 0, hi_n = 0;
   int64_t orow_n = 0;
@@ -830,14 +924,14 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
         a.z *= alpha;
         a.w *= alpha;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          if (mv[u] == -INFINITY) continue;
-          const float wj = __builtin_amdgcn_exp2f(mv[u] - Mn);
-          L = fmaf(wj, lv[u], L);
-          a.x = fmaf(wj, xlo[u].x, a.x);
-          a.y = fmaf(wj, xlo[u].y, a.y);
-          a.z = fmaf(wj, xhi[u].x, a.z);
-          a.w = fmaf(wj, xhi[u].y, a.w);
+        for (int u = 0; u < kBatch; ++u) {  // selects, not branches (see the combine)
+          const bool live = mv[u] != -INFINITY;
+          const float wj = __builtin_amdgcn_exp2f(live ? mv[u] - Mn : 0.0f);
+          L = live ? fmaf(wj, lv[u], L) : L;
+          a.x = live ? fmaf(wj, xlo[u].x, a.x) : a.x;
+          a.y = live ? fmaf(wj, xlo[u].y, a.y) : a.y;
+          a.z = live ? fmaf(wj, xhi[u].x, a.z) : a.z;
+          a.w = live ? fmaf(wj, xhi[u].y, a.w) : a.w;
         }
         M = Mn;
       }
@@ -870,26 +964,10 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
     return;
   }
 
-  // Tiles [t_begin, t_end) of 16 absolute positions hold the keys; the wave's run is
-  // tiles tw0 .. tw0 + nt - 1 of it (earlier ones, below a window, read nothing).
-  const int t_begin = a0 / 16;
-  const int t_end = ceil_div(a1, 16);
-  const int nt = max(0, min(per_wave, t_end - tw0));
-
-  // Lane k holds tile tw0 + k's element offset, or -1 for a hole (a table entry outside
-  // [0, num_blocks), a page past the table, a tile outside the key range).
-  int64_t my_base = -1;
-  if (lane < nt && tw0 + lane >= t_begin && phys_pre >= 0 && phys_pre < p.num_blocks) {
-    const int t = tw0 + lane;
-    const int pg = (t * 16) / p.bs;
-    const int slot0 = t * 16 - pg * p.bs;
-    my_base = static_cast<int64_t>(phys_pre) * p.blk_stride +
-              static_cast<int64_t>(slot0) * p.slot_stride +
-              static_cast<int64_t>(kvh) * p.head_stride;
-  }
-
   // Query rows as the MFMA B operand: lane (g, n) holds Q[row n][dims 8*(4j+g) .. +8].
   typename QChunk<T>::type qb[JD];
+
+  // The query rows (after the first tiles' loads).
   {
     const T* qp = static_cast<const T*>(p.q);
 #pragma unroll
@@ -901,41 +979,6 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
       const int64_t po = static_cast<int64_t>(rope_position(p, b)) * D;
       rope_chunks<T, KT, D>(qb, p.rope_cos + po, p.rope_sin + po, g);
     }
-  }
-
-  // Per-lane byte offsets inside a tile (32-bit: a tile spans 16 slots).
-  constexpr int EB = static_cast<int>(sizeof(KT));
-  const uint32_t k_row_off = static_cast<uint32_t>(tile_token<D>(n) * p.slot_stride * EB);
-  uint32_t v_lane_off[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j)
-    v_lane_off[j] = static_cast<uint32_t>(((TPI * j + va) * p.slot_stride + vc * 8) * EB);
-  const int tile_bytes = static_cast<int>((15 * p.slot_stride + D) * EB);
-
-  const KT* kbase = static_cast<const KT*>(p.k);
-  const KT* vbase = static_cast<const KT*>(p.v);
-
-  // P.V on the matrix core (fp32 query and cache, a full 16-row tile): O = P V as
-  // v_mfma_f32_16x16x4_f32 steps. Step r takes, in lane (g, n), A = P[row n][token
-  // tile_token(4g + r)] (the lane's own weight pr[r], where the scores landed) and
-  // B = V[that token][dim]; lane (g, n) loads 16 bytes of that token's row, dims
-  // 64 h + 4 n .. + 3, and element e of them feeds output block (h, e), whose column n
-  // is dim 64 h + 4 n + e. Output lane (g', n') then holds rows 4 g' .. 4 g' + 3 of dims
-  // 64 h + 4 n' + e: a float4 of consecutive dims per (row, h).
-  constexpr bool kPvMfma = MSATTN_PV_MFMA32 && std::is_same<T, float>::value &&
-                           std::is_same<KT, float>::value && RT == 16;
-  constexpr int NH = D / 64;         // 16-byte V loads per token step
-  constexpr int NVQ = 4 * NH;        // V loads per tile (MFMA P.V)
-  constexpr int NOB = 4 * NH;        // 16x16 output blocks (MFMA P.V)
-  uint32_t v_mfma_off[kPvMfma ? NVQ : 1];
-  if constexpr (kPvMfma) {
-    static_assert(NVQ == 2 * NJ, "the V ring holds the MFMA P.V loads");
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int h = 0; h < NH; ++h)
-        v_mfma_off[r * NH + h] = static_cast<uint32_t>(
-            (tile_token<D>(4 * g + r) * p.slot_stride + 64 * h + 4 * n) * EB);
   }
   // Tiles a wave may own: partitions of the fp32 16-row route reach kPartLongF32 tokens.
   constexpr int kMaxT = kPvMfma ? kPartLongF32 / 16 / kWaves : kMaxTilesPerWave;
@@ -953,32 +996,6 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
   for (int r = 0; r < RTA; ++r)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
-
-  // Element offset of the wave's tile k, or -1 (hole, or k >= nt).
-  auto tile_base = [&](int k) -> int64_t __attribute__((always_inline)) {
-    const uint32_t lo = static_cast<uint32_t>(
-        __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(my_base)), k));
-    const int hi = __builtin_amdgcn_readlane(static_cast<int>(my_base >> 32), k);
-    return static_cast<int64_t>(lo) | (static_cast<int64_t>(hi) << 32);
-  };
-  auto issue = [&](int64_t base, raw_t (&kb)[JD], raw_t (&vb)[NJ]) __attribute__((always_inline)) {
-    const bool ok = base >= 0;
-    const int64_t b0 = ok ? base : 0;
-    const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kbase + b0, ok ? tile_bytes : 0);
-    const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vbase + b0, ok ? tile_bytes : 0);
-    KV::template load_k<0, JD>(rk, k_row_off, g, kb);
-    if constexpr (kPvMfma) {
-#pragma unroll
-      for (int q = 0; q < NVQ; ++q) {
-        const uint4 x = buffer_load16<0>(rv, v_mfma_off[q]);
-        if (q % 2 == 0) vb[q / 2].lo = x;
-        else vb[q / 2].hi = x;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) vb[j] = KV::template load<0>(rv, v_lane_off[j]);
-    }
-  };
 
   auto consume = [&](int k, const raw_t (&kb)[JD], const raw_t (&vb)[NJ], int64_t base) __attribute__((always_inline)) {
     mf_f32x4 s = {0.f, 0.f, 0.f, 0.f};
@@ -1113,18 +1130,6 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
     }
   };
 
-  // A ring of DEPTH tiles: the loads of DEPTH - 1 tiles are in flight while one is
-  // consumed. The sequence is fully unrolled (a wave owns at most kMaxT tiles) so
-  // every wait for a tile's loads is exact; loads for tiles at or past nt read
-  // nothing (their descriptors have no records).
-  constexpr int DEPTH = D == 64 ? MSATTN_MFMA_DEPTH_D64 : MSATTN_MFMA_DEPTH;
-  raw_t kr[DEPTH][JD], vr[DEPTH][NJ];
-  int64_t br[DEPTH];
-  static_for<DEPTH - 1>([&](auto dc) {
-    constexpr int d = decltype(dc)::value;
-    br[d] = tile_base(d);
-    issue(br[d], kr[d], vr[d]);
-  });
   if constexpr (kBalance) {  // the progress words start at zero (every wave reaches here)
     if (tid < kWaves) s_prog[tid] = 0;
     __syncthreads();
@@ -1182,7 +1187,10 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
   }
   __syncthreads();
 
-  // Combine the waves, four dims a thread: rescale each wave to the common max.
+  // Combine the waves, four dims a thread: rescale each wave to the common max. A wave
+  // without keys (m = -inf) takes weight 0 through selects, not branches, so that every
+  // wave's LDS reads go out together (a branch per wave serialises them; C5-decode's
+  // combine took 1.2 us that way).
   for (int idx = tid; idx < nrows * D4; idx += kThreads) {
     const int r = idx / D4;
     const int d = (idx - r * D4) * 4;
@@ -1194,26 +1202,21 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
       M = fmaxf(M, mw[ww]);
     }
     float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (M != -INFINITY) {
+    float L = 0.0f;
 #pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) {
-        if (mw[ww] == -INFINITY) continue;
-        const float f = __builtin_amdgcn_exp2f(mw[ww] - M);
-        const float4 v = *reinterpret_cast<const float4*>(&s_red[ww][r][d]);
-        a.x = fmaf(v.x, f, a.x);
-        a.y = fmaf(v.y, f, a.y);
-        a.z = fmaf(v.z, f, a.z);
-        a.w = fmaf(v.w, f, a.w);
-      }
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const bool live = mw[ww] != -INFINITY;  // then M is finite too
+      const float f = __builtin_amdgcn_exp2f(live ? mw[ww] - M : 0.0f);
+      const float4 v = *reinterpret_cast<const float4*>(&s_red[ww][r][d]);
+      const float lw = s_ml[ww][r][1];
+      a.x = live ? fmaf(v.x, f, a.x) : a.x;
+      a.y = live ? fmaf(v.y, f, a.y) : a.y;
+      a.z = live ? fmaf(v.z, f, a.z) : a.z;
+      a.w = live ? fmaf(v.w, f, a.w) : a.w;
+      L = live ? fmaf(lw, f, L) : L;
     }
     const int64_t orow = out_row(r);
     if (direct) {  // the only partition: normalise and write the output
-      float L = 0.0f;
-      if (M != -INFINITY) {
-#pragma unroll
-        for (int ww = 0; ww < kWaves; ++ww)
-          if (mw[ww] != -INFINITY) L = fmaf(s_ml[ww][r][1], __builtin_amdgcn_exp2f(mw[ww] - M), L);
-      }
       store_out4(orow, d, a, L > 0.0f ? 1.0f / L : 0.0f);
     } else if (fused) {
       float* slot = p.acc + (orow * p.max_parts + part) * D + d;
@@ -1225,16 +1228,20 @@ __global__ __launch_bounds__(W * kWave) void decode_mfma_kernel(const SplitParam
   }
   if (direct) return;
   if (tid < nrows) {
+    float mw[kWaves], lw[kWaves];
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, s_ml[ww][tid][0]);
+    for (int ww = 0; ww < kWaves; ++ww) {
+      mw[ww] = s_ml[ww][tid][0];
+      lw[ww] = s_ml[ww][tid][1];
+      M = fmaxf(M, mw[ww]);
+    }
     float L = 0.0f;
-    if (M != -INFINITY) {
 #pragma unroll
-      for (int ww = 0; ww < kWaves; ++ww) {
-        const float mw = s_ml[ww][tid][0];
-        if (mw != -INFINITY) L = fmaf(s_ml[ww][tid][1], __builtin_amdgcn_exp2f(mw - M), L);
-      }
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const bool live = mw[ww] != -INFINITY;
+      const float f = __builtin_amdgcn_exp2f(live ? mw[ww] - M : 0.0f);
+      L = live ? fmaf(lw[ww], f, L) : L;
     }
     float* ml = p.ml + (orow_n * p.max_parts + part) * 2;
     if (fused) {
