@@ -342,8 +342,8 @@ def main():
     torch.cuda.synchronize()
     # Which partials kernel ran: the workspace header's first word is the layout kind
     # (1 = stream-K); otherwise the partition kernel, on MFMA with head_dim 64 or 128 for a
-    # bf16/fp16 query over its own type, fp8 or fp32 and for an fp32 query over fp32, else
-    # the generic kernel.
+    # bf16/fp16 query over its own type, fp8 or fp32 and for an fp32 query over any cache,
+    # else the generic kernel.
     hdr = ws[:64].view(torch.int32).cpu()
     kind = int(hdr[0])
     # The partition kernels record their launch's partition length and waves per
